@@ -1,0 +1,204 @@
+/*
+ * moe_hip.h — C ABI of libmoe_hip, the MI355X (gfx950) routed-MoE layer.
+ *
+ * The reference (JGalego/Moe, a Rust crate) has no FFI: its boundary is the
+ * internal call
+ *     Model::feed_forward(&self, layer, li, x: &[f32], t, st: &mut State,
+ *                         out: &mut [f32])            src/model.rs:836-841
+ * whose Ffn::Moe arm (src/model.rs:841-971) routes, dispatches, runs the
+ * SwiGLU experts over Q4_0/Q5_0/Q8_0 row ranges and combines.  Every entry
+ * point below names the reference interface it replaces.  Plain C types only:
+ * pointers, sizes and POD structs; no C++ or torch types cross this line.
+ *
+ * Conventions
+ *   - Every function returns 0 on success or a negative MOE_E* code; the
+ *     message of the most recent failure on the calling thread is returned by
+ *     moe_last_error().
+ *   - Device pointers are HIP device addresses on the context's device.
+ *     `stream` is a hipStream_t passed as void* (NULL = the null stream).
+ *   - A forward call is asynchronous on `stream`; concurrent calls on one
+ *     layer must use one stream (the layer's workspace is shared).
+ */
+#ifndef MOE_HIP_H
+#define MOE_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Status codes. */
+#define MOE_OK 0
+#define MOE_EINVAL (-1)   /* bad argument, shape or format */
+#define MOE_ENOMEM (-2)   /* device or host allocation failed */
+#define MOE_EHIP (-3)     /* a HIP runtime call failed */
+#define MOE_EUNSUP (-4)   /* valid for the reference, not supported here */
+
+/* Storage formats, numbered as GGUF numbers them.  Replaces quant::Dt
+ * (src/quant.rs:19-37); Q4_0/Q5_0/Q8_0 are byte-identical to the engine's
+ * Dt::Q4/Q5/Q8 (src/gguf.rs:165-173). */
+#define MOE_DT_F32 0
+#define MOE_DT_F16 1
+#define MOE_DT_Q4_0 2
+#define MOE_DT_Q5_0 6
+#define MOE_DT_Q8_0 8
+#define MOE_DT_BF16 30
+
+/* Gate kinds (Spec::sigmoid, src/spec.rs:305-306). */
+#define MOE_GATE_SOFTMAX 0
+#define MOE_GATE_SIGMOID 1
+
+typedef struct moe_ctx moe_ctx;
+typedef struct moe_layer moe_layer;
+
+/* A 2-D row-major weight view inside an uploaded region.  Replaces quant::QT
+ * (src/quant.rs:97-129) as produced by Store::view (src/store.rs:303-315):
+ * `offset` is the byte offset of the view's first row inside the region,
+ * rows are Dt::row_bytes(cols) apart (src/quant.rs:68-83).  dt < 0 means
+ * "absent" for optional tensors. */
+typedef struct moe_tensor {
+    int32_t dt;
+    int32_t rows;
+    int32_t cols;
+    int32_t _reserved;
+    uint64_t region;
+    uint64_t offset;
+} moe_tensor;
+
+/* One routed layer: the fields of Ffn::Moe (src/model.rs:68-71) plus the
+ * Spec routing scalars it reads (src/spec.rs:199-207). */
+typedef struct moe_layer_desc {
+    int32_t hidden;        /* H */
+    int32_t n_experts;     /* E */
+    int32_t top_k;         /* Spec::top_k */
+    int32_t gate;          /* MOE_GATE_* */
+    int32_t norm_topk;     /* Spec::norm_topk */
+    int32_t n_group;       /* Spec::n_group (1 = no group limit) */
+    int32_t topk_group;    /* Spec::topk_group */
+    float routed_scale;    /* Spec::routed_scale */
+    moe_tensor router;     /* F32 [E, H]   (mlp.gate.weight) */
+    moe_tensor e_bias;     /* F32 [1, E] or dt<0 (mlp.gate.e_score_correction_bias) */
+    const moe_tensor *experts; /* 3*E views: expert e at [3e+0]=gate [I,H], [3e+1]=up [I,H], [3e+2]=down [H,I] */
+    moe_tensor shared[3];  /* gate, up, down of the shared expert, or dt<0 */
+    moe_tensor shared_gate;/* F32 [1, H] or dt<0 (mlp.shared_expert_gate.weight) */
+} moe_layer_desc;
+
+/* Router interventions for one layer.  Replaces model::Routing
+ * (src/model.rs:238-280) as applied at src/model.rs:846-888. */
+typedef struct moe_routing {
+    const int32_t *disabled; /* expert ids this layer may not select (host memory) */
+    int32_t n_disabled;
+    const int32_t *forced;   /* expert ids always selected, in order (host memory) */
+    int32_t n_forced;
+    float temp;              /* divides the logits when > 0 */
+    int32_t top_k;           /* overrides Spec::top_k when > 0 */
+} moe_routing;
+
+/* One routing decision: Route::experts entries (src/model.rs:84-91). */
+typedef struct moe_route {
+    uint32_t expert;
+    float weight;
+} moe_route;
+
+/* ------------------------------------------------------------------ setup */
+
+/* Open a context on HIP device `device`.  Replaces Model::load's ownership of
+ * the Store (src/model.rs:336-341). */
+int moe_ctx_create(int device, moe_ctx **out);
+void moe_ctx_destroy(moe_ctx *ctx);
+
+/* Copy `bytes` of host memory (e.g. an mmap'd checkpoint range) into a new
+ * 256-byte-aligned device region and return its handle.  Replaces
+ * Store::open's mmap (src/store.rs:72-77, 126-136): byte offsets inside the
+ * region are preserved, so views address it exactly as Store::view does. */
+int moe_upload(moe_ctx *ctx, const void *host, uint64_t bytes, uint64_t *region_out);
+
+/* Device address of a region (for callers that fill regions themselves). */
+int moe_region_ptr(moe_ctx *ctx, uint64_t region, void **dev_out);
+
+/* Build a layer over uploaded views.  Replaces the per-layer binding in
+ * Model::load_with (src/model.rs:396-441).  Validates formats, shapes and
+ * that every view lies inside its region (Rec::fits_in, src/store.rs:44-46). */
+int moe_layer_create(moe_ctx *ctx, const moe_layer_desc *desc, moe_layer **out);
+void moe_layer_destroy(moe_layer *layer);
+
+/* Install router interventions (NULL clears them).  Replaces setting
+ * Model::routing for one layer (src/model.rs:238-280). */
+int moe_layer_set_routing(moe_layer *layer, const moe_routing *routing);
+
+/* Pre-size the per-call workspace for up to `max_t` tokens so that later
+ * forward calls with t <= max_t allocate nothing. */
+int moe_layer_reserve(moe_layer *layer, int32_t max_t);
+
+/* Kernel path: 0 = automatic (MFMA grouped GEMM once experts average three or
+ * more tokens, register GEMV below that, exact kernels for shapes neither
+ * fits), 1 = exact kernels (bit-identical to the CPU path, slow), 2 = GEMV,
+ * 3 = MFMA.  No counterpart in the reference, which has one CPU path. */
+int moe_layer_set_mode(moe_layer *layer, int mode);
+
+/* Experts each token is routed to (min(top_k, E)) under the current routing. */
+int moe_layer_k(const moe_layer *layer);
+
+/* ---------------------------------------------------------------- forward */
+
+/* The routed layer over `t` tokens.  Replaces Model::feed_forward's Ffn::Moe
+ * arm (src/model.rs:841-971) and, when `residual` is given, trunk's residual
+ * add that follows it (src/model.rs:680-683).
+ *   x        device f32 [t, H]  layer input (post-norm activations)
+ *   out      device f32 [t, H]  overwritten with the layer output (delta)
+ *   residual device f32 [t, H]  or NULL; if given, residual += out
+ *   routes   device [t, k]      or NULL; routing table strongest first
+ *                               (Route.experts, src/model.rs:943-950)
+ *   hits     device u32 [E+1]   or NULL; hits[0] = n, hits[1..n] = experts
+ *                               with >= 1 token, ascending (State::prev,
+ *                               src/model.rs:951)
+ *   prev     device u32 [E+1]   or NULL; the previous call's `hits`, used for
+ *                               the reuse counter (src/model.rs:913-916)
+ *   stats    device u64 [4]     or NULL; += routed, reused, expert_bytes and
+ *                               tokens with an exact rank tie in the selected
+ *                               prefix (Stats, src/model.rs:116-126)
+ */
+int moe_layer_forward(moe_layer *layer, const float *x, int32_t t, float *out, float *residual, moe_route *routes,
+                      uint32_t *hits, const uint32_t *prev, uint64_t *stats, void *stream);
+
+/* Router logits and gating only: routes [t, k] for x [t, H], as
+ * src/model.rs:844-898 computes them.  `logits` (device f32 [t, E]) may be
+ * NULL; if given it receives the router logits after the temperature. */
+int moe_layer_route(moe_layer *layer, const float *x, int32_t t, moe_route *routes, float *logits, void *stream);
+
+const char *moe_last_error(void);
+
+/* Diagnostics: y[i] = exp(x[i]) computed on the device by the gates' exp (a
+ * port of glibc's expf), for checking it against the host libm.  x and y are
+ * device f32 [n].  No counterpart in the reference. */
+int moe_debug_expf(const float *x, float *y, uint64_t n, void *stream);
+
+/* ------------------------------------------------------- host utilities */
+
+/* Dt::row_bytes (src/quant.rs:68-83); 0 for an unknown format. */
+uint64_t moe_row_bytes(int32_t dt, uint64_t cols);
+
+/* quant::quantize over `rows` rows (src/quant.rs:304-365): F32, F16, Q8_0,
+ * Q4_0, Q5_0.  cols must fit the format (Dt::fits, src/quant.rs:86-92). */
+int moe_quantize_rows(int32_t dt, const float *src, uint64_t rows, uint64_t cols, uint8_t *dst);
+
+/* quant::dequant over `rows` rows (src/quant.rs:177-227). */
+int moe_dequant_rows(int32_t dt, const uint8_t *src, uint64_t rows, uint64_t cols, float *dst);
+
+/* Seeded synthetic data (no counterpart in the reference, which has no normal
+ * generator): element i of stream (seed, stream) is mean + std*z_i, z from
+ * Box-Muller over splitmix64 uniforms, computed in double then rounded to
+ * float.  Multithreaded, deterministic. */
+int moe_synth_normal(uint64_t seed, uint64_t stream, uint64_t n, double mean, double std, float *out);
+
+/* The same values, quantised row by row as quantize would store them, without
+ * materialising the f32 tensor.  dst holds rows * row_bytes(dt, cols). */
+int moe_synth_quantized(uint64_t seed, uint64_t stream, int32_t dt, uint64_t rows, uint64_t cols, double mean,
+                        double std, uint8_t *dst);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* MOE_HIP_H */

@@ -1,0 +1,595 @@
+// moe_abi.hip — the C ABI of libmoe_hip: contexts, uploaded regions, layers
+// and the forward orchestration (router -> gating -> dispatch -> experts ->
+// combine), all asynchronous on the caller's stream.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <memory>
+#include <mutex>
+#include <string>
+#include <vector>
+
+#include "moe_internal.h"
+
+using namespace moe;
+
+namespace {
+
+thread_local std::string g_err;
+
+int fail(int code, const char *fmt, ...) {
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof buf, fmt, ap);
+    va_end(ap);
+    g_err = buf;
+    return code;
+}
+int hip_fail(hipError_t e, const char *what) { return fail(MOE_EHIP, "%s: %s", what, hipGetErrorString(e)); }
+
+struct DeviceGuard {
+    int prev = -1;
+    explicit DeviceGuard(int dev) {
+        hipGetDevice(&prev);
+        if (prev != dev) hipSetDevice(dev);
+    }
+    ~DeviceGuard() {
+        int cur = -1;
+        hipGetDevice(&cur);
+        if (prev >= 0 && cur != prev) hipSetDevice(prev);
+    }
+};
+
+struct Region {
+    void *ptr = nullptr;
+    uint64_t bytes = 0;
+};
+
+// Forward path for a call.
+enum Path { kExact = 1, kGemv = 2, kMfma = 3 };
+
+}  // namespace
+
+struct moe_ctx {
+    int device = 0;
+    std::mutex mu;
+    std::vector<Region> regions;
+};
+
+struct moe_layer {
+    moe_ctx *ctx = nullptr;
+    int H = 0, E = 0, I = 0, I_s = 0;
+    int top_k_spec = 0;
+    int gate = 0, norm_topk = 1, n_group = 1, topk_group = 1;
+    float routed_scale = 1.0f;
+    bool has_shared = false, has_shared_gate = false;
+    bool fast_ok = false, mfma_ok = false;
+    int mode = 0;  // 0 auto, else a Path
+    // routing override
+    float temp = 0.0f;
+    int top_k_override = 0;
+    int n_forced = 0;
+    // device memory owned by the layer
+    float *router = nullptr;             // [E + has_shared_gate, H]
+    const float *e_bias = nullptr;       // points into a region
+    uint8_t *disabled = nullptr;         // [E]
+    int32_t *forced = nullptr;           // [kMaxForced]
+    ExpertDev *experts_dev = nullptr;    // [E + 1]
+    unsigned long long *expert_bytes = nullptr;  // [E]
+    std::vector<ExpertDev> experts_host;
+    bool any_disabled = false;
+    Workspace ws;
+    int ws_k = 0;
+};
+
+namespace {
+
+const Region *region_of(moe_ctx *ctx, uint64_t id) {
+    if (id >= ctx->regions.size() || !ctx->regions[id].ptr) return nullptr;
+    return &ctx->regions[id];
+}
+
+bool dt_ok(int dt) { return dt == MOE_DT_F32 || dt == MOE_DT_Q4_0 || dt == MOE_DT_Q5_0 || dt == MOE_DT_Q8_0; }
+
+// Resolve a view to a device matrix, checking format, shape and bounds
+// (Rec::fits_in, src/store.rs:44-46).
+int resolve(moe_ctx *ctx, const moe_tensor &t, int rows, int cols, const char *what, MatDev &out) {
+    if (!dt_ok(t.dt)) return fail(MOE_EUNSUP, "%s: storage format %d is not supported (F32, Q4_0, Q5_0, Q8_0)", what, t.dt);
+    if (t.rows != rows || t.cols != cols)
+        return fail(MOE_EINVAL, "%s: shape [%d, %d], expected [%d, %d]", what, t.rows, t.cols, rows, cols);
+    if (t.dt != MOE_DT_F32 && cols % kBlk != 0)
+        return fail(MOE_EINVAL, "%s: %d columns is not a whole number of 32-value blocks", what, cols);
+    const Region *r = region_of(ctx, t.region);
+    if (!r) return fail(MOE_EINVAL, "%s: unknown region %llu", what, (unsigned long long)t.region);
+    const uint64_t rb = moe_row_bytes(t.dt, (uint64_t)cols);
+    const uint64_t len = rb * (uint64_t)rows;
+    if (t.offset > r->bytes || len > r->bytes - t.offset)
+        return fail(MOE_EINVAL, "%s: %llu bytes at offset %llu overrun its %llu-byte region", what,
+                    (unsigned long long)len, (unsigned long long)t.offset, (unsigned long long)r->bytes);
+    out.ptr = static_cast<const uint8_t *>(r->ptr) + t.offset;
+    out.stride = (uint32_t)rb;
+    out.dt = t.dt;
+    out.rows = rows;
+    out.cols = cols;
+    return MOE_OK;
+}
+
+bool present(const moe_tensor &t) { return t.dt >= 0; }
+
+// A matrix can take the fast kernels: 4-byte aligned rows of whole 64-value
+// units, at most 256 units wide.
+bool fast_mat(const MatDev &m) {
+    return ((uintptr_t)m.ptr % 4 == 0) && (m.stride % 4 == 0) && (m.cols % 64 == 0) && (m.cols / 64 <= 256);
+}
+
+int effective_k(const moe_layer *L) {
+    int k = L->top_k_override > 0 ? L->top_k_override : L->top_k_spec;
+    return std::min(k, L->E);
+}
+
+size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
+
+void free_ws(Workspace &w) {
+    if (w.base) hipFree(w.base);
+    w = Workspace();
+}
+
+int reserve(moe_layer *L, int max_t, int k) {
+    if (max_t <= L->ws.max_t && k <= L->ws_k) return MOE_OK;
+    max_t = std::max(max_t, L->ws.max_t);
+    k = std::max(k, L->ws_k);
+    const size_t T = (size_t)max_t, E = (size_t)L->E, H = (size_t)L->H;
+    const size_t I = (size_t)std::max(L->I, 1), Is = (size_t)std::max(L->I_s, 1);
+    const size_t max_tiles = T * k / 16 + E + 2 + (T + 15) / 16;
+    struct Item {
+        void **dst;
+        size_t bytes;
+    };
+    Workspace w;
+    w.max_t = max_t;
+    Item items[] = {
+        {(void **)&w.logits, T * (E + 1) * 4},
+        {(void **)&w.sel, T * k * 4},
+        {(void **)&w.wsel, T * k * 4},
+        {(void **)&w.shgate, T * 4},
+        {(void **)&w.counts, (E + 2) * 4},
+        {(void **)&w.offsets, (E + 2) * 4},
+        {(void **)&w.perm_tok, T * k * 4},
+        {(void **)&w.perm_w, T * k * 4},
+        {(void **)&w.pos, T * k * 4},
+        {(void **)&w.hits, (E + 2) * 4},
+        {(void **)&w.tiles, 2 * max_tiles * 4},
+        {(void **)&w.ntiles, 4},
+        {(void **)&w.xh, T * H * 2},
+        {(void **)&w.h, T * k * I * 4},
+        {(void **)&w.hs, T * Is * 4},
+        {(void **)&w.y, T * k * H * 4},
+        {(void **)&w.ys, T * H * 4},
+        {(void **)&w.stats, 4 * 8},
+    };
+    size_t total = 0;
+    for (auto &it : items) total += align_up(it.bytes, 256);
+    void *base = nullptr;
+    hipError_t e = hipMalloc(&base, total);
+    if (e != hipSuccess) return fail(MOE_ENOMEM, "workspace of %zu bytes for %d tokens: %s", total, max_t, hipGetErrorString(e));
+    size_t off = 0;
+    for (auto &it : items) {
+        *it.dst = static_cast<char *>(base) + off;
+        off += align_up(it.bytes, 256);
+    }
+    w.base = base;
+    w.bytes = total;
+    // Old workspace may still be in use by queued work on some stream.
+    hipDeviceSynchronize();
+    free_ws(L->ws);
+    L->ws = w;
+    L->ws_k = k;
+    return MOE_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char *moe_last_error(void) { return g_err.c_str(); }
+
+int moe_debug_expf(const float *x, float *y, uint64_t n, void *stream) {
+    if ((!x || !y) && n) return fail(MOE_EINVAL, "moe_debug_expf: bad argument");
+    hipError_t e = launch_expf(x, y, (size_t)n, (hipStream_t)stream);
+    return e == hipSuccess ? MOE_OK : hip_fail(e, "expf kernel");
+}
+
+int moe_ctx_create(int device, moe_ctx **out) {
+    if (!out) return fail(MOE_EINVAL, "moe_ctx_create: out is NULL");
+    int n = 0;
+    hipError_t e = hipGetDeviceCount(&n);
+    if (e != hipSuccess) return hip_fail(e, "hipGetDeviceCount");
+    if (device < 0 || device >= n) return fail(MOE_EINVAL, "device %d does not exist (%d visible)", device, n);
+    auto *c = new moe_ctx();
+    c->device = device;
+    *out = c;
+    return MOE_OK;
+}
+
+void moe_ctx_destroy(moe_ctx *ctx) {
+    if (!ctx) return;
+    DeviceGuard g(ctx->device);
+    hipDeviceSynchronize();
+    for (auto &r : ctx->regions)
+        if (r.ptr) hipFree(r.ptr);
+    delete ctx;
+}
+
+int moe_upload(moe_ctx *ctx, const void *host, uint64_t bytes, uint64_t *region_out) {
+    if (!ctx || (!host && bytes) || !region_out) return fail(MOE_EINVAL, "moe_upload: bad argument");
+    DeviceGuard g(ctx->device);
+    void *p = nullptr;
+    hipError_t e = hipMalloc(&p, std::max<uint64_t>(align_up(bytes, 256), 256));
+    if (e != hipSuccess) return fail(MOE_ENOMEM, "moe_upload: %llu bytes: %s", (unsigned long long)bytes, hipGetErrorString(e));
+    if (bytes) {
+        e = hipMemcpy(p, host, bytes, hipMemcpyHostToDevice);
+        if (e != hipSuccess) {
+            hipFree(p);
+            return hip_fail(e, "moe_upload: hipMemcpy");
+        }
+    }
+    std::lock_guard<std::mutex> lk(ctx->mu);
+    ctx->regions.push_back(Region{p, bytes});
+    *region_out = ctx->regions.size() - 1;
+    return MOE_OK;
+}
+
+int moe_region_ptr(moe_ctx *ctx, uint64_t region, void **dev_out) {
+    if (!ctx || !dev_out) return fail(MOE_EINVAL, "moe_region_ptr: bad argument");
+    std::lock_guard<std::mutex> lk(ctx->mu);
+    const Region *r = region_of(ctx, region);
+    if (!r) return fail(MOE_EINVAL, "moe_region_ptr: unknown region %llu", (unsigned long long)region);
+    *dev_out = r->ptr;
+    return MOE_OK;
+}
+
+int moe_layer_create(moe_ctx *ctx, const moe_layer_desc *d, moe_layer **out) {
+    if (!ctx || !d || !out) return fail(MOE_EINVAL, "moe_layer_create: bad argument");
+    if (d->hidden <= 0 || d->n_experts <= 0 || d->top_k <= 0)
+        return fail(MOE_EINVAL, "moe_layer_create: hidden %d, experts %d, top_k %d", d->hidden, d->n_experts, d->top_k);
+    if (d->n_experts > kMaxExperts) return fail(MOE_EUNSUP, "%d experts; at most %d are supported", d->n_experts, kMaxExperts);
+    if (std::min(d->top_k, d->n_experts) > kMaxTopK) return fail(MOE_EUNSUP, "top_k %d; at most %d is supported", d->top_k, kMaxTopK);
+    if (d->n_group < 1 || d->topk_group < 0 || d->n_group > 64)
+        return fail(MOE_EINVAL, "n_group %d, topk_group %d", d->n_group, d->topk_group);
+    if (d->gate != MOE_GATE_SOFTMAX && d->gate != MOE_GATE_SIGMOID) return fail(MOE_EINVAL, "gate kind %d", d->gate);
+    if (!d->experts) return fail(MOE_EINVAL, "moe_layer_create: experts is NULL");
+    DeviceGuard g(ctx->device);
+    std::lock_guard<std::mutex> lk(ctx->mu);
+    auto L = std::make_unique<moe_layer>();
+    L->ctx = ctx;
+    L->H = d->hidden;
+    L->E = d->n_experts;
+    L->top_k_spec = d->top_k;
+    L->gate = d->gate;
+    L->norm_topk = d->norm_topk;
+    L->n_group = d->n_group;
+    L->topk_group = d->topk_group;
+    L->routed_scale = d->routed_scale;
+    const int H = L->H, E = L->E;
+
+    MatDev router;
+    int rc = resolve(ctx, d->router, E, H, "router", router);
+    if (rc) return rc;
+    if (router.dt != MOE_DT_F32) return fail(MOE_EUNSUP, "router: only F32 routers are supported");
+    MatDev sg{};
+    L->has_shared_gate = present(d->shared_gate);
+    if (L->has_shared_gate) {
+        if ((rc = resolve(ctx, d->shared_gate, 1, H, "shared_gate", sg))) return rc;
+        if (sg.dt != MOE_DT_F32) return fail(MOE_EUNSUP, "shared_gate: only F32 is supported");
+    }
+    if (present(d->e_bias)) {
+        MatDev b;
+        if ((rc = resolve(ctx, d->e_bias, 1, E, "e_bias", b))) return rc;
+        if (b.dt != MOE_DT_F32) return fail(MOE_EUNSUP, "e_bias: only F32 is supported");
+        if ((uintptr_t)b.ptr % 4) return fail(MOE_EINVAL, "e_bias: not 4-byte aligned");
+        L->e_bias = reinterpret_cast<const float *>(b.ptr);
+    }
+
+    // Experts.
+    L->experts_host.resize(E + 1);
+    int I = -1;
+    for (int e = 0; e < E; e++) {
+        const moe_tensor *t = d->experts + 3 * e;
+        const int inter = t[0].rows;
+        if (inter <= 0) return fail(MOE_EINVAL, "expert %d: %d rows", e, inter);
+        if (I < 0) I = inter;
+        if (inter != I) return fail(MOE_EUNSUP, "expert %d: intermediate %d differs from expert 0's %d", e, inter, I);
+        char what[64];
+        ExpertDev &x = L->experts_host[e];
+        snprintf(what, sizeof what, "expert %d gate", e);
+        if ((rc = resolve(ctx, t[0], inter, H, what, x.m[0]))) return rc;
+        snprintf(what, sizeof what, "expert %d up", e);
+        if ((rc = resolve(ctx, t[1], inter, H, what, x.m[1]))) return rc;
+        snprintf(what, sizeof what, "expert %d down", e);
+        if ((rc = resolve(ctx, t[2], H, inter, what, x.m[2]))) return rc;
+        x.inter = inter;
+    }
+    L->I = I;
+    L->has_shared = present(d->shared[0]);
+    if (L->has_shared) {
+        const int inter = d->shared[0].rows;
+        ExpertDev &x = L->experts_host[E];
+        if ((rc = resolve(ctx, d->shared[0], inter, H, "shared gate_proj", x.m[0]))) return rc;
+        if ((rc = resolve(ctx, d->shared[1], inter, H, "shared up_proj", x.m[1]))) return rc;
+        if ((rc = resolve(ctx, d->shared[2], H, inter, "shared down_proj", x.m[2]))) return rc;
+        x.inter = inter;
+        L->I_s = inter;
+    }
+
+    // Which kernels the shapes allow.
+    const ExpertDev &e0 = L->experts_host[0];
+    bool fast = true;
+    for (int e = 0; e < E; e++)
+        for (int m = 0; m < 3; m++) {
+            const MatDev &a = L->experts_host[e].m[m], &b = e0.m[m];
+            fast &= fast_mat(a) && a.dt == b.dt;
+        }
+    fast &= e0.m[0].dt == e0.m[1].dt;
+    if (L->has_shared) {
+        const ExpertDev &s = L->experts_host[E];
+        for (int m = 0; m < 3; m++) fast &= fast_mat(s.m[m]);
+        fast &= s.m[0].dt == s.m[1].dt;
+    }
+    L->fast_ok = fast;
+    L->mfma_ok = fast && H % 128 == 0 && I % 128 == 0 && (!L->has_shared || L->I_s % 128 == 0);
+
+    // Device-side tables.
+    hipError_t he;
+    const int n_rows = E + (L->has_shared_gate ? 1 : 0);
+    if ((he = hipMalloc(&L->router, (size_t)n_rows * H * 4)) != hipSuccess) return hip_fail(he, "router copy");
+    if ((he = hipMemcpy(L->router, router.ptr, (size_t)E * H * 4, hipMemcpyDeviceToDevice)) != hipSuccess)
+        return hip_fail(he, "router copy");
+    if (L->has_shared_gate &&
+        (he = hipMemcpy(L->router + (size_t)E * H, sg.ptr, (size_t)H * 4, hipMemcpyDeviceToDevice)) != hipSuccess)
+        return hip_fail(he, "shared gate copy");
+    if ((he = hipMalloc(&L->experts_dev, sizeof(ExpertDev) * (E + 1))) != hipSuccess) return hip_fail(he, "expert table");
+    if ((he = hipMemcpy(L->experts_dev, L->experts_host.data(), sizeof(ExpertDev) * (E + 1), hipMemcpyHostToDevice)) !=
+        hipSuccess)
+        return hip_fail(he, "expert table");
+    std::vector<unsigned long long> eb(E);
+    for (int e = 0; e < E; e++) {
+        const ExpertDev &x = L->experts_host[e];
+        for (int m = 0; m < 3; m++) eb[e] += (unsigned long long)moe_row_bytes(x.m[m].dt, x.m[m].cols) * x.m[m].rows;
+    }
+    if ((he = hipMalloc(&L->expert_bytes, 8 * E)) != hipSuccess) return hip_fail(he, "expert bytes");
+    if ((he = hipMemcpy(L->expert_bytes, eb.data(), 8 * E, hipMemcpyHostToDevice)) != hipSuccess)
+        return hip_fail(he, "expert bytes");
+    if ((he = hipMalloc(&L->disabled, E)) != hipSuccess) return hip_fail(he, "routing tables");
+    if ((he = hipMemset(L->disabled, 0, E)) != hipSuccess) return hip_fail(he, "routing tables");
+    if ((he = hipMalloc(&L->forced, 4 * kMaxForced)) != hipSuccess) return hip_fail(he, "routing tables");
+    *out = L.release();
+    return MOE_OK;
+}
+
+void moe_layer_destroy(moe_layer *L) {
+    if (!L) return;
+    DeviceGuard g(L->ctx->device);
+    hipDeviceSynchronize();
+    free_ws(L->ws);
+    hipFree(L->router);
+    hipFree(L->experts_dev);
+    hipFree(L->expert_bytes);
+    hipFree(L->disabled);
+    hipFree(L->forced);
+    delete L;
+}
+
+int moe_layer_set_routing(moe_layer *L, const moe_routing *r) {
+    if (!L) return fail(MOE_EINVAL, "moe_layer_set_routing: layer is NULL");
+    DeviceGuard g(L->ctx->device);
+    std::vector<uint8_t> dis(L->E, 0);
+    std::vector<int32_t> forced;
+    float temp = 0.0f;
+    int top_k = 0;
+    if (r) {
+        if (r->n_disabled < 0 || r->n_forced < 0 || (r->n_disabled && !r->disabled) || (r->n_forced && !r->forced))
+            return fail(MOE_EINVAL, "moe_layer_set_routing: bad lists");
+        for (int i = 0; i < r->n_disabled; i++)
+            if (r->disabled[i] >= 0 && r->disabled[i] < L->E) dis[r->disabled[i]] = 1;
+        for (int i = 0; i < r->n_forced; i++) forced.push_back(r->forced[i]);
+        if ((int)forced.size() > kMaxForced) return fail(MOE_EUNSUP, "at most %d forced experts", kMaxForced);
+        temp = r->temp;
+        top_k = r->top_k;
+        if (top_k < 0) return fail(MOE_EINVAL, "top_k %d", top_k);
+        if (std::min(top_k, L->E) > kMaxTopK) return fail(MOE_EUNSUP, "top_k %d; at most %d is supported", top_k, kMaxTopK);
+    }
+    hipError_t he = hipMemcpy(L->disabled, dis.data(), L->E, hipMemcpyHostToDevice);
+    if (he == hipSuccess && !forced.empty())
+        he = hipMemcpy(L->forced, forced.data(), 4 * forced.size(), hipMemcpyHostToDevice);
+    if (he != hipSuccess) return hip_fail(he, "moe_layer_set_routing");
+    L->any_disabled = std::any_of(dis.begin(), dis.end(), [](uint8_t v) { return v != 0; });
+    L->n_forced = (int)forced.size();
+    L->temp = temp;
+    L->top_k_override = top_k;
+    return MOE_OK;
+}
+
+int moe_layer_set_mode(moe_layer *L, int mode) {
+    if (!L || mode < 0 || mode > kMfma) return fail(MOE_EINVAL, "moe_layer_set_mode: mode %d", mode);
+    if (mode == kGemv && !L->fast_ok) return fail(MOE_EUNSUP, "this layer's shapes do not fit the GEMV kernels");
+    if (mode == kMfma && !L->mfma_ok) return fail(MOE_EUNSUP, "this layer's shapes do not fit the MFMA kernels");
+    L->mode = mode;
+    return MOE_OK;
+}
+
+int moe_layer_reserve(moe_layer *L, int32_t max_t) {
+    if (!L || max_t <= 0) return fail(MOE_EINVAL, "moe_layer_reserve: bad argument");
+    DeviceGuard g(L->ctx->device);
+    return reserve(L, max_t, std::max(effective_k(L), std::min(L->top_k_spec, L->E)));
+}
+
+int moe_layer_k(const moe_layer *L) { return L ? effective_k(L) : 0; }
+
+static GateParams gate_params(const moe_layer *L, int k) {
+    GateParams p{};
+    p.n_experts = L->E;
+    p.top_k = k;
+    p.sigmoid = L->gate == MOE_GATE_SIGMOID;
+    p.norm_topk = L->norm_topk;
+    p.n_group = L->n_group;
+    p.topk_group = L->topk_group;
+    p.routed_scale = L->routed_scale;
+    p.temp = L->temp;
+    p.n_forced = L->n_forced;
+    p.has_shared_gate = L->has_shared_gate;
+    p.e_bias = L->e_bias;
+    p.disabled = L->any_disabled ? L->disabled : nullptr;
+    p.forced = L->forced;
+    return p;
+}
+
+// Router, gating and dispatch; shared by forward and route.
+static int route_and_dispatch(moe_layer *L, const float *x, int t, int k, int bm, moe_route *routes, uint32_t *hits,
+                              const uint32_t *prev, uint64_t *stats, float *logits_out, hipStream_t s) {
+    Workspace &w = L->ws;
+    const int n_rows = L->E + (L->has_shared_gate ? 1 : 0);
+    hipError_t e = launch_router(L->router, x, t, n_rows, L->E, L->H, L->temp, w.logits, s);
+    if (e != hipSuccess) return hip_fail(e, "router kernel");
+    unsigned long long *st = stats ? reinterpret_cast<unsigned long long *>(stats) : w.stats;
+    GateParams p = gate_params(L, k);
+    if ((e = launch_gating(w.logits, n_rows, t, p, w.sel, w.wsel, w.shgate, st, s)) != hipSuccess)
+        return hip_fail(e, "gating kernel");
+    if (logits_out) {
+        if ((e = hipMemcpy2DAsync(logits_out, (size_t)L->E * 4, w.logits, (size_t)n_rows * 4, (size_t)L->E * 4, t,
+                                  hipMemcpyDeviceToDevice, s)) != hipSuccess)
+            return hip_fail(e, "logits copy");
+    }
+    DispatchArgs a{};
+    a.sel = w.sel;
+    a.wsel = w.wsel;
+    a.T = t;
+    a.k = k;
+    a.E = L->E;
+    a.has_shared = L->has_shared;
+    a.bm = bm;
+    a.expert_bytes = L->expert_bytes;
+    a.prev = prev;
+    a.counts = w.counts;
+    a.offsets = w.offsets;
+    a.perm_tok = w.perm_tok;
+    a.pos = w.pos;
+    a.hits = w.hits;
+    a.tiles = w.tiles;
+    a.ntiles = w.ntiles;
+    a.perm_w = w.perm_w;
+    a.routes = routes;
+    a.hits_out = hits;
+    a.stats = st;
+    if ((e = launch_dispatch(a, s)) != hipSuccess) return hip_fail(e, "dispatch kernel");
+    return MOE_OK;
+}
+
+int moe_layer_route(moe_layer *L, const float *x, int32_t t, moe_route *routes, float *logits, void *stream) {
+    if (!L || !x || t <= 0) return fail(MOE_EINVAL, "moe_layer_route: bad argument");
+    DeviceGuard g(L->ctx->device);
+    const int k = effective_k(L);
+    int rc = reserve(L, t, k);
+    if (rc) return rc;
+    return route_and_dispatch(L, x, t, k, 0, routes, nullptr, nullptr, nullptr, logits, (hipStream_t)stream);
+}
+
+int moe_layer_forward(moe_layer *L, const float *x, int32_t t, float *out, float *residual, moe_route *routes,
+                      uint32_t *hits, const uint32_t *prev, uint64_t *stats, void *stream) {
+    if (!L || !x || !out || t <= 0) return fail(MOE_EINVAL, "moe_layer_forward: bad argument (t = %d)", t);
+    DeviceGuard g(L->ctx->device);
+    hipStream_t s = (hipStream_t)stream;
+    const int k = effective_k(L);
+    int rc = reserve(L, t, k);
+    if (rc) return rc;
+    Workspace &w = L->ws;
+
+    // Path: MFMA once experts average a few tokens each, GEMV below that,
+    // the exact kernels when the shapes fit neither (or when asked).
+    Path path = kExact;
+    if (L->mode) {
+        path = (Path)L->mode;
+    } else if (L->fast_ok) {
+        const double avg = (double)t * k / L->E;
+        path = (L->mfma_ok && avg >= 3.0) ? kMfma : kGemv;
+    }
+    int bm = 0;
+    if (path == kMfma) {
+        const double avg = (double)t * k / L->E;
+        bm = avg <= 16.0 ? 16 : (avg <= 32.0 ? 32 : 64);
+    }
+    if ((rc = route_and_dispatch(L, x, t, k, bm, routes, hits, prev, stats, nullptr, s))) return rc;
+
+    const ExpertDev &e0 = L->experts_host[0];
+    const ExpertDev *sh = L->has_shared ? &L->experts_host[L->E] : nullptr;
+    hipError_t e = hipSuccess;
+    if (path == kMfma) {
+        if ((e = launch_to_f16(x, w.xh, (size_t)t * L->H, s)) != hipSuccess) return hip_fail(e, "f16 conversion");
+        MfmaArgs m{};
+        m.experts = L->experts_dev;
+        m.tiles = w.tiles;
+        m.ntiles = w.ntiles;
+        m.counts = w.counts;
+        m.offsets = w.offsets;
+        m.perm_tok = w.perm_tok;
+        m.xh = w.xh;
+        m.h = reinterpret_cast<uint16_t *>(w.h);
+        m.hs = reinterpret_cast<uint16_t *>(w.hs);
+        m.y = w.y;
+        m.ys = w.ys;
+        m.T = t;
+        m.H = L->H;
+        m.I = L->I;
+        m.I_s = L->I_s;
+        m.E = L->E;
+        m.max_tiles = t * k / bm + std::min(L->E, t * k) + 1;
+        if ((e = launch_mfma(true, m, bm, e0, sh, s)) != hipSuccess) return hip_fail(e, "MFMA up kernel");
+        if ((e = launch_mfma(false, m, bm, e0, sh, s)) != hipSuccess) return hip_fail(e, "MFMA down kernel");
+    } else {
+        GemvArgs a{};
+        a.experts = L->experts_dev;
+        a.hits = w.hits;
+        a.counts = w.counts;
+        a.offsets = w.offsets;
+        a.perm_tok = w.perm_tok;
+        a.x = x;
+        a.h = w.h;
+        a.hs = w.hs;
+        a.y = w.y;
+        a.ys = w.ys;
+        a.T = t;
+        a.H = L->H;
+        a.I = L->I;
+        a.I_s = L->I_s;
+        a.E = L->E;
+        a.task_bound = std::min(L->E, t * k);
+        a.has_shared = L->has_shared;
+        if (path == kGemv) {
+            if ((e = launch_gemv_up(a, e0, sh, s)) != hipSuccess) return hip_fail(e, "GEMV up kernel");
+            if ((e = launch_gemv_down(a, e0, sh, s)) != hipSuccess) return hip_fail(e, "GEMV down kernel");
+        } else {
+            if ((e = launch_gemv_exact(true, a, s)) != hipSuccess) return hip_fail(e, "exact up kernel");
+            if ((e = launch_gemv_exact(false, a, s)) != hipSuccess) return hip_fail(e, "exact down kernel");
+        }
+    }
+    CombineArgs c{};
+    c.y = w.y;
+    c.ys = w.ys;
+    c.pos = w.pos;
+    c.sel = w.sel;
+    c.wsel = w.wsel;
+    c.shgate = L->has_shared_gate ? w.shgate : nullptr;
+    c.out = out;
+    c.residual = residual;
+    c.T = t;
+    c.H = L->H;
+    c.k = k;
+    c.has_shared = L->has_shared;
+    if ((e = launch_combine(c, s)) != hipSuccess) return hip_fail(e, "combine kernel");
+    return MOE_OK;
+}
+
+}  // extern "C"

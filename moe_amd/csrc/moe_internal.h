@@ -1,0 +1,167 @@
+// moe_internal.h — types shared by the gfx950 kernels and the C ABI layer.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/moe_hip.h"
+
+namespace moe {
+
+constexpr int kBlk = 32;          // values per quantisation block
+constexpr int kMaxExperts = 512;  // routed experts per layer the kernels support
+constexpr int kMaxTopK = 64;      // experts per token the kernels support
+constexpr int kMaxForced = 64;    // forced experts per layer
+
+// Bytes of one 32-value block in format `dt` (F32 counts 32 floats).
+__host__ __device__ inline int block_bytes(int dt) {
+    switch (dt) {
+    case MOE_DT_F32: return 128;
+    case MOE_DT_Q8_0: return 34;
+    case MOE_DT_Q4_0: return 18;
+    case MOE_DT_Q5_0: return 22;
+    default: return 0;
+    }
+}
+
+// One weight matrix as the kernels see it: rows `stride` bytes apart.
+struct MatDev {
+    const uint8_t *ptr;
+    uint32_t stride;  // bytes between rows (>= row bytes, multiple of 4)
+    int32_t dt;
+    int32_t rows;
+    int32_t cols;
+};
+
+// A SwiGLU expert: gate [I,H], up [I,H], down [H,I].  Routed experts occupy
+// entries 0..E-1 of the layer's table; the shared expert, if any, entry E.
+struct ExpertDev {
+    MatDev m[3];
+    int32_t inter;
+    int32_t _pad;
+};
+
+// Routing parameters the gating kernel needs.
+struct GateParams {
+    int32_t n_experts;
+    int32_t top_k;          // effective k (after the routing override)
+    int32_t sigmoid;
+    int32_t norm_topk;
+    int32_t n_group;
+    int32_t topk_group;
+    float routed_scale;
+    float temp;             // > 0: logits /= temp
+    int32_t n_forced;
+    int32_t has_shared_gate;
+    const float *e_bias;        // [E] or null
+    const uint8_t *disabled;    // [E] 0/1 or null
+    const int32_t *forced;      // [n_forced]
+};
+
+// Per-call scratch, sized for max_t tokens (see moe_layer_reserve).
+struct Workspace {
+    int32_t max_t = 0;
+    float *logits = nullptr;      // [T, E+1]
+    int32_t *sel = nullptr;       // [T, k]
+    float *wsel = nullptr;        // [T, k]
+    float *shgate = nullptr;      // [T] sigmoid of the shared-expert gate
+    int32_t *counts = nullptr;    // [E+1]
+    int32_t *offsets = nullptr;   // [E+2]
+    int32_t *perm_tok = nullptr;  // [T*k] token of each permuted row
+    float *perm_w = nullptr;      // [T*k]
+    int32_t *pos = nullptr;       // [T*k] permuted row of (t, slot)
+    int32_t *hits = nullptr;      // [E+2] n, then experts ascending
+    int32_t *tiles = nullptr;     // [2 * max_tiles] (group, m0) pairs for the MFMA path
+    int32_t *ntiles = nullptr;    // [1]
+    uint16_t *xh = nullptr;       // [T, H] f16 activations (MFMA path)
+    float *h = nullptr;           // [T*k, I] routed SwiGLU activations (f32, or f16 on the MFMA path)
+    float *hs = nullptr;          // [T, I_s] shared-expert activations
+    float *y = nullptr;           // [T*k, H] routed expert outputs
+    float *ys = nullptr;          // [T, H] shared-expert outputs
+    unsigned long long *stats = nullptr;  // [4] fallback when the caller passes none
+    void *base = nullptr;         // single allocation backing all of the above
+    size_t bytes = 0;
+};
+
+// --------------------------------------------------------------- launchers
+// Each returns hipSuccess or the launch error.
+
+// Router logits, bit-exact to the reference's dot (src/quant.rs:386-420):
+// logits[t][e] = W[e] . x[t] for e < n_rows, divided by temp (e < E only)
+// when temp > 0.  Row E (if n_rows == E+1) is the shared-expert gate.
+hipError_t launch_router(const float *W, const float *x, int T, int n_rows, int E, int H, float temp, float *logits,
+                         hipStream_t s);
+
+// Gating + top-k + weights per token (src/model.rs:855-897).
+hipError_t launch_gating(const float *logits, int ld, int T, const GateParams &p, int32_t *sel, float *wsel,
+                         float *shgate, unsigned long long *stats, hipStream_t s);
+
+// Stable token->expert dispatch (src/model.rs:900-930) plus the work lists.
+struct DispatchArgs {
+    const int32_t *sel;
+    const float *wsel;
+    int T, k, E;
+    int has_shared;
+    int bm;                       // MFMA M-tile (0: no tile list)
+    const unsigned long long *expert_bytes;  // [E]
+    const uint32_t *prev;         // [E+1] or null
+    int32_t *counts, *offsets, *perm_tok, *pos, *hits, *tiles, *ntiles;
+    float *perm_w;
+    moe_route *routes;            // [T, k] or null
+    uint32_t *hits_out;           // [E+1] or null
+    unsigned long long *stats;    // [4]
+};
+hipError_t launch_dispatch(const DispatchArgs &a, hipStream_t s);
+
+// y = the gates' exp (glibc expf port) over n values; diagnostics.
+hipError_t launch_expf(const float *x, float *y, size_t n, hipStream_t s);
+
+// f32 -> f16 conversion of the activations (MFMA path).
+hipError_t launch_to_f16(const float *x, uint16_t *xh, size_t n, hipStream_t s);
+
+// Decode-path expert GEMVs (fp32, weights dequantised exactly in registers).
+struct GemvArgs {
+    const ExpertDev *experts;     // device table [E+1]
+    const int32_t *hits;          // [E+2]
+    const int32_t *counts, *offsets, *perm_tok;
+    const float *x;               // [T, H]
+    float *h, *hs;                // routed [T*k, I], shared [T, I_s]
+    float *y, *ys;                // routed [T*k, H], shared [T, H]
+    int T, H, I, I_s, E;
+    int task_bound;               // routed tasks launched (>= hits[0])
+    int has_shared;
+};
+hipError_t launch_gemv_up(const GemvArgs &a, const ExpertDev &host_e0, const ExpertDev *host_shared, hipStream_t s);
+hipError_t launch_gemv_down(const GemvArgs &a, const ExpertDev &host_e0, const ExpertDev *host_shared, hipStream_t s);
+
+// Exact-order expert GEMVs (bit-identical to the reference's dot).
+hipError_t launch_gemv_exact(bool up, const GemvArgs &a, hipStream_t s);
+
+// Prefill-path grouped GEMMs on MFMA (f16 operands, f32 accumulation).
+struct MfmaArgs {
+    const ExpertDev *experts;
+    const int32_t *tiles, *ntiles;
+    const int32_t *counts, *offsets, *perm_tok;
+    const uint16_t *xh;           // [T, H] f16
+    uint16_t *h, *hs;             // f16 [T*k, I], [T, I_s]
+    float *y, *ys;                // f32 [T*k, H], [T, H]
+    int T, H, I, I_s, E;
+    int max_tiles;
+};
+// up: gate/up + SwiGLU; down: down projection.  Routed tiles come from the
+// dispatch list; the shared expert (sh != null) gets its own launch.
+hipError_t launch_mfma(bool up, const MfmaArgs &a, int bm, const ExpertDev &e0, const ExpertDev *sh, hipStream_t s);
+
+// Weighted combine in ascending expert order + shared expert + residual
+// (src/model.rs:936-942, 956-970, 680-683).
+struct CombineArgs {
+    const float *y, *ys;
+    const int32_t *pos;
+    const int32_t *sel;
+    const float *wsel;
+    const float *shgate;          // [T] or null
+    float *out, *residual;
+    int T, H, k, has_shared;
+};
+hipError_t launch_combine(const CombineArgs &a, hipStream_t s);
+
+}  // namespace moe

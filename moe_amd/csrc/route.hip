@@ -1,0 +1,601 @@
+// route.hip — router logits, gating and token->expert dispatch for gfx950.
+//
+// Everything here is bit-exact to the reference's CPU path, because expert
+// selection must be: the logits follow dot_avx2's lane and reduction order
+// (src/quant.rs:386-420), the gates use a port of glibc's expf, and every
+// sum the reference folds sequentially is folded sequentially here too.
+// This file is compiled with -ffp-contract=off so that no multiply and add
+// are fused except where fmaf() says so.
+#include <hip/hip_fp16.h>
+#include <hip/hip_runtime.h>
+
+#include "exact_math.h"
+#include "moe_internal.h"
+
+namespace moe {
+namespace {
+
+constexpr int kSmallRouterTokens = 4;
+
+// Rust f32::total_cmp as a signed integer key.
+__device__ inline int32_t tkey(float v) {
+    int32_t b = __float_as_int(v);
+    return b ^ (int32_t)(((uint32_t)(b >> 31)) >> 1);
+}
+
+// Rust f32::max: NaN loses to a number.
+__device__ inline float fmax_rs(float a, float b) { return (a != a) ? b : ((b != b) ? a : (a > b ? a : b)); }
+
+// Reduce the 16 per-lane chains of one dot product in dot_avx2's order:
+// s[j] = acc0[j] + acc1[j]; q[j] = s[j+4] + s[j]; (q0+q1) + (q2+q3).
+// `acc` is lane j's chain (j = lane & 15); the result is valid in j == 0.
+__device__ inline float reduce16_avx2(float acc) {
+    float s = acc + __shfl_down(acc, 8, 16);
+    float q = __shfl_down(s, 4, 16) + s;
+    float a = q + __shfl_down(q, 1, 16);   // lane 0: q0+q1, lane 2: q2+q3
+    return a + __shfl_down(a, 2, 16);      // lane 0: (q0+q1)+(q2+q3)
+}
+
+// Scalar tail of dot_avx2 (elements past the last full 8): out += a*b.
+__device__ inline float dot_tail(float out, const float *a, const float *b, int from, int n) {
+    for (int i = from; i < n; i++) {
+        float p = a[i] * b[i];
+        out += p;
+    }
+    return out;
+}
+
+// Small-T router: one block stages `eb` router rows and all T (<= 4) token
+// rows in LDS, then thread (row, j) runs lane j's FMA chain for every token.
+__global__ __launch_bounds__(256) void router_small_kernel(const float *__restrict__ W, const float *__restrict__ x,
+                                                           int T, int n_rows, int E, int H, int eb, float temp,
+                                                           float *__restrict__ logits) {
+    extern __shared__ float lds[];
+    float *wl = lds;
+    float *xl = lds + (size_t)eb * H;
+    const int r0 = blockIdx.x * eb;
+    const int nr = min(eb, n_rows - r0);
+    const int tid = threadIdx.x;
+    if ((H & 3) == 0) {
+        const float4 *w4 = reinterpret_cast<const float4 *>(W + (size_t)r0 * H);
+        float4 *wl4 = reinterpret_cast<float4 *>(wl);
+        for (int i = tid; i < nr * H / 4; i += 256) wl4[i] = w4[i];
+        const float4 *x4 = reinterpret_cast<const float4 *>(x);
+        float4 *xl4 = reinterpret_cast<float4 *>(xl);
+        for (int i = tid; i < T * H / 4; i += 256) xl4[i] = x4[i];
+    } else {
+        for (int i = tid; i < nr * H; i += 256) wl[i] = W[(size_t)r0 * H + i];
+        for (int i = tid; i < T * H; i += 256) xl[i] = x[i];
+    }
+    __syncthreads();
+    const int j = tid & 15, rl = tid >> 4;
+    if (rl >= nr) return;  // whole 16-lane groups leave together
+    const float *a = wl + (size_t)rl * H;
+    const int n16 = H / 16;
+    const bool has8 = (H % 16) >= 8;
+    float acc[kSmallRouterTokens];
+#pragma unroll
+    for (int t = 0; t < kSmallRouterTokens; t++) acc[t] = 0.0f;
+    for (int c = 0; c < n16; c++) {
+        float av = a[16 * c + j];
+#pragma unroll
+        for (int t = 0; t < kSmallRouterTokens; t++)
+            if (t < T) acc[t] = fmaf(av, xl[(size_t)t * H + 16 * c + j], acc[t]);
+    }
+    if (has8 && j < 8) {
+#pragma unroll
+        for (int t = 0; t < kSmallRouterTokens; t++)
+            if (t < T) acc[t] = fmaf(a[16 * n16 + j], xl[(size_t)t * H + 16 * n16 + j], acc[t]);
+    }
+    const int tail = 16 * n16 + (has8 ? 8 : 0);
+    const int r = r0 + rl;
+#pragma unroll
+    for (int t = 0; t < kSmallRouterTokens; t++) {
+        if (t >= T) break;
+        float v = reduce16_avx2(acc[t]);
+        if (j == 0) {
+            v = dot_tail(v, a, xl + (size_t)t * H, tail, H);
+            if (temp > 0.0f && r < E) v = v / temp;
+            logits[(size_t)t * n_rows + r] = v;
+        }
+    }
+}
+
+// Tiled router for larger T: a 32-row x 32-token tile per block, K staged
+// through LDS 64 values at a time.  Thread (j, g) owns lane j of the chains
+// of 8 rows x 8 tokens.  Chunks past the last full 16 are zero-padded, and
+// fma(0, 0, acc) == acc for every acc a chain can hold (chains start at +0
+// and never reach -0), so padding does not change a single bit.
+constexpr int kRT = 32;   // rows per tile
+constexpr int kTT = 32;   // tokens per tile
+constexpr int kKC = 64;   // K chunk
+__global__ __launch_bounds__(256) void router_tiled_kernel(const float *__restrict__ W, const float *__restrict__ x,
+                                                           int T, int n_rows, int E, int H, float temp,
+                                                           float *__restrict__ logits) {
+    __shared__ float wt[kRT][kKC + 4];
+    __shared__ float xt[kTT][kKC + 4];
+    const int tid = threadIdx.x, j = tid & 15, g = tid >> 4;
+    const int rg = g & 3, tg = g >> 2;
+    const int r0 = blockIdx.x * kRT, t0 = blockIdx.y * kTT;
+    const int n16 = H / 16;
+    const int kfull = n16 * 16;  // elements covered by full 16-chunks
+    float acc[8][8];
+#pragma unroll
+    for (int i = 0; i < 8; i++)
+#pragma unroll
+        for (int u = 0; u < 8; u++) acc[i][u] = 0.0f;
+    for (int k0 = 0; k0 < kfull; k0 += kKC) {
+        // 32 x 64 floats per operand: 2048 values, 8 per thread.
+        for (int q = tid; q < kRT * kKC; q += 256) {
+            int rr = q / kKC, kk = q % kKC;
+            int gk = k0 + kk;
+            int gr = r0 + rr, gt = t0 + rr;
+            wt[rr][kk] = (gr < n_rows && gk < kfull) ? W[(size_t)gr * H + gk] : 0.0f;
+            xt[rr][kk] = (gt < T && gk < kfull) ? x[(size_t)gt * H + gk] : 0.0f;
+        }
+        __syncthreads();
+#pragma unroll
+        for (int s = 0; s < kKC / 16; s++) {
+            float wv[8], xv[8];
+#pragma unroll
+            for (int i = 0; i < 8; i++) wv[i] = wt[rg * 8 + i][16 * s + j];
+#pragma unroll
+            for (int u = 0; u < 8; u++) xv[u] = xt[tg * 8 + u][16 * s + j];
+#pragma unroll
+            for (int i = 0; i < 8; i++)
+#pragma unroll
+                for (int u = 0; u < 8; u++) acc[i][u] = fmaf(wv[i], xv[u], acc[i][u]);
+        }
+        __syncthreads();
+    }
+    const bool has8 = (H % 16) >= 8;
+    const int tail = kfull + (has8 ? 8 : 0);
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+        const int r = r0 + rg * 8 + i;
+#pragma unroll
+        for (int u = 0; u < 8; u++) {
+            const int t = t0 + tg * 8 + u;
+            float a = acc[i][u];
+            const bool valid = r < n_rows && t < T;
+            if (has8 && j < 8 && valid) a = fmaf(W[(size_t)r * H + kfull + j], x[(size_t)t * H + kfull + j], a);
+            float v = reduce16_avx2(a);
+            if (j == 0 && valid) {
+                v = dot_tail(v, W + (size_t)r * H, x + (size_t)t * H, tail, H);
+                if (temp > 0.0f && r < E) v = v / temp;
+                logits[(size_t)t * n_rows + r] = v;
+            }
+        }
+    }
+}
+
+// ------------------------------------------------------------------ gating
+
+// Wave-wide argmax of a packed (key << 32 | ~index) value.
+__device__ inline long long wave_max64(long long v) {
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) {
+        long long o = __shfl_xor(v, m, 64);
+        v = o > v ? o : v;
+    }
+    return v;
+}
+__device__ inline float wave_max_rs(float v) {
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) v = fmax_rs(v, __shfl_xor(v, m, 64));
+    return v;
+}
+__device__ inline long long pack_key(int32_t key, int e) {
+    const unsigned long long hi = (unsigned long long)(uint32_t)key << 32;
+    return (long long)(hi | (0xffffffffu - (uint32_t)e));
+}
+constexpr long long kTaken = (long long)0x8000000000000000ull;
+
+// One wavefront per token, experts e = lane*EPL + i.  Restates
+// src/model.rs:855-897: gate, rank = score + bias, prune_groups, disabled,
+// stable descending sort truncated to k (ties: lower index first), forced
+// experts, weights = max(score, 0), renormalise, scale.
+template <int EPL>
+__global__ __launch_bounds__(256) void gating_kernel(const float *__restrict__ logits, int ld, int T, GateParams p,
+                                                     int32_t *__restrict__ sel, float *__restrict__ wsel,
+                                                     float *__restrict__ shgate,
+                                                     unsigned long long *__restrict__ stats) {
+    __shared__ float s_sc[4][EPL * 64];
+    __shared__ float s_rank[4][EPL * 64];
+    __shared__ float s_gs[4][64];
+    __shared__ int s_idx[4][kMaxTopK];
+    __shared__ float s_bcast[4];
+    const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int t = blockIdx.x * 4 + w;
+    const bool active = t < T;
+    const int E = p.n_experts;
+    const float *lg = logits + (size_t)(active ? t : 0) * ld;
+
+    float sc[EPL], rank[EPL];
+#pragma unroll
+    for (int i = 0; i < EPL; i++) {
+        const int e = lane * EPL + i;
+        sc[i] = e < E ? lg[e] : 0.0f;
+    }
+    if (p.sigmoid) {
+#pragma unroll
+        for (int i = 0; i < EPL; i++) {
+            float nv = -sc[i];
+            float den = 1.0f + expf_exact(nv);
+            sc[i] = 1.0f / den;
+        }
+    } else {
+        float m = -INFINITY;
+#pragma unroll
+        for (int i = 0; i < EPL; i++)
+            if (lane * EPL + i < E) m = fmax_rs(m, sc[i]);
+        m = wave_max_rs(m);
+#pragma unroll
+        for (int i = 0; i < EPL; i++) {
+            sc[i] = expf_exact(sc[i] - m);
+            if (lane * EPL + i < E) s_sc[w][lane * EPL + i] = sc[i];
+        }
+        __syncthreads();
+        if (lane == 0) {
+            float s = 0.0f;
+            for (int e = 0; e < E; e++) s += s_sc[w][e];
+            s_bcast[w] = s;
+        }
+        __syncthreads();
+        const float s = s_bcast[w];
+#pragma unroll
+        for (int i = 0; i < EPL; i++) sc[i] = sc[i] / s;
+    }
+#pragma unroll
+    for (int i = 0; i < EPL; i++) {
+        const int e = lane * EPL + i;
+        rank[i] = (p.e_bias && e < E) ? sc[i] + p.e_bias[e] : sc[i];
+    }
+    if (p.n_group > 1 && p.topk_group < p.n_group) {
+#pragma unroll
+        for (int i = 0; i < EPL; i++)
+            if (lane * EPL + i < E) s_rank[w][lane * EPL + i] = rank[i];
+        __syncthreads();
+        const int per = E / p.n_group;
+        if (lane < p.n_group) {
+            int32_t k1 = INT32_MIN, k2 = INT32_MIN;
+            float v1 = 0.0f, v2 = 0.0f;
+            for (int i = 0; i < per; i++) {
+                float v = s_rank[w][lane * per + i];
+                int32_t k = tkey(v);
+                if (k > k1) {
+                    k2 = k1, v2 = v1;
+                    k1 = k, v1 = v;
+                } else if (k > k2) {
+                    k2 = k, v2 = v;
+                }
+            }
+            float gsum = -0.0f;
+            if (per >= 1) gsum = gsum + v1;
+            if (per >= 2) gsum = gsum + v2;
+            s_gs[w][lane] = gsum;
+        }
+        __syncthreads();
+#pragma unroll
+        for (int i = 0; i < EPL; i++) {
+            const int e = lane * EPL + i;
+            const int g = per > 0 ? e / per : p.n_group;
+            if (e < E && g < p.n_group) {
+                const int32_t kg = tkey(s_gs[w][g]);
+                int position = 0;
+                for (int g2 = 0; g2 < p.n_group; g2++) {
+                    const int32_t k2 = tkey(s_gs[w][g2]);
+                    position += (k2 > kg) || (k2 == kg && g2 < g);
+                }
+                if (position >= p.topk_group) rank[i] = -INFINITY;
+            }
+        }
+    }
+    if (p.disabled) {
+#pragma unroll
+        for (int i = 0; i < EPL; i++) {
+            const int e = lane * EPL + i;
+            if (e < E && p.disabled[e]) rank[i] = -INFINITY;
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < EPL; i++) {
+        const int e = lane * EPL + i;
+        if (e < E) {
+            s_sc[w][e] = sc[i];
+            s_rank[w][e] = rank[i];
+        }
+    }
+    // Selection: k+1 rounds of (key desc, index asc) argmax.  The extra round
+    // finds the best unselected rank for the tie check.
+    const int k = p.top_k;
+    long long cand[EPL];
+#pragma unroll
+    for (int i = 0; i < EPL; i++) {
+        const int e = lane * EPL + i;
+        cand[i] = e < E ? pack_key(tkey(rank[i]), e) : kTaken;
+    }
+    int tie = 0;
+    int32_t prev_key = 0;
+    const int rounds = k < E ? k + 1 : k;
+    for (int r = 0; r < rounds; r++) {
+        long long best = kTaken;
+#pragma unroll
+        for (int i = 0; i < EPL; i++) best = cand[i] > best ? cand[i] : best;
+        best = wave_max64(best);
+        const int e = (int)(0xffffffffu - (uint32_t)(best & 0xffffffffll));
+        const int32_t key = (int32_t)(best >> 32);
+        if (r > 0 && key == prev_key) tie = 1;
+        prev_key = key;
+        if (r < k) {
+            if (lane == 0) s_idx[w][r] = e;
+#pragma unroll
+            for (int i = 0; i < EPL; i++)
+                if (lane * EPL + i == e) cand[i] = kTaken;
+        }
+    }
+    __syncthreads();
+    if (active && lane == 0) {
+        int *idx = s_idx[w];
+        const float *rk = s_rank[w];
+        for (int f = 0; f < p.n_forced; f++) {
+            const int e = p.forced[f];
+            if (e < 0 || e >= E) continue;
+            bool present = false;
+            for (int j = 0; j < k; j++) present |= idx[j] == e;
+            if (present) continue;
+            idx[k - 1] = e;
+            // Stable insertion sort of the k picks by descending rank.
+            for (int a = 1; a < k; a++) {
+                const int v = idx[a];
+                const int32_t kv = tkey(rk[v]);
+                int b = a;
+                while (b > 0 && kv > tkey(rk[idx[b - 1]])) {
+                    idx[b] = idx[b - 1];
+                    b--;
+                }
+                idx[b] = v;
+            }
+        }
+        float wv[kMaxTopK];
+        float z = -0.0f;
+        for (int j = 0; j < k; j++) {
+            wv[j] = fmax_rs(s_sc[w][idx[j]], 0.0f);
+            z += wv[j];
+        }
+        if (p.norm_topk) {
+            z = fmax_rs(z, 1e-20f);
+            for (int j = 0; j < k; j++) wv[j] = wv[j] / z;
+        }
+        for (int j = 0; j < k; j++) {
+            wv[j] = wv[j] * p.routed_scale;
+            sel[(size_t)t * k + j] = idx[j];
+            wsel[(size_t)t * k + j] = wv[j];
+        }
+        if (p.has_shared_gate) {
+            float nv = -lg[E];
+            float den = 1.0f + expf_exact(nv);
+            shgate[t] = 1.0f / den;
+        }
+        if (tie && stats) atomicAdd(stats + 3, 1ull);
+    }
+}
+
+// ---------------------------------------------------------------- dispatch
+
+constexpr int kDispatchThreads = 512;
+constexpr int kDispatchWaves = kDispatchThreads / 64;
+
+// Exclusive scan of one int per thread across the block; returns the
+// exclusive prefix and writes the block total to *total.
+__device__ inline int block_scan_excl(int v, int *wave_sums, int *total) {
+    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+    int incl = v;
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+        int o = __shfl_up(incl, d, 64);
+        if (lane >= d) incl += o;
+    }
+    if (lane == 63) wave_sums[wv] = incl;
+    __syncthreads();
+    int before = 0, all = 0;
+    for (int i = 0; i < kDispatchWaves; i++) {
+        before += i < wv ? wave_sums[i] : 0;
+        all += wave_sums[i];
+    }
+    __syncthreads();
+    *total = all;
+    return before + incl - v;
+}
+
+// One block: histogram, scan, stats, hit list, tile list and the stable
+// per-expert token order (src/model.rs:902-924).  Positions come from
+// per-wave 64-bit ballots, so tokens keep ascending order within an expert
+// without relying on atomic ordering.
+__global__ __launch_bounds__(kDispatchThreads) void dispatch_kernel(DispatchArgs a) {
+    __shared__ int cnt[kMaxExperts];
+    __shared__ int off[kMaxExperts];
+    __shared__ int run[kMaxExperts];
+    __shared__ unsigned long long bm[kDispatchWaves][kMaxExperts];
+    __shared__ int wb[kDispatchWaves][kMaxExperts];
+    __shared__ int wave_sums[kDispatchWaves];
+    __shared__ unsigned long long s_reused, s_bytes;
+    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    const int E = a.E, T = a.T, k = a.k;
+    const int n = T * k;
+    for (int e = tid; e < E; e += kDispatchThreads) {
+        cnt[e] = 0;
+        run[e] = 0;
+    }
+    if (tid == 0) s_reused = 0, s_bytes = 0;
+    __syncthreads();
+    for (int i = tid; i < n; i += kDispatchThreads) {
+        const int e = a.sel[i];
+        if (e >= 0 && e < E) atomicAdd(&cnt[e], 1);
+    }
+    __syncthreads();
+
+    // Offsets, hit list and tile list: one expert per thread (E <= 512).
+    const int e = tid;
+    const int c = e < E ? cnt[e] : 0;
+    int total;
+    const int o = block_scan_excl(c, wave_sums, &total);
+    if (e < E) {
+        off[e] = o;
+        a.counts[e] = c;
+        a.offsets[e] = o;
+    }
+    if (tid == 0) {
+        a.offsets[E] = total;
+        a.offsets[E + 1] = total + (a.has_shared ? T : 0);
+        a.counts[E] = a.has_shared ? T : 0;
+    }
+    int nh;
+    const int hp = block_scan_excl(c > 0 ? 1 : 0, wave_sums, &nh);
+    if (c > 0) {
+        a.hits[1 + hp] = e;
+        if (a.hits_out) a.hits_out[1 + hp] = (uint32_t)e;
+        atomicAdd(&s_bytes, a.expert_bytes[e]);
+        if (a.prev) {
+            const uint32_t np = a.prev[0];
+            bool in_prev = false;
+            for (uint32_t j = 0; j < np; j++) in_prev |= a.prev[1 + j] == (uint32_t)e;
+            if (in_prev) atomicAdd(&s_reused, (unsigned long long)c);
+        }
+    }
+    if (tid == 0) {
+        a.hits[0] = nh;
+        if (a.hits_out) a.hits_out[0] = (uint32_t)nh;
+    }
+    if (a.bm > 0) {
+        const int nt = (c + a.bm - 1) / a.bm;
+        int tt;
+        const int tb = block_scan_excl(nt, wave_sums, &tt);
+        for (int i = 0; i < nt; i++) {
+            a.tiles[2 * (tb + i)] = e;
+            a.tiles[2 * (tb + i) + 1] = i * a.bm;
+        }
+        if (tid == 0) {
+            int ntot = tt;
+            if (a.has_shared) {
+                const int ns = (T + a.bm - 1) / a.bm;
+                for (int i = 0; i < ns; i++) {
+                    a.tiles[2 * (tt + i)] = E;
+                    a.tiles[2 * (tt + i) + 1] = i * a.bm;
+                }
+                ntot += ns;
+            }
+            a.ntiles[0] = ntot;
+        }
+    }
+    __syncthreads();
+    if (tid == 0) {
+        a.stats[0] += (unsigned long long)n;
+        a.stats[1] += s_reused;
+        a.stats[2] += s_bytes;
+    }
+
+    // Stable positions, kDispatchThreads tokens per pass.
+    for (int t0 = 0; t0 < T; t0 += kDispatchThreads) {
+        const int t = t0 + tid;
+        for (int x = lane; x < E; x += 64) bm[wv][x] = 0ull;
+        __syncthreads();
+        if (t < T)
+            for (int s = 0; s < k; s++) atomicOr(&bm[wv][a.sel[(size_t)t * k + s]], 1ull << lane);
+        __syncthreads();
+        for (int x = tid; x < E; x += kDispatchThreads) {
+            int r = run[x];
+            for (int w2 = 0; w2 < kDispatchWaves; w2++) {
+                wb[w2][x] = r;
+                r += __popcll(bm[w2][x]);
+            }
+            run[x] = r;
+        }
+        __syncthreads();
+        if (t < T) {
+            const unsigned long long below = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
+            for (int s = 0; s < k; s++) {
+                const int ex = a.sel[(size_t)t * k + s];
+                const float wt = a.wsel[(size_t)t * k + s];
+                const int pp = off[ex] + wb[wv][ex] + __popcll(bm[wv][ex] & below);
+                a.perm_tok[pp] = t;
+                a.perm_w[pp] = wt;
+                a.pos[(size_t)t * k + s] = pp;
+                if (a.routes) {
+                    a.routes[(size_t)t * k + s].expert = (uint32_t)ex;
+                    a.routes[(size_t)t * k + s].weight = wt;
+                }
+            }
+        }
+        __syncthreads();
+    }
+}
+
+__global__ void expf_kernel(const float *__restrict__ x, float *__restrict__ y, size_t n) {
+    size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    size_t stride = (size_t)gridDim.x * blockDim.x;
+    for (; i < n; i += stride) y[i] = expf_exact(x[i]);
+}
+
+__global__ void to_f16_kernel(const float *__restrict__ x, __half *__restrict__ xh, size_t n) {
+    size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    size_t stride = (size_t)gridDim.x * blockDim.x;
+    for (; i < n; i += stride) xh[i] = __float2half_rn(x[i]);
+}
+
+}  // namespace
+
+hipError_t launch_router(const float *W, const float *x, int T, int n_rows, int E, int H, float temp, float *logits,
+                         hipStream_t s) {
+    const size_t row_bytes = (size_t)H * 4;
+    const size_t budget = 64 * 1024;
+    if (T <= kSmallRouterTokens && (size_t)(1 + T) * row_bytes <= budget) {
+        int eb = (int)(budget / row_bytes) - T;
+        eb = eb < 1 ? 1 : (eb > 16 ? 16 : eb);
+        const int blocks = (n_rows + eb - 1) / eb;
+        const size_t lds = (size_t)(eb + T) * row_bytes;
+        hipLaunchKernelGGL(router_small_kernel, dim3(blocks), dim3(256), lds, s, W, x, T, n_rows, E, H, eb, temp,
+                           logits);
+    } else {
+        dim3 grid((n_rows + kRT - 1) / kRT, (T + kTT - 1) / kTT);
+        hipLaunchKernelGGL(router_tiled_kernel, grid, dim3(256), 0, s, W, x, T, n_rows, E, H, temp, logits);
+    }
+    return hipGetLastError();
+}
+
+hipError_t launch_gating(const float *logits, int ld, int T, const GateParams &p, int32_t *sel, float *wsel,
+                         float *shgate, unsigned long long *stats, hipStream_t s) {
+    dim3 grid((T + 3) / 4);
+    if (p.n_experts <= 64)
+        hipLaunchKernelGGL(gating_kernel<1>, grid, dim3(256), 0, s, logits, ld, T, p, sel, wsel, shgate, stats);
+    else if (p.n_experts <= 128)
+        hipLaunchKernelGGL(gating_kernel<2>, grid, dim3(256), 0, s, logits, ld, T, p, sel, wsel, shgate, stats);
+    else if (p.n_experts <= 256)
+        hipLaunchKernelGGL(gating_kernel<4>, grid, dim3(256), 0, s, logits, ld, T, p, sel, wsel, shgate, stats);
+    else
+        hipLaunchKernelGGL(gating_kernel<8>, grid, dim3(256), 0, s, logits, ld, T, p, sel, wsel, shgate, stats);
+    return hipGetLastError();
+}
+
+hipError_t launch_dispatch(const DispatchArgs &a, hipStream_t s) {
+    hipLaunchKernelGGL(dispatch_kernel, dim3(1), dim3(kDispatchThreads), 0, s, a);
+    return hipGetLastError();
+}
+
+hipError_t launch_expf(const float *x, float *y, size_t n, hipStream_t s) {
+    size_t blocks = (n + 255) / 256;
+    if (blocks > 8192) blocks = 8192;
+    if (blocks < 1) blocks = 1;
+    hipLaunchKernelGGL(expf_kernel, dim3((unsigned)blocks), dim3(256), 0, s, x, y, n);
+    return hipGetLastError();
+}
+
+hipError_t launch_to_f16(const float *x, uint16_t *xh, size_t n, hipStream_t s) {
+    size_t blocks = (n + 255) / 256;
+    if (blocks > 4096) blocks = 4096;
+    if (blocks < 1) blocks = 1;
+    hipLaunchKernelGGL(to_f16_kernel, dim3((unsigned)blocks), dim3(256), 0, s, x, reinterpret_cast<__half *>(xh), n);
+    return hipGetLastError();
+}
+
+}  // namespace moe

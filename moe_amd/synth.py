@@ -1,0 +1,194 @@
+"""Seeded synthetic MoE layers at the benchmark shapes.
+
+A layer is laid out as one byte region the way a packed checkpoint lays out
+its tensors: the router, the optional correction bias, the experts as three
+stacked tensors (``experts.gate`` / ``experts.up`` as [E, I, H] and
+``experts.down`` as [E, H, I], GGUF's ``ffn_*_exps`` layout), and the
+optional shared expert and its gate.  Every tensor starts on a 256-byte
+boundary, and an expert is a row range inside its stack (src/store.rs:303-315,
+src/model.rs:396-421).  Values are N(mean, std) from the library's seeded
+generator and are quantised with the reference's quantiser.
+"""
+from __future__ import annotations
+
+import ctypes as C
+from dataclasses import dataclass, replace
+from typing import Optional
+
+import numpy as np
+
+from . import _lib as L
+from .layer import MoeSpec, Rec, Store, View, row_bytes
+
+# Generator streams of a layer's tensors.
+STREAM_ROUTER, STREAM_EBIAS, STREAM_SHGATE = 1, 2, 3
+STREAM_SHARED = (4, 5, 6)
+STREAM_ACTS = 0xA000
+
+
+def stream_expert(e: int, which: int) -> int:
+    return 16 + 3 * e + which
+
+
+@dataclass(frozen=True)
+class Shape:
+    """A routed layer's shape and routing rule."""
+
+    name: str
+    hidden: int
+    inter: int
+    n_experts: int
+    top_k: int
+    expert_dt: int
+    sigmoid: bool = False
+    norm_topk: bool = True
+    routed_scale: float = 1.0
+    n_group: int = 1
+    topk_group: int = 1
+    shared_inter: int = 0
+    shared_dt: Optional[int] = None
+    e_bias_std: float = 0.0
+    shared_gate: bool = False
+    weight_std: float = 0.02
+    router_std: float = 0.02
+
+    def spec(self) -> MoeSpec:
+        return MoeSpec(hidden=self.hidden, n_experts=self.n_experts, top_k=self.top_k, sigmoid=self.sigmoid,
+                       norm_topk=self.norm_topk, routed_scale=self.routed_scale, n_group=self.n_group,
+                       topk_group=self.topk_group)
+
+    def expert_bytes(self) -> int:
+        return 2 * self.inter * row_bytes(self.expert_dt, self.hidden) + self.hidden * row_bytes(self.expert_dt,
+                                                                                                  self.inter)
+
+    def shared_bytes(self) -> int:
+        if not self.shared_inter:
+            return 0
+        dt = self.shared_dt if self.shared_dt is not None else self.expert_dt
+        return 2 * self.shared_inter * row_bytes(dt, self.hidden) + self.hidden * row_bytes(dt, self.shared_inter)
+
+
+SHAPES = {
+    # Mixtral-8x7B layer, Q4_0, softmax top-2, renormalised.
+    "mixtral": Shape("mixtral", 4096, 14336, 8, 2, L.DT_Q4_0),
+    # Qwen3-30B-A3B layer, Q8_0, softmax top-8, renormalised.
+    "qwen3": Shape("qwen3", 2048, 768, 128, 8, L.DT_Q8_0),
+    # DeepSeek-V3 layer: sigmoid + bias N(0, 0.1), 8 groups keep 4,
+    # top-8, scale 2.5, Q4_0 routed experts, one Q5_0 shared expert.
+    "deepseek_v3": Shape("deepseek_v3", 7168, 2048, 256, 8, L.DT_Q4_0, sigmoid=True, routed_scale=2.5,
+                         n_group=8, topk_group=4, shared_inter=2048, shared_dt=L.DT_Q5_0, e_bias_std=0.1),
+    # DeepSeek-V2-Lite MoE layer: 64 experts top-6 plus two shared
+    # experts loaded as one 2816-wide MLP (src/model.rs:431-439), Q8_0.  The
+    # model's own config sets norm_topk_prob false, which the reference reads.
+    "v2_lite": Shape("v2_lite", 2048, 1408, 64, 6, L.DT_Q8_0, norm_topk=False, shared_inter=2816,
+                     shared_dt=L.DT_Q8_0),
+    # configs[0]'s MoE layer: tiny Mixtral, hidden 512, 8 experts top-2, Q8_0.
+    "tiny_mixtral": Shape("tiny_mixtral", 512, 1408, 8, 2, L.DT_Q8_0),
+}
+
+
+def scaled(shape: Shape, **kw) -> Shape:
+    """The same routing rule at other sizes (for quick parity cases)."""
+    return replace(shape, **kw)
+
+
+def _align(v: int, a: int = 256) -> int:
+    return (v + a - 1) // a * a
+
+
+@dataclass
+class HostLayer:
+    """A layer's bytes in host memory plus its tensor index."""
+
+    shape: Shape
+    buf: np.ndarray          # uint8
+    index: dict              # name -> Rec
+
+    def tensor(self, name: str) -> np.ndarray:
+        r = self.index[name]
+        return self.buf[r.offset:r.offset + r.nbytes]
+
+
+def _fill(dst: np.ndarray, seed: int, stream: int, dt: int, rows: int, cols: int, mean: float, std: float) -> None:
+    rc = L.lib().moe_synth_quantized(seed, stream, dt, rows, cols, mean, std, dst.ctypes.data_as(C.c_void_p))
+    L.check(rc, "moe_synth_quantized")
+
+
+def build_host_layer(shape: Shape, seed: int) -> HostLayer:
+    """Generate and quantise every tensor of a layer into one byte buffer."""
+    E, H, I = shape.n_experts, shape.hidden, shape.inter
+    plan = [("router", L.DT_F32, 1, E, H)]
+    if shape.e_bias_std > 0:
+        plan.append(("e_bias", L.DT_F32, 1, 1, E))
+    plan += [("experts.gate", shape.expert_dt, E, I, H), ("experts.up", shape.expert_dt, E, I, H),
+             ("experts.down", shape.expert_dt, E, H, I)]
+    if shape.shared_inter:
+        sdt = shape.shared_dt if shape.shared_dt is not None else shape.expert_dt
+        Is = shape.shared_inter
+        plan += [("shared.gate", sdt, 1, Is, H), ("shared.up", sdt, 1, Is, H), ("shared.down", sdt, 1, H, Is)]
+    if shape.shared_gate:
+        plan.append(("shared_gate", L.DT_F32, 1, 1, H))
+    index, off = {}, 0
+    for name, dt, slabs, rows, cols in plan:
+        rec = Rec(dt, slabs, rows, cols, off)
+        index[name] = rec
+        off = _align(off + rec.nbytes)
+    buf = np.zeros(max(off, 256), dtype=np.uint8)
+    for name, dt, slabs, rows, cols in plan:
+        r = index[name]
+        dst = buf[r.offset:r.offset + r.nbytes]
+        if name == "router":
+            _fill(dst, seed, STREAM_ROUTER, dt, rows, cols, 0.0, shape.router_std)
+        elif name == "e_bias":
+            _fill(dst, seed, STREAM_EBIAS, dt, rows, cols, 0.0, shape.e_bias_std)
+        elif name == "shared_gate":
+            _fill(dst, seed, STREAM_SHGATE, dt, rows, cols, 0.0, shape.router_std)
+        elif name.startswith("experts."):
+            which = ("experts.gate", "experts.up", "experts.down").index(name)
+            rb = row_bytes(dt, cols) * rows
+            for e in range(slabs):
+                _fill(dst[e * rb:(e + 1) * rb], seed, stream_expert(e, which), dt, rows, cols, 0.0,
+                      shape.weight_std)
+        else:
+            which = ("shared.gate", "shared.up", "shared.down").index(name)
+            _fill(dst, seed, STREAM_SHARED[which], dt, rows, cols, 0.0, shape.weight_std)
+    return HostLayer(shape, buf, index)
+
+
+def activations(seed: int, t: int, hidden: int) -> np.ndarray:
+    """x [t, hidden] ~ N(0, 1), f32 (stream depends on t, so every T is its own input)."""
+    out = np.empty((t, hidden), dtype=np.float32)
+    L.check(L.lib().moe_synth_normal(seed, STREAM_ACTS + t, out.size, 0.0, 1.0, out.ctypes.data_as(C.c_void_p)),
+            "moe_synth_normal")
+    return out
+
+
+def normal(seed: int, stream: int, n: int, mean: float = 0.0, std: float = 1.0) -> np.ndarray:
+    out = np.empty(n, dtype=np.float32)
+    L.check(L.lib().moe_synth_normal(seed, stream, n, mean, std, out.ctypes.data_as(C.c_void_p)), "moe_synth_normal")
+    return out
+
+
+def layer_views(store: Store, shape: Shape):
+    """(router, e_bias, experts[(gate, up, down)], shared, shared_gate) views,
+    each expert a row range of its stack (src/model.rs:396-421)."""
+    E, I, H = shape.n_experts, shape.inter, shape.hidden
+    experts = [(store.view("experts.gate", e, 0, I), store.view("experts.up", e, 0, I),
+                store.view("experts.down", e, 0, H)) for e in range(E)]
+    shared = None
+    if shape.shared_inter:
+        shared = (store.get("shared.gate"), store.get("shared.up"), store.get("shared.down"))
+    return (store.get("router"), store.get("e_bias"), experts, shared, store.get("shared_gate"))
+
+
+def make_layer(ctx, host: HostLayer, layer_index: int = 0):
+    """Upload a host layer and bind a MoeLayer over it."""
+    from .layer import MoeLayer
+
+    region = ctx.upload(host.buf)
+    store = Store(region, host.index)
+    router, e_bias, experts, shared, shared_gate = layer_views(store, host.shape)
+    layer = MoeLayer(ctx, host.shape.spec(), router, experts, e_bias=e_bias, shared=shared,
+                     shared_gate=shared_gate, layer_index=layer_index)
+    layer._region = region  # keep the region alive with the layer
+    return layer

@@ -1,0 +1,233 @@
+#!/usr/bin/env python3
+"""Routed-MoE-layer throughput on one MI355X.
+
+    python bench.py [--steps K] [--warmup W] [--tokens 512] [--decode-tokens 1]
+
+A step is one pass of the Mixtral-8x7B-shape routed layer (hidden 4096, 8
+SwiGLU experts of 14336, Q4_0, softmax top-2 renormalised) over one batch of
+synthetic tokens already resident in HBM.  The headline `value` is tokens/s
+at T=512 (prefill); the same line carries the T=1 decode figures under
+`decode`.  Weights are uploaded as several distinct copies (like consecutive
+layers of a model) and the steps cycle through them, so decode steps read
+their experts from HBM rather than from the 256 MB last-level cache.
+
+`roofline` is for the dominant kernel of the step (the expert gate/up
+kernel): algorithmic flops (prefill) or bytes (decode) per launch divided by
+its average duration, timed with HIP events recorded around it on its stream
+inside the library.  `cpu_baseline` times the CPU restatement of the
+reference's MoE path (oracle/, OpenMP over the host's cores) on a bounded
+sample of the same workload.
+"""
+from __future__ import annotations
+
+import argparse
+import ctypes as C
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+METRIC = "MoE-layer tokens/s at T=1 and T=512; % of HBM (decode) / MFMA (prefill) peak"
+HBM_PEAK_GBS = 8000.0
+MFMA_F16_PEAK_TFLOPS = 2500.0
+
+
+def log(msg: str) -> None:
+    print(f"# {msg}", file=sys.stderr, flush=True)
+
+
+def expert_flops(shape, t: int, k: int, up_only: bool = False) -> float:
+    """2*T*k*(2*H*I) for gate+up; + 2*T*k*H*I for down; plus the shared expert."""
+    H, I = shape.hidden, shape.inter
+    mats = 2 if up_only else 3
+    f = 2.0 * t * k * mats * H * I
+    if shape.shared_inter:
+        f += 2.0 * t * mats * H * shape.shared_inter
+    return f
+
+
+def time_steps(layers, x, out, steps: int, warmup: int):
+    import torch
+
+    for i in range(warmup):
+        layers[i % len(layers)].feed_forward(x, out)
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for i in range(steps):
+        layers[i % len(layers)].feed_forward(x, out)
+    end.record()
+    torch.cuda.synchronize()
+    return start.elapsed_time(end) / steps
+
+
+def stage_times(layers, x, out, steps: int):
+    """Average milliseconds per launch of each stage, from HIP events the
+    library records around every stage on the forward's stream."""
+    import torch
+
+    from moe_amd import _lib as L
+
+    for layer in layers:
+        L.check(L.lib().moe_layer_profile(layer.handle, 1))
+    for i in range(steps):
+        layers[i % len(layers)].feed_forward(x, out)
+    torch.cuda.synchronize()
+    ms = (C.c_double * 6)()
+    n = (C.c_uint64 * 6)()
+    for layer in layers:
+        L.check(L.lib().moe_layer_stage_times(layer.handle, ms, n))
+        L.check(L.lib().moe_layer_profile(layer.handle, 0))
+    return {L.STAGES[i]: (ms[i] / n[i] if n[i] else 0.0) for i in range(6)}
+
+
+def selected_bytes(layer, host, x) -> tuple[int, int]:
+    """(gate+up bytes, down bytes) of the distinct experts this input selects."""
+    import torch
+
+    from moe_amd.layer import State
+
+    st = State(1)
+    out = torch.empty_like(x)
+    layer.feed_forward(x, out, state=st)
+    hits = st.previous(0)
+    s = host.shape
+    from moe_amd.layer import row_bytes
+
+    up = len(hits) * 2 * s.inter * row_bytes(s.expert_dt, s.hidden)
+    down = len(hits) * s.hidden * row_bytes(s.expert_dt, s.inter)
+    return up, down
+
+
+def cpu_baseline(host, t_decode: int, t_prefill: int, seconds: float):
+    """The CPU restatement of the reference path on this host's cores."""
+    sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
+    from moe_amd import synth
+    from oracle import pyoracle
+
+    pyoracle.build()
+    ol = pyoracle.from_host_layer(host)
+    cores = int(pyoracle.lib().orc_max_threads())
+    xd = synth.activations(1, t_decode, host.shape.hidden)
+    ol.forward(xd)  # warm: pages in the weights
+    n, t0 = 0, time.perf_counter()
+    while time.perf_counter() - t0 < seconds * 0.5:
+        ol.forward(xd)
+        n += 1
+    dec = n * t_decode / (time.perf_counter() - t0)
+    xp = synth.activations(1, t_prefill, host.shape.hidden)
+    n, t0 = 0, time.perf_counter()
+    while n < 1 or time.perf_counter() - t0 < seconds * 0.5:
+        ol.forward(xp)
+        n += 1
+    pre = n * t_prefill / (time.perf_counter() - t0)
+    return dec, pre, cores, n
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--shape", default="mixtral")
+    ap.add_argument("--tokens", type=int, default=512)
+    ap.add_argument("--decode-tokens", type=int, default=1)
+    ap.add_argument("--copies", type=int, default=4, help="distinct weight copies cycled through")
+    ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    ap.add_argument("--no-cpu", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU: this build has no multi-GPU path (every GPU box here has one GPU); "
+              "run with --gpus 1", file=sys.stderr)
+        return 2
+
+    import torch
+
+    from moe_amd import synth
+    from moe_amd.layer import Context
+
+    shape = synth.SHAPES[args.shape]
+    log(f"generating {shape.name} layer (seed 1)")
+    t0 = time.time()
+    host = synth.build_host_layer(shape, 1)
+    log(f"generated {host.buf.nbytes / 1e6:.0f} MB in {time.time() - t0:.1f}s; uploading {args.copies} copies")
+    ctx = Context(0)
+    layers = [synth.make_layer(ctx, host, layer_index=0) for _ in range(args.copies)]
+    dev = torch.device("cuda:0")
+    k = layers[0].k
+
+    results = {}
+    for t in (args.decode_tokens, args.tokens):
+        for layer in layers:
+            layer.reserve(t)
+        x = torch.from_numpy(synth.activations(1, t, shape.hidden)).to(dev)
+        out = torch.empty_like(x)
+        ms = time_steps(layers, x, out, args.steps, args.warmup)
+        stages = stage_times(layers, x, out, args.steps)
+        up_bytes, down_bytes = selected_bytes(layers[0], host, x)
+        results[t] = dict(ms=ms, stages=stages, up_bytes=up_bytes, down_bytes=down_bytes)
+        log(f"T={t}: {ms:.4f} ms/step, {t / ms * 1e3:.0f} tok/s; stages " +
+            ", ".join(f"{k_}={v * 1e3:.1f}us" for k_, v in stages.items()))
+
+    # Prefill (headline): MFMA-bound gate/up kernel.
+    tp = results[args.tokens]
+    up_ms = tp["stages"]["expert_up"]
+    up_flops = expert_flops(shape, args.tokens, k, up_only=True)
+    achieved = up_flops / (up_ms * 1e-3) / 1e12
+    layer_tflops = expert_flops(shape, args.tokens, k) / (tp["ms"] * 1e-3) / 1e12
+    # Decode: HBM-bound gate/up kernel.
+    td = results[args.decode_tokens]
+    dec_up_ms = td["stages"]["expert_up"]
+    dec_bytes = td["up_bytes"] + args.decode_tokens * shape.hidden * 4 + args.decode_tokens * k * shape.inter * 4
+    dec_gbs = dec_bytes / (dec_up_ms * 1e-3) / 1e9
+    layer_bytes = td["up_bytes"] + td["down_bytes"] + shape.n_experts * shape.hidden * 4 + \
+        2 * args.decode_tokens * shape.hidden * 4
+    layer_gbs = layer_bytes / (td["ms"] * 1e-3) / 1e9
+
+    cpu = None
+    if not args.no_cpu:
+        log("timing the CPU restatement (oracle/) on the host cores")
+        dec, pre, cores, n = cpu_baseline(host, args.decode_tokens, args.tokens, args.cpu_seconds)
+        cpu = dict(value=round(pre, 2), unit="tokens/s", cores=cores, kind="port",
+                   sample=f"{n} forward(s) of the same layer at T={args.tokens} plus repeated T={args.decode_tokens}"
+                          f" decode for ~{args.cpu_seconds / 2:.0f}s each, same weights and inputs",
+                   decode_value=round(dec, 2))
+
+    line = {
+        "metric": METRIC,
+        "value": round(args.tokens / (tp["ms"] * 1e-3), 1),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(tp["ms"], 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f16",
+        "data": "synthetic",
+        "config": {"workload": f"{shape.name}_moe_layer_T{args.tokens}", "hidden": shape.hidden,
+                   "inter": shape.inter, "experts": shape.n_experts, "top_k": shape.top_k,
+                   "weights": "Q4_0" if shape.expert_dt == 2 else str(shape.expert_dt), "tokens": args.tokens,
+                   "weight_copies": args.copies},
+        "roofline": {"bound": "mfma", "kernel": "expert gate/up (MFMA grouped GEMM)",
+                     "achieved": round(achieved, 2), "peak": MFMA_F16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                     "frac": round(achieved / MFMA_F16_PEAK_TFLOPS, 4), "traffic": None,
+                     "layer_frac": round(layer_tflops / MFMA_F16_PEAK_TFLOPS, 4)},
+        "cpu_baseline": cpu,
+        "decode": {"tokens": args.decode_tokens, "value": round(args.decode_tokens / (td["ms"] * 1e-3), 1),
+                   "unit": "tokens/s", "ms_per_step": round(td["ms"], 5), "dtype": "f32",
+                   "roofline": {"bound": "hbm", "kernel": "expert gate/up (GEMV)", "achieved": round(dec_gbs, 1),
+                                "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(dec_gbs / HBM_PEAK_GBS, 4),
+                                "traffic": None, "layer_frac": round(layer_gbs / HBM_PEAK_GBS, 4)},
+                   "stages_us": {k_: round(v * 1e3, 2) for k_, v in td["stages"].items()}},
+        "stages_us": {k_: round(v * 1e3, 2) for k_, v in tp["stages"].items()},
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

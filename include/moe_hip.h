@@ -168,6 +168,16 @@ int moe_layer_forward(moe_layer *layer, const float *x, int32_t t, float *out, f
  * NULL; if given it receives the router logits after the temperature. */
 int moe_layer_route(moe_layer *layer, const float *x, int32_t t, moe_route *routes, float *logits, void *stream);
 
+/* Stage timing (no counterpart in the reference).  While enabled, forward
+ * records HIP events around each of its stages on the call's stream:
+ * 0 router, 1 gating, 2 dispatch, 3 expert gate/up, 4 expert down,
+ * 5 combine.  moe_layer_stage_times synchronises on the last event and adds
+ * each stage's accumulated milliseconds and launch count into ms[6], n[6],
+ * then resets the accumulators. */
+#define MOE_STAGES 6
+int moe_layer_profile(moe_layer *layer, int enable);
+int moe_layer_stage_times(moe_layer *layer, double *ms, uint64_t *n);
+
 const char *moe_last_error(void);
 
 /* Diagnostics: y[i] = exp(x[i]) computed on the device by the gates' exp (a

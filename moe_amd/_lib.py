@@ -75,7 +75,11 @@ PROTOTYPES = {
     "moe_synth_quantized": (C.c_int, [C.c_uint64, C.c_uint64, C.c_int32, C.c_uint64, C.c_uint64, C.c_double,
                                       C.c_double, C.c_void_p]),
     "moe_debug_expf": (C.c_int, [C.c_void_p, C.c_void_p, C.c_uint64, C.c_void_p]),
+    "moe_layer_profile": (C.c_int, [C.c_void_p, C.c_int]),
+    "moe_layer_stage_times": (C.c_int, [C.c_void_p, C.POINTER(C.c_double), C.POINTER(C.c_uint64)]),
 }
+
+STAGES = ("router", "gating", "dispatch", "expert_up", "expert_down", "combine")
 
 _lib = None
 

@@ -84,7 +84,45 @@ struct moe_layer {
     bool any_disabled = false;
     Workspace ws;
     int ws_k = 0;
+    // stage timing
+    bool profile = false;
+    struct StageRec {
+        int stage;
+        hipEvent_t a, b;
+    };
+    std::vector<hipEvent_t> event_pool;
+    std::vector<StageRec> pending;
+    double stage_ms[MOE_STAGES] = {};
+    uint64_t stage_n[MOE_STAGES] = {};
 };
+
+namespace {
+
+hipEvent_t take_event(moe_layer *L) {
+    if (!L->event_pool.empty()) {
+        hipEvent_t e = L->event_pool.back();
+        L->event_pool.pop_back();
+        return e;
+    }
+    hipEvent_t e = nullptr;
+    hipEventCreate(&e);
+    return e;
+}
+
+// Runs `fn` (which launches one stage's kernels on `s`) between two events
+// when profiling is on.
+template <class F>
+int stage(moe_layer *L, int id, hipStream_t s, F fn) {
+    if (!L->profile) return fn();
+    hipEvent_t a = take_event(L), b = take_event(L);
+    hipEventRecord(a, s);
+    const int rc = fn();
+    hipEventRecord(b, s);
+    L->pending.push_back({id, a, b});
+    return rc;
+}
+
+}  // namespace
 
 namespace {
 
@@ -380,6 +418,8 @@ void moe_layer_destroy(moe_layer *L) {
     hipFree(L->expert_bytes);
     hipFree(L->disabled);
     hipFree(L->forced);
+    for (auto &r : L->pending) L->event_pool.push_back(r.a), L->event_pool.push_back(r.b);
+    for (hipEvent_t ev : L->event_pool) hipEventDestroy(ev);
     delete L;
 }
 
@@ -452,12 +492,19 @@ static int route_and_dispatch(moe_layer *L, const float *x, int t, int k, int bm
                               const uint32_t *prev, uint64_t *stats, float *logits_out, hipStream_t s) {
     Workspace &w = L->ws;
     const int n_rows = L->E + (L->has_shared_gate ? 1 : 0);
-    hipError_t e = launch_router(L->router, x, t, n_rows, L->E, L->H, L->temp, w.logits, s);
-    if (e != hipSuccess) return hip_fail(e, "router kernel");
+    hipError_t e = hipSuccess;
+    int rc = stage(L, 0, s, [&] {
+        e = launch_router(L->router, x, t, n_rows, L->E, L->H, L->temp, w.logits, s);
+        return e == hipSuccess ? MOE_OK : hip_fail(e, "router kernel");
+    });
+    if (rc) return rc;
     unsigned long long *st = stats ? reinterpret_cast<unsigned long long *>(stats) : w.stats;
     GateParams p = gate_params(L, k);
-    if ((e = launch_gating(w.logits, n_rows, t, p, w.sel, w.wsel, w.shgate, st, s)) != hipSuccess)
-        return hip_fail(e, "gating kernel");
+    rc = stage(L, 1, s, [&] {
+        e = launch_gating(w.logits, n_rows, t, p, w.sel, w.wsel, w.shgate, st, s);
+        return e == hipSuccess ? MOE_OK : hip_fail(e, "gating kernel");
+    });
+    if (rc) return rc;
     if (logits_out) {
         if ((e = hipMemcpy2DAsync(logits_out, (size_t)L->E * 4, w.logits, (size_t)n_rows * 4, (size_t)L->E * 4, t,
                                   hipMemcpyDeviceToDevice, s)) != hipSuccess)
@@ -484,8 +531,10 @@ static int route_and_dispatch(moe_layer *L, const float *x, int t, int k, int bm
     a.routes = routes;
     a.hits_out = hits;
     a.stats = st;
-    if ((e = launch_dispatch(a, s)) != hipSuccess) return hip_fail(e, "dispatch kernel");
-    return MOE_OK;
+    return stage(L, 2, s, [&] {
+        e = launch_dispatch(a, s);
+        return e == hipSuccess ? MOE_OK : hip_fail(e, "dispatch kernel");
+    });
 }
 
 int moe_layer_route(moe_layer *L, const float *x, int32_t t, moe_route *routes, float *logits, void *stream) {
@@ -527,7 +576,6 @@ int moe_layer_forward(moe_layer *L, const float *x, int32_t t, float *out, float
     const ExpertDev *sh = L->has_shared ? &L->experts_host[L->E] : nullptr;
     hipError_t e = hipSuccess;
     if (path == kMfma) {
-        if ((e = launch_to_f16(x, w.xh, (size_t)t * L->H, s)) != hipSuccess) return hip_fail(e, "f16 conversion");
         MfmaArgs m{};
         m.experts = L->experts_dev;
         m.tiles = w.tiles;
@@ -546,8 +594,17 @@ int moe_layer_forward(moe_layer *L, const float *x, int32_t t, float *out, float
         m.I_s = L->I_s;
         m.E = L->E;
         m.max_tiles = t * k / bm + std::min(L->E, t * k) + 1;
-        if ((e = launch_mfma(true, m, bm, e0, sh, s)) != hipSuccess) return hip_fail(e, "MFMA up kernel");
-        if ((e = launch_mfma(false, m, bm, e0, sh, s)) != hipSuccess) return hip_fail(e, "MFMA down kernel");
+        rc = stage(L, 3, s, [&] {
+            if ((e = launch_to_f16(x, w.xh, (size_t)t * L->H, s)) != hipSuccess) return hip_fail(e, "f16 conversion");
+            e = launch_mfma(true, m, bm, e0, sh, s);
+            return e == hipSuccess ? MOE_OK : hip_fail(e, "MFMA up kernel");
+        });
+        if (rc) return rc;
+        rc = stage(L, 4, s, [&] {
+            e = launch_mfma(false, m, bm, e0, sh, s);
+            return e == hipSuccess ? MOE_OK : hip_fail(e, "MFMA down kernel");
+        });
+        if (rc) return rc;
     } else {
         GemvArgs a{};
         a.experts = L->experts_dev;
@@ -567,13 +624,17 @@ int moe_layer_forward(moe_layer *L, const float *x, int32_t t, float *out, float
         a.E = L->E;
         a.task_bound = std::min(L->E, t * k);
         a.has_shared = L->has_shared;
-        if (path == kGemv) {
-            if ((e = launch_gemv_up(a, e0, sh, s)) != hipSuccess) return hip_fail(e, "GEMV up kernel");
-            if ((e = launch_gemv_down(a, e0, sh, s)) != hipSuccess) return hip_fail(e, "GEMV down kernel");
-        } else {
-            if ((e = launch_gemv_exact(true, a, s)) != hipSuccess) return hip_fail(e, "exact up kernel");
-            if ((e = launch_gemv_exact(false, a, s)) != hipSuccess) return hip_fail(e, "exact down kernel");
-        }
+        const bool fast = path == kGemv;
+        rc = stage(L, 3, s, [&] {
+            e = fast ? launch_gemv_up(a, e0, sh, s) : launch_gemv_exact(true, a, s);
+            return e == hipSuccess ? MOE_OK : hip_fail(e, "expert gate/up kernel");
+        });
+        if (rc) return rc;
+        rc = stage(L, 4, s, [&] {
+            e = fast ? launch_gemv_down(a, e0, sh, s) : launch_gemv_exact(false, a, s);
+            return e == hipSuccess ? MOE_OK : hip_fail(e, "expert down kernel");
+        });
+        if (rc) return rc;
     }
     CombineArgs c{};
     c.y = w.y;
@@ -588,7 +649,41 @@ int moe_layer_forward(moe_layer *L, const float *x, int32_t t, float *out, float
     c.H = L->H;
     c.k = k;
     c.has_shared = L->has_shared;
-    if ((e = launch_combine(c, s)) != hipSuccess) return hip_fail(e, "combine kernel");
+    return stage(L, 5, s, [&] {
+        e = launch_combine(c, s);
+        return e == hipSuccess ? MOE_OK : hip_fail(e, "combine kernel");
+    });
+}
+
+int moe_layer_profile(moe_layer *L, int enable) {
+    if (!L) return fail(MOE_EINVAL, "moe_layer_profile: layer is NULL");
+    L->profile = enable != 0;
+    return MOE_OK;
+}
+
+int moe_layer_stage_times(moe_layer *L, double *ms, uint64_t *n) {
+    if (!L || !ms || !n) return fail(MOE_EINVAL, "moe_layer_stage_times: bad argument");
+    DeviceGuard g(L->ctx->device);
+    if (!L->pending.empty()) {
+        hipError_t e = hipEventSynchronize(L->pending.back().b);
+        if (e != hipSuccess) return hip_fail(e, "hipEventSynchronize");
+    }
+    for (auto &r : L->pending) {
+        float t = 0.0f;
+        if (hipEventElapsedTime(&t, r.a, r.b) == hipSuccess) {
+            L->stage_ms[r.stage] += t;
+            L->stage_n[r.stage] += 1;
+        }
+        L->event_pool.push_back(r.a);
+        L->event_pool.push_back(r.b);
+    }
+    L->pending.clear();
+    for (int i = 0; i < MOE_STAGES; i++) {
+        ms[i] += L->stage_ms[i];
+        n[i] += L->stage_n[i];
+        L->stage_ms[i] = 0.0;
+        L->stage_n[i] = 0;
+    }
     return MOE_OK;
 }
 

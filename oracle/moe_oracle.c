@@ -639,3 +639,9 @@ void orc_mlp_forward(const orc_qt *gate, const orc_qt *up, const orc_qt *down, c
 float orc_expf(float x) { return expf(x); }
 void orc_set_threads(int n) { omp_set_num_threads(n); }
 int orc_max_threads(void) { return omp_get_max_threads(); }
+
+/* expf over an array (host glibc), for checking the device port. */
+void orc_expf_array(const float *x, float *y, size_t n) {
+#pragma omp parallel for schedule(static)
+    for (size_t i = 0; i < n; i++) y[i] = expf(x[i]);
+}

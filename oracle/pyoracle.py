@@ -65,6 +65,7 @@ def lib() -> C.CDLL:
                                           vp]),
             "orc_mlp_forward": (None, [C.POINTER(QT), C.POINTER(QT), C.POINTER(QT), vp, C.c_int, vp]),
             "orc_expf": (C.c_float, [C.c_float]),
+            "orc_expf_array": (None, [vp, vp, sz]),
             "orc_set_threads": (None, [C.c_int]),
             "orc_max_threads": (C.c_int, []),
         }
@@ -133,6 +134,13 @@ def matmul(w: QT, x: np.ndarray) -> np.ndarray:
 
 def expf(x: float) -> np.float32:
     return np.float32(lib().orc_expf(float(x)))
+
+
+def expf_array(x: np.ndarray) -> np.ndarray:
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    y = np.empty_like(x)
+    lib().orc_expf_array(_p(x), _p(y), x.size)
+    return y
 
 
 class OracleLayer:

@@ -1,0 +1,70 @@
+"""Shared helpers for the GPU parity tests."""
+from __future__ import annotations
+
+import sys
+import time
+
+import numpy as np
+
+TOL = 1e-3  # max |gpu - ref| / max |ref| per output tensor (fp32 accumulation)
+
+
+def log(msg: str) -> None:
+    print(f"[{time.strftime('%H:%M:%S')}] {msg}", flush=True)
+    sys.stdout.flush()
+
+
+def rel_err(got: np.ndarray, ref: np.ndarray) -> float:
+    den = float(np.abs(ref).max())
+    return float(np.abs(got.astype(np.float64) - ref).max()) / (den if den > 0 else 1.0)
+
+
+def run_gpu(layer, x: np.ndarray, mode=None, routing=None, prev=None, residual: np.ndarray = None):
+    """One forward through the C ABI; returns host copies of everything."""
+    import torch
+
+    from moe_amd import _lib as L
+
+    dev = torch.device("cuda:0")
+    if mode is not None:
+        layer.set_mode(mode)
+    if routing is not None:
+        layer.set_routing(routing)
+    t, H = x.shape
+    xd = torch.from_numpy(np.ascontiguousarray(x)).to(dev)
+    out = torch.full((t, H), float("nan"), dtype=torch.float32, device=dev)
+    res = torch.from_numpy(np.ascontiguousarray(residual)).to(dev) if residual is not None else None
+    k = layer.k
+    routes = torch.empty((t, k, 2), dtype=torch.int32, device=dev)
+    E = layer.spec.n_experts
+    hits = torch.full((E + 1,), -1, dtype=torch.int32, device=dev)
+    stats = torch.zeros(4, dtype=torch.int64, device=dev)
+    pv = torch.from_numpy(prev.astype(np.int32)).to(dev) if prev is not None else None
+    import ctypes as C
+
+    rc = L.lib().moe_layer_forward(layer.handle, C.c_void_p(xd.data_ptr()), t, C.c_void_p(out.data_ptr()),
+                                   C.c_void_p(res.data_ptr() if res is not None else None),
+                                   C.c_void_p(routes.data_ptr()), C.c_void_p(hits.data_ptr()),
+                                   C.c_void_p(pv.data_ptr() if pv is not None else None),
+                                   C.c_void_p(stats.data_ptr()),
+                                   C.c_void_p(torch.cuda.current_stream().cuda_stream))
+    L.check(rc, "moe_layer_forward")
+    torch.cuda.synchronize()
+    r = routes.cpu().numpy()
+    return dict(out=out.cpu().numpy(), sel=r[..., 0].copy(), w=r[..., 1].view(np.float32).copy(),
+                hits=hits.cpu().numpy().view(np.uint32), stats=stats.cpu().numpy().view(np.uint64),
+                residual=res.cpu().numpy() if res is not None else None)
+
+
+def assert_routing_equal(g: dict, sel: np.ndarray, w: np.ndarray, what: str) -> None:
+    """Selected experts (and their order) and weights bit-exact."""
+    if not np.array_equal(g["sel"], sel):
+        bad = np.argwhere(g["sel"] != sel)
+        t = bad[0][0]
+        raise AssertionError(f"{what}: expert selection differs at {len(bad)} slots; token {t}: "
+                             f"gpu {g['sel'][t].tolist()} ref {sel[t].tolist()}")
+    if not np.array_equal(g["w"].view(np.uint32), w.view(np.uint32)):
+        bad = np.argwhere(g["w"].view(np.uint32) != w.view(np.uint32))
+        t = bad[0][0]
+        raise AssertionError(f"{what}: routing weights differ in {len(bad)} slots; token {t}: "
+                             f"gpu {g['w'][t].tolist()} ref {w[t].tolist()}")

@@ -36,11 +36,14 @@ __global__ __launch_bounds__(256) void combine_kernel(CombineArgs a) {
     for (int c = blockIdx.y * 256 + threadIdx.x; c < a.H; c += gridDim.y * 256) {
         float acc = 0.0f;
         for (int s = 0; s < k; s++) {
-            const float prod = ws[s] * a.y[(size_t)ps[s] * a.H + c];
+            float yv = a.y[(size_t)ps[s] * a.H + c];
+            if (a.y2) yv = yv + a.y2[(size_t)ps[s] * a.H + c];
+            const float prod = ws[s] * yv;
             acc = acc + prod;
         }
         if (a.has_shared) {
             float v = a.ys[(size_t)t * a.H + c];
+            if (a.ys2) v = v + a.ys2[(size_t)t * a.H + c];
             if (a.shgate) v = v * g;
             acc = acc + v;
         }

@@ -16,6 +16,7 @@
 
 using namespace moe;
 
+
 namespace {
 
 thread_local std::string g_err;
@@ -207,6 +208,8 @@ int reserve(moe_layer *L, int max_t, int k) {
         {(void **)&w.hs, T * Is * 4},
         {(void **)&w.y, T * k * H * 4},
         {(void **)&w.ys, T * H * 4},
+        {(void **)&w.y2, T * k * H * 4},
+        {(void **)&w.ys2, T * H * 4},
         {(void **)&w.stats, 4 * 8},
     };
     size_t total = 0;
@@ -378,7 +381,10 @@ int moe_layer_create(moe_ctx *ctx, const moe_layer_desc *d, moe_layer **out) {
         fast &= s.m[0].dt == s.m[1].dt;
     }
     L->fast_ok = fast;
-    L->mfma_ok = fast && H % 128 == 0 && I % 128 == 0 && (!L->has_shared || L->I_s % 128 == 0);
+    bool fmt = true;
+    for (int e = 0; e < E + (L->has_shared ? 1 : 0); e++)
+        for (int m = 0; m < 3; m++) fmt &= mfma_format_ok(L->experts_host[e].m[m].dt);
+    L->mfma_ok = fast && fmt && H % 64 == 0 && I % 64 == 0 && (!L->has_shared || L->I_s % 64 == 0);
 
     // Device-side tables.
     hipError_t he;
@@ -565,16 +571,13 @@ int moe_layer_forward(moe_layer *L, const float *x, int32_t t, float *out, float
         const double avg = (double)t * k / L->E;
         path = (L->mfma_ok && avg >= 3.0) ? kMfma : kGemv;
     }
-    int bm = 0;
-    if (path == kMfma) {
-        const double avg = (double)t * k / L->E;
-        bm = avg <= 16.0 ? 16 : (avg <= 32.0 ? 32 : 64);
-    }
+    const int bm = path == kMfma ? mfma_tile_m() : 0;
     if ((rc = route_and_dispatch(L, x, t, k, bm, routes, hits, prev, stats, nullptr, s))) return rc;
 
     const ExpertDev &e0 = L->experts_host[0];
     const ExpertDev *sh = L->has_shared ? &L->experts_host[L->E] : nullptr;
     hipError_t e = hipSuccess;
+    int ksplit = 1;
     if (path == kMfma) {
         MfmaArgs m{};
         m.experts = L->experts_dev;
@@ -594,6 +597,11 @@ int moe_layer_forward(moe_layer *L, const float *x, int32_t t, float *out, float
         m.I_s = L->I_s;
         m.E = L->E;
         m.max_tiles = t * k / bm + std::min(L->E, t * k) + 1;
+        m.y2 = w.y2;
+        m.ys2 = w.ys2;
+        m.ksplit = mfma_down_ksplit((t * k + bm - 1) / bm + std::min(L->E, t * k) / 2, L->H, L->I);
+        if (L->has_shared && m.ksplit == 2 && L->I_s % 128 != 0) m.ksplit = 1;
+        ksplit = m.ksplit;
         rc = stage(L, 3, s, [&] {
             if ((e = launch_to_f16(x, w.xh, (size_t)t * L->H, s)) != hipSuccess) return hip_fail(e, "f16 conversion");
             e = launch_mfma(true, m, bm, e0, sh, s);
@@ -624,21 +632,31 @@ int moe_layer_forward(moe_layer *L, const float *x, int32_t t, float *out, float
         a.E = L->E;
         a.task_bound = std::min(L->E, t * k);
         a.has_shared = L->has_shared;
+        a.perm_w = w.perm_w;
+        a.shgate = L->has_shared_gate ? w.shgate : nullptr;
+        a.out = out;
+        a.residual = residual;
         const bool fast = path == kGemv;
         rc = stage(L, 3, s, [&] {
             e = fast ? launch_gemv_up(a, e0, sh, s) : launch_gemv_exact(true, a, s);
             return e == hipSuccess ? MOE_OK : hip_fail(e, "expert gate/up kernel");
         });
         if (rc) return rc;
+        // Few tokens: the down projection performs the combine, the shared
+        // expert and the residual add itself.
+        const bool fused = fast && t <= kFusedMaxT;
         rc = stage(L, 4, s, [&] {
-            e = fast ? launch_gemv_down(a, e0, sh, s) : launch_gemv_exact(false, a, s);
+            e = fast ? (fused ? launch_gemv_down_combine(a, e0, sh, s) : launch_gemv_down(a, e0, sh, s))
+                     : launch_gemv_exact(false, a, s);
             return e == hipSuccess ? MOE_OK : hip_fail(e, "expert down kernel");
         });
-        if (rc) return rc;
+        if (rc || fused) return rc;
     }
     CombineArgs c{};
     c.y = w.y;
     c.ys = w.ys;
+    c.y2 = ksplit == 2 ? w.y2 : nullptr;
+    c.ys2 = ksplit == 2 ? w.ys2 : nullptr;
     c.pos = w.pos;
     c.sel = w.sel;
     c.wsel = w.wsel;

@@ -77,6 +77,8 @@ struct Workspace {
     float *hs = nullptr;          // [T, I_s] shared-expert activations
     float *y = nullptr;           // [T*k, H] routed expert outputs
     float *ys = nullptr;          // [T, H] shared-expert outputs
+    float *y2 = nullptr;          // second K half of y (split down projection)
+    float *ys2 = nullptr;         // second K half of ys
     unsigned long long *stats = nullptr;  // [4] fallback when the caller passes none
     void *base = nullptr;         // single allocation backing all of the above
     size_t bytes = 0;
@@ -123,15 +125,23 @@ struct GemvArgs {
     const ExpertDev *experts;     // device table [E+1]
     const int32_t *hits;          // [E+2]
     const int32_t *counts, *offsets, *perm_tok;
+    const float *perm_w;          // [T*k] routing weight of each permuted row
+    const float *shgate;          // [T] sigmoid shared-expert gate, or null
     const float *x;               // [T, H]
     float *h, *hs;                // routed [T*k, I], shared [T, I_s]
     float *y, *ys;                // routed [T*k, H], shared [T, H]
+    float *out, *residual;        // fused combine: [T, H] (residual may be null)
     int T, H, I, I_s, E;
     int task_bound;               // routed tasks launched (>= hits[0])
     int has_shared;
 };
 hipError_t launch_gemv_up(const GemvArgs &a, const ExpertDev &host_e0, const ExpertDev *host_shared, hipStream_t s);
 hipError_t launch_gemv_down(const GemvArgs &a, const ExpertDev &host_e0, const ExpertDev *host_shared, hipStream_t s);
+// Down projection with the combine, shared expert and residual folded in
+// (T <= kFusedMaxT): writes out (and residual) directly.
+constexpr int kFusedMaxT = 8;
+hipError_t launch_gemv_down_combine(const GemvArgs &a, const ExpertDev &host_e0, const ExpertDev *host_shared,
+                                    hipStream_t s);
 
 // Exact-order expert GEMVs (bit-identical to the reference's dot).
 hipError_t launch_gemv_exact(bool up, const GemvArgs &a, hipStream_t s);
@@ -144,9 +154,14 @@ struct MfmaArgs {
     const uint16_t *xh;           // [T, H] f16
     uint16_t *h, *hs;             // f16 [T*k, I], [T, I_s]
     float *y, *ys;                // f32 [T*k, H], [T, H]
+    float *y2, *ys2;              // second K half of the down projection (ksplit == 2)
     int T, H, I, I_s, E;
     int max_tiles;
+    int ksplit;                   // down projection: 1, or 2 halves of K
 };
+int mfma_tile_m();
+bool mfma_format_ok(int dt);
+int mfma_down_ksplit(int m_tiles, int n_rows, int K);
 // up: gate/up + SwiGLU; down: down projection.  Routed tiles come from the
 // dispatch list; the shared expert (sh != null) gets its own launch.
 hipError_t launch_mfma(bool up, const MfmaArgs &a, int bm, const ExpertDev &e0, const ExpertDev *sh, hipStream_t s);
@@ -155,6 +170,7 @@ hipError_t launch_mfma(bool up, const MfmaArgs &a, int bm, const ExpertDev &e0, 
 // (src/model.rs:936-942, 956-970, 680-683).
 struct CombineArgs {
     const float *y, *ys;
+    const float *y2, *ys2;        // or null: second K half, added before weighting
     const int32_t *pos;
     const int32_t *sel;
     const float *wsel;

@@ -45,59 +45,73 @@ __device__ inline float dot_tail(float out, const float *a, const float *b, int 
     return out;
 }
 
-// Small-T router: one block stages `eb` router rows and all T (<= 4) token
-// rows in LDS, then thread (row, j) runs lane j's FMA chain for every token.
-__global__ __launch_bounds__(256) void router_small_kernel(const float *__restrict__ W, const float *__restrict__ x,
-                                                           int T, int n_rows, int E, int H, int eb, float temp,
-                                                           float *__restrict__ logits) {
-    extern __shared__ float lds[];
-    float *wl = lds;
-    float *xl = lds + (size_t)eb * H;
-    const int r0 = blockIdx.x * eb;
-    const int nr = min(eb, n_rows - r0);
-    const int tid = threadIdx.x;
-    if ((H & 3) == 0) {
-        const float4 *w4 = reinterpret_cast<const float4 *>(W + (size_t)r0 * H);
-        float4 *wl4 = reinterpret_cast<float4 *>(wl);
-        for (int i = tid; i < nr * H / 4; i += 256) wl4[i] = w4[i];
-        const float4 *x4 = reinterpret_cast<const float4 *>(x);
-        float4 *xl4 = reinterpret_cast<float4 *>(xl);
-        for (int i = tid; i < T * H / 4; i += 256) xl4[i] = x4[i];
+// Copy n floats from global memory to LDS with every thread of the block,
+// eight 16-byte loads in flight per thread before any store.
+__device__ inline void stage_to_lds(const float *__restrict__ src, float *dst, int n) {
+    const int tid = threadIdx.x, nt = blockDim.x;
+    if ((n & 3) == 0 && (((uintptr_t)src) & 15) == 0) {
+        const float4 *s4 = reinterpret_cast<const float4 *>(src);
+        float4 *d4 = reinterpret_cast<float4 *>(dst);
+        const int n4 = n >> 2;
+        for (int base = 0; base < n4; base += 8 * nt) {
+            float4 v[8];
+#pragma unroll
+            for (int u = 0; u < 8; u++) {
+                const int i = base + u * nt + tid;
+                if (i < n4) v[u] = s4[i];
+            }
+#pragma unroll
+            for (int u = 0; u < 8; u++) {
+                const int i = base + u * nt + tid;
+                if (i < n4) d4[i] = v[u];
+            }
+        }
     } else {
-        for (int i = tid; i < nr * H; i += 256) wl[i] = W[(size_t)r0 * H + i];
-        for (int i = tid; i < T * H; i += 256) xl[i] = x[i];
+        for (int i = tid; i < n; i += nt) dst[i] = src[i];
     }
+}
+
+// Latency-bound router: a block stages RB router rows and TB token rows in
+// LDS (the whole of H), then thread (pair, j) runs lane j of dot_avx2 for one
+// (row, token) pair — one chain per thread, read eight steps at a time.
+__global__ __launch_bounds__(256) void router_lds_kernel(const float *__restrict__ W, const float *__restrict__ x,
+                                                         int T, int n_rows, int E, int H, int RB, int TB, float temp,
+                                                         float *__restrict__ logits) {
+    extern __shared__ float lds[];
+    const int r0 = blockIdx.x * RB, t0 = blockIdx.y * TB;
+    const int nr = min(RB, n_rows - r0), nt = min(TB, T - t0);
+    float *wl = lds;
+    float *xl = lds + (size_t)RB * H;
+    stage_to_lds(W + (size_t)r0 * H, wl, nr * H);
+    stage_to_lds(x + (size_t)t0 * H, xl, nt * H);
     __syncthreads();
-    const int j = tid & 15, rl = tid >> 4;
-    if (rl >= nr) return;  // whole 16-lane groups leave together
+    const int tid = threadIdx.x, j = tid & 15, p = tid >> 4;
+    if (p >= nr * nt) return;  // whole 16-lane groups leave together
+    const int rl = p / nt, tl = p % nt;
     const float *a = wl + (size_t)rl * H;
+    const float *b = xl + (size_t)tl * H;
     const int n16 = H / 16;
     const bool has8 = (H % 16) >= 8;
-    float acc[kSmallRouterTokens];
+    float acc = 0.0f;
+    int c = 0;
+    for (; c + 8 <= n16; c += 8) {
+        float av[8], bv[8];
 #pragma unroll
-    for (int t = 0; t < kSmallRouterTokens; t++) acc[t] = 0.0f;
-    for (int c = 0; c < n16; c++) {
-        float av = a[16 * c + j];
-#pragma unroll
-        for (int t = 0; t < kSmallRouterTokens; t++)
-            if (t < T) acc[t] = fmaf(av, xl[(size_t)t * H + 16 * c + j], acc[t]);
-    }
-    if (has8 && j < 8) {
-#pragma unroll
-        for (int t = 0; t < kSmallRouterTokens; t++)
-            if (t < T) acc[t] = fmaf(a[16 * n16 + j], xl[(size_t)t * H + 16 * n16 + j], acc[t]);
-    }
-    const int tail = 16 * n16 + (has8 ? 8 : 0);
-    const int r = r0 + rl;
-#pragma unroll
-    for (int t = 0; t < kSmallRouterTokens; t++) {
-        if (t >= T) break;
-        float v = reduce16_avx2(acc[t]);
-        if (j == 0) {
-            v = dot_tail(v, a, xl + (size_t)t * H, tail, H);
-            if (temp > 0.0f && r < E) v = v / temp;
-            logits[(size_t)t * n_rows + r] = v;
+        for (int u = 0; u < 8; u++) {
+            av[u] = a[16 * (c + u) + j];
+            bv[u] = b[16 * (c + u) + j];
         }
+#pragma unroll
+        for (int u = 0; u < 8; u++) acc = fmaf(av[u], bv[u], acc);
+    }
+    for (; c < n16; c++) acc = fmaf(a[16 * c + j], b[16 * c + j], acc);
+    if (has8 && j < 8) acc = fmaf(a[16 * n16 + j], b[16 * n16 + j], acc);
+    float v = reduce16_avx2(acc);
+    if (j == 0) {
+        v = dot_tail(v, a, b, 16 * n16 + (has8 ? 8 : 0), H);
+        const int r = r0 + rl;
+        if (temp > 0.0f && r < E) v = v / temp;
+        logits[(size_t)(t0 + tl) * n_rows + r] = v;
     }
 }
 
@@ -112,8 +126,8 @@ constexpr int kKC = 64;   // K chunk
 __global__ __launch_bounds__(256) void router_tiled_kernel(const float *__restrict__ W, const float *__restrict__ x,
                                                            int T, int n_rows, int E, int H, float temp,
                                                            float *__restrict__ logits) {
-    __shared__ float wt[kRT][kKC + 4];
-    __shared__ float xt[kTT][kKC + 4];
+    __shared__ __attribute__((aligned(16))) float wt[kRT][kKC + 4];
+    __shared__ __attribute__((aligned(16))) float xt[kTT][kKC + 4];
     const int tid = threadIdx.x, j = tid & 15, g = tid >> 4;
     const int rg = g & 3, tg = g >> 2;
     const int r0 = blockIdx.x * kRT, t0 = blockIdx.y * kTT;
@@ -124,16 +138,39 @@ __global__ __launch_bounds__(256) void router_tiled_kernel(const float *__restri
     for (int i = 0; i < 8; i++)
 #pragma unroll
         for (int u = 0; u < 8; u++) acc[i][u] = 0.0f;
+    // Each thread moves 2 float4 of W and 2 of x per chunk (32 rows x 16
+    // float4); the next chunk's loads are issued before this chunk's FMAs.
+    const bool vec = (H & 3) == 0;
+    float4 pw[2], px[2];
+    auto load_chunk = [&](int k0) {
+#pragma unroll
+        for (int u = 0; u < 2; u++) {
+            const int q = tid + 256 * u, rr = q >> 4, kk = (q & 15) * 4;
+            const int gk = k0 + kk, gr = r0 + rr, gt = t0 + rr;
+            float4 w4 = make_float4(0.f, 0.f, 0.f, 0.f), x4 = w4;
+            if (vec) {
+                if (gr < n_rows && gk < kfull) w4 = *reinterpret_cast<const float4 *>(W + (size_t)gr * H + gk);
+                if (gt < T && gk < kfull) x4 = *reinterpret_cast<const float4 *>(x + (size_t)gt * H + gk);
+            } else {
+                float *wp = &w4.x, *xp = &x4.x;
+                for (int e = 0; e < 4; e++) {
+                    if (gr < n_rows && gk + e < kfull) wp[e] = W[(size_t)gr * H + gk + e];
+                    if (gt < T && gk + e < kfull) xp[e] = x[(size_t)gt * H + gk + e];
+                }
+            }
+            pw[u] = w4, px[u] = x4;
+        }
+    };
+    if (kfull > 0) load_chunk(0);
     for (int k0 = 0; k0 < kfull; k0 += kKC) {
-        // 32 x 64 floats per operand: 2048 values, 8 per thread.
-        for (int q = tid; q < kRT * kKC; q += 256) {
-            int rr = q / kKC, kk = q % kKC;
-            int gk = k0 + kk;
-            int gr = r0 + rr, gt = t0 + rr;
-            wt[rr][kk] = (gr < n_rows && gk < kfull) ? W[(size_t)gr * H + gk] : 0.0f;
-            xt[rr][kk] = (gt < T && gk < kfull) ? x[(size_t)gt * H + gk] : 0.0f;
+#pragma unroll
+        for (int u = 0; u < 2; u++) {
+            const int q = tid + 256 * u, rr = q >> 4, kk = (q & 15) * 4;
+            *reinterpret_cast<float4 *>(&wt[rr][kk]) = pw[u];
+            *reinterpret_cast<float4 *>(&xt[rr][kk]) = px[u];
         }
         __syncthreads();
+        if (k0 + kKC < kfull) load_chunk(k0 + kKC);
 #pragma unroll
         for (int s = 0; s < kKC / 16; s++) {
             float wv[8], xv[8];
@@ -191,26 +228,36 @@ __device__ inline long long pack_key(int32_t key, int e) {
 }
 constexpr long long kTaken = (long long)0x8000000000000000ull;
 
-// One wavefront per token, experts e = lane*EPL + i.  Restates
+// LDS scratch of one gating wavefront.
+template <int EPL>
+struct GateScratch {
+    float sc[EPL * 64];
+    float rank[EPL * 64];
+    float gs[64];
+    int idx[kMaxTopK];
+    float bcast;
+};
+
+// Orders this wavefront's LDS writes before its later LDS reads (the
+// gating scratch is private to one wavefront, so no block barrier is needed).
+__device__ inline void wave_sync() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+}
+
+// Gating for token t by one wavefront, experts e = lane*EPL + i.  Restates
 // src/model.rs:855-897: gate, rank = score + bias, prune_groups, disabled,
 // stable descending sort truncated to k (ties: lower index first), forced
-// experts, weights = max(score, 0), renormalise, scale.
+// experts, weights = max(score, 0), renormalise, scale.  `lg` is the token's
+// logits row (temperature already applied; entry E is the shared-expert gate
+// logit when the layer has one).
 template <int EPL>
-__global__ __launch_bounds__(256) void gating_kernel(const float *__restrict__ logits, int ld, int T, GateParams p,
-                                                     int32_t *__restrict__ sel, float *__restrict__ wsel,
-                                                     float *__restrict__ shgate,
-                                                     unsigned long long *__restrict__ stats) {
-    __shared__ float s_sc[4][EPL * 64];
-    __shared__ float s_rank[4][EPL * 64];
-    __shared__ float s_gs[4][64];
-    __shared__ int s_idx[4][kMaxTopK];
-    __shared__ float s_bcast[4];
-    const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    const int t = blockIdx.x * 4 + w;
-    const bool active = t < T;
+__device__ void gate_token(const float *__restrict__ lg, int t, const GateParams &p, GateScratch<EPL> &S,
+                           int32_t *__restrict__ sel, float *__restrict__ wsel, float *__restrict__ shgate,
+                           unsigned long long *__restrict__ stats) {
+    const int lane = threadIdx.x & 63;
     const int E = p.n_experts;
-    const float *lg = logits + (size_t)(active ? t : 0) * ld;
-
     float sc[EPL], rank[EPL];
 #pragma unroll
     for (int i = 0; i < EPL; i++) {
@@ -233,16 +280,16 @@ __global__ __launch_bounds__(256) void gating_kernel(const float *__restrict__ l
 #pragma unroll
         for (int i = 0; i < EPL; i++) {
             sc[i] = expf_exact(sc[i] - m);
-            if (lane * EPL + i < E) s_sc[w][lane * EPL + i] = sc[i];
+            if (lane * EPL + i < E) S.sc[lane * EPL + i] = sc[i];
         }
-        __syncthreads();
+        wave_sync();
         if (lane == 0) {
             float s = 0.0f;
-            for (int e = 0; e < E; e++) s += s_sc[w][e];
-            s_bcast[w] = s;
+            for (int e = 0; e < E; e++) s += S.sc[e];
+            S.bcast = s;
         }
-        __syncthreads();
-        const float s = s_bcast[w];
+        wave_sync();
+        const float s = S.bcast;
 #pragma unroll
         for (int i = 0; i < EPL; i++) sc[i] = sc[i] / s;
     }
@@ -254,14 +301,14 @@ __global__ __launch_bounds__(256) void gating_kernel(const float *__restrict__ l
     if (p.n_group > 1 && p.topk_group < p.n_group) {
 #pragma unroll
         for (int i = 0; i < EPL; i++)
-            if (lane * EPL + i < E) s_rank[w][lane * EPL + i] = rank[i];
-        __syncthreads();
+            if (lane * EPL + i < E) S.rank[lane * EPL + i] = rank[i];
+        wave_sync();
         const int per = E / p.n_group;
         if (lane < p.n_group) {
             int32_t k1 = INT32_MIN, k2 = INT32_MIN;
             float v1 = 0.0f, v2 = 0.0f;
             for (int i = 0; i < per; i++) {
-                float v = s_rank[w][lane * per + i];
+                float v = S.rank[lane * per + i];
                 int32_t k = tkey(v);
                 if (k > k1) {
                     k2 = k1, v2 = v1;
@@ -273,18 +320,18 @@ __global__ __launch_bounds__(256) void gating_kernel(const float *__restrict__ l
             float gsum = -0.0f;
             if (per >= 1) gsum = gsum + v1;
             if (per >= 2) gsum = gsum + v2;
-            s_gs[w][lane] = gsum;
+            S.gs[lane] = gsum;
         }
-        __syncthreads();
+        wave_sync();
 #pragma unroll
         for (int i = 0; i < EPL; i++) {
             const int e = lane * EPL + i;
             const int g = per > 0 ? e / per : p.n_group;
             if (e < E && g < p.n_group) {
-                const int32_t kg = tkey(s_gs[w][g]);
+                const int32_t kg = tkey(S.gs[g]);
                 int position = 0;
                 for (int g2 = 0; g2 < p.n_group; g2++) {
-                    const int32_t k2 = tkey(s_gs[w][g2]);
+                    const int32_t k2 = tkey(S.gs[g2]);
                     position += (k2 > kg) || (k2 == kg && g2 < g);
                 }
                 if (position >= p.topk_group) rank[i] = -INFINITY;
@@ -298,12 +345,13 @@ __global__ __launch_bounds__(256) void gating_kernel(const float *__restrict__ l
             if (e < E && p.disabled[e]) rank[i] = -INFINITY;
         }
     }
+    wave_sync();
 #pragma unroll
     for (int i = 0; i < EPL; i++) {
         const int e = lane * EPL + i;
         if (e < E) {
-            s_sc[w][e] = sc[i];
-            s_rank[w][e] = rank[i];
+            S.sc[e] = sc[i];
+            S.rank[e] = rank[i];
         }
     }
     // Selection: k+1 rounds of (key desc, index asc) argmax.  The extra round
@@ -328,16 +376,16 @@ __global__ __launch_bounds__(256) void gating_kernel(const float *__restrict__ l
         if (r > 0 && key == prev_key) tie = 1;
         prev_key = key;
         if (r < k) {
-            if (lane == 0) s_idx[w][r] = e;
+            if (lane == 0) S.idx[r] = e;
 #pragma unroll
             for (int i = 0; i < EPL; i++)
                 if (lane * EPL + i == e) cand[i] = kTaken;
         }
     }
-    __syncthreads();
-    if (active && lane == 0) {
-        int *idx = s_idx[w];
-        const float *rk = s_rank[w];
+    wave_sync();
+    if (lane == 0) {
+        int *idx = S.idx;
+        const float *rk = S.rank;
         for (int f = 0; f < p.n_forced; f++) {
             const int e = p.forced[f];
             if (e < 0 || e >= E) continue;
@@ -357,20 +405,15 @@ __global__ __launch_bounds__(256) void gating_kernel(const float *__restrict__ l
                 idx[b] = v;
             }
         }
-        float wv[kMaxTopK];
         float z = -0.0f;
+        for (int j = 0; j < k; j++) z += fmax_rs(S.sc[idx[j]], 0.0f);
+        if (p.norm_topk) z = fmax_rs(z, 1e-20f);
         for (int j = 0; j < k; j++) {
-            wv[j] = fmax_rs(s_sc[w][idx[j]], 0.0f);
-            z += wv[j];
-        }
-        if (p.norm_topk) {
-            z = fmax_rs(z, 1e-20f);
-            for (int j = 0; j < k; j++) wv[j] = wv[j] / z;
-        }
-        for (int j = 0; j < k; j++) {
-            wv[j] = wv[j] * p.routed_scale;
+            float wv = fmax_rs(S.sc[idx[j]], 0.0f);
+            if (p.norm_topk) wv = wv / z;
+            wv = wv * p.routed_scale;
             sel[(size_t)t * k + j] = idx[j];
-            wsel[(size_t)t * k + j] = wv[j];
+            wsel[(size_t)t * k + j] = wv;
         }
         if (p.has_shared_gate) {
             float nv = -lg[E];
@@ -379,6 +422,19 @@ __global__ __launch_bounds__(256) void gating_kernel(const float *__restrict__ l
         }
         if (tie && stats) atomicAdd(stats + 3, 1ull);
     }
+}
+
+// One wavefront per token.
+template <int EPL>
+__global__ __launch_bounds__(256) void gating_kernel(const float *__restrict__ logits, int ld, int T, GateParams p,
+                                                     int32_t *__restrict__ sel, float *__restrict__ wsel,
+                                                     float *__restrict__ shgate,
+                                                     unsigned long long *__restrict__ stats) {
+    __shared__ GateScratch<EPL> S[4];
+    const int w = threadIdx.x >> 6;
+    const int t = blockIdx.x * 4 + w;
+    if (t >= T) return;
+    gate_token<EPL>(logits + (size_t)t * ld, t, p, S[w], sel, wsel, shgate, stats);
 }
 
 // ---------------------------------------------------------------- dispatch
@@ -549,13 +605,22 @@ hipError_t launch_router(const float *W, const float *x, int T, int n_rows, int 
                          hipStream_t s) {
     const size_t row_bytes = (size_t)H * 4;
     const size_t budget = 64 * 1024;
-    if (T <= kSmallRouterTokens && (size_t)(1 + T) * row_bytes <= budget) {
-        int eb = (int)(budget / row_bytes) - T;
-        eb = eb < 1 ? 1 : (eb > 16 ? 16 : eb);
-        const int blocks = (n_rows + eb - 1) / eb;
-        const size_t lds = (size_t)(eb + T) * row_bytes;
-        hipLaunchKernelGGL(router_small_kernel, dim3(blocks), dim3(256), lds, s, W, x, T, n_rows, E, H, eb, temp,
-                           logits);
+    // Latency kernel: grow the (rows x tokens) block tile while the grid is
+    // larger than two blocks per CU and the tile still fits in LDS.
+    int RB = 1, TB = 1;
+    auto blocks = [&] { return (long long)((n_rows + RB - 1) / RB) * ((T + TB - 1) / TB); };
+    while (blocks() > 512) {
+        if (TB < T && (size_t)(RB + 2 * TB) * row_bytes <= budget && RB * 2 * TB <= 16)
+            TB *= 2;
+        else if (RB < n_rows && (size_t)(2 * RB + TB) * row_bytes <= budget && 2 * RB * TB <= 16)
+            RB *= 2;
+        else
+            break;
+    }
+    if ((size_t)(RB + TB) * row_bytes <= budget && blocks() <= 4096) {
+        dim3 grid((n_rows + RB - 1) / RB, (T + TB - 1) / TB);
+        const size_t lds = (size_t)(RB + TB) * row_bytes;
+        hipLaunchKernelGGL(router_lds_kernel, grid, dim3(256), lds, s, W, x, T, n_rows, E, H, RB, TB, temp, logits);
     } else {
         dim3 grid((n_rows + kRT - 1) / kRT, (T + kTT - 1) / kTT);
         hipLaunchKernelGGL(router_tiled_kernel, grid, dim3(256), 0, s, W, x, T, n_rows, E, H, temp, logits);

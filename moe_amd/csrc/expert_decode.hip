@@ -1,0 +1,684 @@
+// expert_decode.hip — the experts of one token (T = 1) on gfx950.
+//
+// Decoding one token reads every weight of the k selected experts once and
+// does two multiply-adds per weight, so the kernels are HBM-bound only if the
+// arithmetic per weight byte stays small.  They dot the quantised weights
+// directly against two-level int8 activations (qact.h) with v_dot4_i32_i8:
+// a Q4_0 block of 32 values costs 3 unpack operations and 4 integer dots per
+// 8 values plus 5 float operations per block, about 2.4 times fewer
+// operations than dequantising to fp32.  The integer sums are exact; the
+// activation error is at most 2^-16 of each 32-value block's range.
+//
+//  * decode_up_kernel: h = silu(gate . x) * (up . x) for every row of the
+//    selected experts (and the shared expert): src/model.rs:31-33 and the
+//    expert's forward at src/model.rs:925-935.  Persistent waves stream rows
+//    with several rows' weights in flight; each block first encodes x into
+//    LDS.
+//  * decode_down_kernel: a block owns ranges of output rows and one group of
+//    waves per selected expert; it encodes the experts' h into LDS, streams
+//    their down rows and combines each row in LDS: out = sum over the
+//    selected experts in ascending order of w * y, from +0, separate
+//    multiply and add (src/model.rs:842, 936-942); plus the shared expert
+//    times its sigmoid gate (src/model.rs:956-970); plus the residual add
+//    (src/model.rs:680-683).
+//
+// Lanes and rows: a row of `units` 64-value units is covered by CG lanes of
+// a wave (CG = 16, 32 or 64 >= units; lanes own units c and, for rows of
+// 65..128 units, c + 64) or, for wider down rows, by 4 waves of 64 lanes.
+// A lane keeps its units of the activations in registers and streams the
+// same units of many rows.
+#include <hip/hip_fp16.h>
+#include <hip/hip_runtime.h>
+
+#include <mutex>
+#include <vector>
+
+#include "moe_internal.h"
+#include "qact.h"
+
+namespace moe {
+namespace {
+
+typedef uint32_t u32x4a4 __attribute__((ext_vector_type(4), aligned(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+__device__ inline float h2f(uint32_t bits) { return __half2float(__ushort_as_half((unsigned short)(bits & 0xffff))); }
+__device__ inline uint32_t alignb(uint32_t hi, uint32_t lo, uint32_t s) { return __builtin_amdgcn_alignbyte(hi, lo, s); }
+__device__ inline int sdot4(uint32_t a, uint32_t b, int c) { return __builtin_amdgcn_sdot4((int)a, (int)b, c, false); }
+// Bits 0..3 of h moved to bit 4 of bytes 0..3.
+__device__ inline uint32_t spread4(uint32_t h) { return ((h * 0x00204081u) & 0x01010101u) << 4; }
+
+// A 64-value unit of a weight row: two quantisation blocks, 4-byte aligned.
+template <int DT>
+struct WUnit;
+template <>
+struct WUnit<MOE_DT_Q4_0> {
+    static constexpr int dw = 9, bytes = 36;
+};
+template <>
+struct WUnit<MOE_DT_Q5_0> {
+    static constexpr int dw = 11, bytes = 44;
+};
+template <>
+struct WUnit<MOE_DT_Q8_0> {
+    static constexpr int dw = 17, bytes = 68;
+};
+
+// Loads the first WUnit<DT>::dw entries of d (a buffer sized for the widest
+// format in use).
+template <int DT, int DN>
+__device__ inline void load_wunit(const uint8_t *p, uint32_t (&d)[DN]) {
+    static_assert(DN >= WUnit<DT>::dw, "unit buffer too small");
+    const uint32_t *q = reinterpret_cast<const uint32_t *>(__builtin_assume_aligned(p, 4));
+    constexpr int N = WUnit<DT>::dw;
+#pragma unroll
+    for (int i = 0; i + 4 <= N; i += 4) {
+        const u32x4a4 v = *reinterpret_cast<const u32x4a4 *>(q + i);
+        d[i] = v.x, d[i + 1] = v.y, d[i + 2] = v.z, d[i + 3] = v.w;
+    }
+#pragma unroll
+    for (int i = N & ~3; i < N; i++) d[i] = q[i];
+}
+
+// The activation unit (144 bytes, 16-byte aligned) into 36 registers.
+__device__ inline void load_qunit(const uint8_t *p, uint32_t (&x)[kQUnitDw]) {
+    const u32x4 *q = reinterpret_cast<const u32x4 *>(__builtin_assume_aligned(p, 16));
+#pragma unroll
+    for (int i = 0; i < kQUnitDw / 4; i++) {
+        const u32x4 v = q[i];
+        x[4 * i] = v.x, x[4 * i + 1] = v.y, x[4 * i + 2] = v.z, x[4 * i + 3] = v.w;
+    }
+}
+
+// Dot of a weight unit with an activation unit.
+//   Q4_0 [dA qA0..15][dB qB0..15]: byte j holds value j (low nibble) and
+//        value j + 16 (high nibble), stored unsigned with offset 8.
+//   Q5_0 [dA hA(4) qA][dB hB qB]: bit j of h is bit 4 of value j, offset 16.
+//   Q8_0 [dA qA0..31][dB qB0..31]: signed bytes.
+// For a block: sum_i d (q_i - o) x_i = d s2 (254 A + B - o sq) with
+// A = sum q hi, B = sum q lo; B starts at -o sq.
+template <int DT, int DN>
+__device__ inline float qdot(const uint32_t (&d)[DN], const uint32_t (&x)[kQUnitDw]) {
+    static_assert(DN >= WUnit<DT>::dw, "unit buffer too small");
+    const float s2a = __uint_as_float(x[32]), s2b = __uint_as_float(x[33]);
+    const int sqa = (int)x[34], sqb = (int)x[35];
+    int Aa = 0, Ab = 0, Ba, Bb;
+    float sa, sb;
+    if constexpr (DT == MOE_DT_Q4_0) {
+        sa = h2f(d[0]), sb = h2f(d[4] >> 16);
+        Ba = -8 * sqa, Bb = -8 * sqb;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const uint32_t qa = alignb(d[i + 1], d[i], 2), qb = d[5 + i];
+            const uint32_t la = qa & 0x0f0f0f0fu, ha = (qa >> 4) & 0x0f0f0f0fu;
+            const uint32_t lb = qb & 0x0f0f0f0fu, hb = (qb >> 4) & 0x0f0f0f0fu;
+            Aa = sdot4(la, x[i], Aa), Aa = sdot4(ha, x[4 + i], Aa);
+            Ba = sdot4(la, x[16 + i], Ba), Ba = sdot4(ha, x[20 + i], Ba);
+            Ab = sdot4(lb, x[8 + i], Ab), Ab = sdot4(hb, x[12 + i], Ab);
+            Bb = sdot4(lb, x[24 + i], Bb), Bb = sdot4(hb, x[28 + i], Bb);
+        }
+    } else if constexpr (DT == MOE_DT_Q5_0) {
+        sa = h2f(d[0]), sb = h2f(d[5] >> 16);
+        Ba = -16 * sqa, Bb = -16 * sqb;
+        const uint32_t hA = alignb(d[1], d[0], 2), hB = d[6];
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const uint32_t qa = alignb(d[i + 2], d[i + 1], 2), qb = d[7 + i];
+            const uint32_t la = (qa & 0x0f0f0f0fu) | spread4((hA >> (4 * i)) & 0xfu);
+            const uint32_t ha = ((qa >> 4) & 0x0f0f0f0fu) | spread4((hA >> (16 + 4 * i)) & 0xfu);
+            const uint32_t lb = (qb & 0x0f0f0f0fu) | spread4((hB >> (4 * i)) & 0xfu);
+            const uint32_t hb = ((qb >> 4) & 0x0f0f0f0fu) | spread4((hB >> (16 + 4 * i)) & 0xfu);
+            Aa = sdot4(la, x[i], Aa), Aa = sdot4(ha, x[4 + i], Aa);
+            Ba = sdot4(la, x[16 + i], Ba), Ba = sdot4(ha, x[20 + i], Ba);
+            Ab = sdot4(lb, x[8 + i], Ab), Ab = sdot4(hb, x[12 + i], Ab);
+            Bb = sdot4(lb, x[24 + i], Bb), Bb = sdot4(hb, x[28 + i], Bb);
+        }
+    } else {
+        sa = h2f(d[0]), sb = h2f(d[8] >> 16);
+        Ba = 0, Bb = 0;
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            const uint32_t qa = alignb(d[i + 1], d[i], 2), qb = d[9 + i];
+            Aa = sdot4(qa, x[i], Aa), Ba = sdot4(qa, x[16 + i], Ba);
+            Ab = sdot4(qb, x[8 + i], Ab), Bb = sdot4(qb, x[24 + i], Bb);
+        }
+    }
+    const float fa = (float)(254 * Aa + Ba), fb = (float)(254 * Ab + Bb);
+    return fmaf(sb * s2b, fb, (sa * s2a) * fa);
+}
+
+// Sum over groups of CG consecutive lanes (CG = 16, 32, 64); every lane of
+// a group receives the same sum.  The first four steps are DPP moves inside
+// a row of 16 lanes.
+__device__ inline float dpp_add(float v, int ctrl) {
+    int r;
+    switch (ctrl) {
+    case 0: r = __builtin_amdgcn_update_dpp(0, __float_as_int(v), 0xb1, 0xf, 0xf, false); break;   // quad [1,0,3,2]
+    case 1: r = __builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x4e, 0xf, 0xf, false); break;   // quad [2,3,0,1]
+    case 2: r = __builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x141, 0xf, 0xf, false); break;  // half-row mirror
+    default: r = __builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x140, 0xf, 0xf, false); break; // row mirror
+    }
+    return v + __int_as_float(r);
+}
+// Sums over slices of CG consecutive lanes (CG = 16, 32, 64): afterwards
+// the last lane of each slice holds its slice's sum (every lane of it for
+// CG = 16).  Rows of 16 lanes reduce through quad permutes and mirrors; rows
+// join through row broadcasts, which leave the total in the last lane.
+__device__ inline float slice_sum(float v, int cg) {
+    v = dpp_add(v, 0);
+    v = dpp_add(v, 1);
+    v = dpp_add(v, 2);
+    v = dpp_add(v, 3);
+    if (cg >= 32) v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x142, 0xa, 0xf, false));
+    if (cg >= 64) v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x143, 0xc, 0xf, false));
+    return v;
+}
+
+__device__ inline float silu_mul(float g, float u) { return (g / (1.0f + __expf(-g))) * u; }
+
+// Lanes of a row slice: CG lanes (16, 32, 64) own UPL units each (1, or 2
+// for rows of 65..128 units: units c and c + 64 of lane c).
+__device__ inline int lanes_for(int units) { return units <= 16 ? 16 : units <= 32 ? 32 : 64; }
+
+// Encode rows of f32 activations into units in LDS: n_blk 32-value blocks,
+// block b read from src_of(b) and stored as block b of `dst`, one block per
+// thread.
+template <typename Src>
+__device__ inline void encode_to_lds(uint8_t *dst, int n_blk, Src src_of) {
+    for (int b = threadIdx.x; b < n_blk; b += blockDim.x)
+        qact_block_store(src_of(b), dst + (size_t)(b >> 1) * kQUnitBytes, b & 1);
+}
+
+// Loads the 32 floats at src into registers (16-byte aligned).
+__device__ inline void load32(const float *src, float (&v)[32]) {
+    const float4 *s4 = reinterpret_cast<const float4 *>(src);
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+        const float4 f = s4[i];
+        v[4 * i] = f.x, v[4 * i + 1] = f.y, v[4 * i + 2] = f.z, v[4 * i + 3] = f.w;
+    }
+}
+
+// All vector loads of a wave retire in order, so a wave that waits for one
+// also waits for every load issued before it.  The kernels below therefore
+// read their per-task metadata once, into LDS, before the weight stream
+// starts, and issue activation loads ahead of weight loads.
+
+// ------------------------------------------------------------- gate / up
+//
+// Work is a flat list of steps; step s is one row of one task (routed task
+// i = the i-th selected expert, then the shared expert) for each of the
+// 64 / CG row slices of a wave, i.e. rows s * (64 / CG) + slot.  Waves are
+// persistent: wave w takes steps w, w + W, ..., with the weights of the next
+// NBUF - 1 steps in flight while it computes the current one.  A block
+// first encodes x into LDS (while its first weights load); each row's
+// h = silu(gate . x) * (up . x) is written as f32 by the last lane of its
+// slice.
+struct UpStep {
+    const uint8_t *g, *u;  // this lane's first unit of its row
+    float *h;              // its h value
+    bool ok;
+};
+
+__device__ inline UpStep up_step(const DecodeTask *tasks, int k_bound, int s, int n_steps, int spr, int slices,
+                                 int slot, int c, int UB) {
+    UpStep st;
+    st.ok = false;
+    if (s >= n_steps) return st;
+    const int t = s < k_bound * spr ? s / spr : k_bound;
+    const DecodeTask &T = tasks[t];
+    if (!T.live) return st;
+    const int r = (t < k_bound ? s - t * spr : s - k_bound * spr) * slices + slot;
+    st.g = T.g + (size_t)r * T.gs + (size_t)c * UB;
+    st.u = T.u + (size_t)r * T.us + (size_t)c * UB;
+    st.h = T.h + r;
+    st.ok = true;
+    return st;
+}
+
+template <int DT, int UPL, int DW>
+__device__ inline void up_load(const UpStep &st, const bool (&live)[UPL], uint32_t (&w)[2][UPL][DW]) {
+    if (!st.ok) return;
+    constexpr int UB = WUnit<DT>::bytes;
+#pragma unroll
+    for (int j = 0; j < UPL; j++)
+        if (live[j]) {
+            load_wunit<DT, DW>(st.g + (size_t)j * 64 * UB, w[0][j]);
+            load_wunit<DT, DW>(st.u + (size_t)j * 64 * UB, w[1][j]);
+        }
+}
+
+template <int DT, int UPL, int DW>
+__device__ inline void up_compute(const UpStep &st, const bool (&live)[UPL], const uint32_t (&w)[2][UPL][DW],
+                                  const uint32_t (&xa)[UPL][kQUnitDw], int cg, bool tail) {
+    if (!st.ok) return;
+    float g = 0.0f, u = 0.0f;
+#pragma unroll
+    for (int j = 0; j < UPL; j++)
+        if (live[j]) g += qdot<DT, DW>(w[0][j], xa[j]), u += qdot<DT, DW>(w[1][j], xa[j]);
+    g = slice_sum(g, cg);
+    u = slice_sum(u, cg);
+    if (tail) *st.h = silu_mul(g, u);
+}
+
+// Steps per routed task `spr`; the shared expert's steps follow the routed
+// ones as task k_bound.
+template <int DT, int UPL, int NBUF>
+__global__ __launch_bounds__(256) void decode_up_kernel(DecodeArgs a, const float *__restrict__ x, int spr,
+                                                        int n_steps) {
+    extern __shared__ __align__(16) uint8_t xs[];  // x as units
+    __shared__ DecodeTask tasks[kMaxTopK + 1];
+    constexpr int DW = WUnit<DT>::dw, UB = WUnit<DT>::bytes;
+    const int units = a.H / 64, cg = lanes_for(units), slices = 64 / cg;
+    const int lane = threadIdx.x & 63, slot = lane / cg, c = lane % cg;
+    const bool tail = c == cg - 1;
+    bool live[UPL];
+#pragma unroll
+    for (int j = 0; j < UPL; j++) live[j] = c + 64 * j < units;
+    const int waves = blockDim.x >> 6;
+    const int nw = gridDim.x * waves;
+    const int s0 = blockIdx.x * waves + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+
+    // x block of this thread, then the task table.
+    const int n_xb = a.H / 32;
+    float xv[32];
+    if ((int)threadIdx.x < n_xb) load32(x + (size_t)threadIdx.x * 32, xv);
+    const int ntask = a.k_bound + a.n_shared;
+    for (int t = threadIdx.x; t < ntask; t += blockDim.x) tasks[t] = a.tasks[t];
+    __syncthreads();
+
+    uint32_t w[NBUF][2][UPL][DW];
+    UpStep st[NBUF];
+#pragma unroll
+    for (int b = 0; b + 1 < NBUF; b++) {
+        st[b] = up_step(tasks, a.k_bound, s0 + b * nw, n_steps, spr, slices, slot, c, UB);
+        up_load<DT, UPL, DW>(st[b], live, w[b]);
+    }
+    if ((int)threadIdx.x < n_xb)
+        qact_block_store(xv, xs + (size_t)(threadIdx.x >> 1) * kQUnitBytes, threadIdx.x & 1);
+    __syncthreads();
+    uint32_t xa[UPL][kQUnitDw];
+#pragma unroll
+    for (int j = 0; j < UPL; j++)
+        if (live[j]) load_qunit(xs + (size_t)(c + 64 * j) * kQUnitBytes, xa[j]);
+
+    for (int s = s0; s < n_steps;) {
+#pragma unroll
+        for (int b = 0; b < NBUF; b++) {
+            const int nb = (b + NBUF - 1) % NBUF;
+            st[nb] = up_step(tasks, a.k_bound, s + (NBUF - 1) * nw, n_steps, spr, slices, slot, c, UB);
+            up_load<DT, UPL, DW>(st[nb], live, w[nb]);
+            if (s >= n_steps) break;
+            up_compute<DT, UPL, DW>(st[b], live, w[b], xa, cg, tail);
+            s += nw;
+        }
+    }
+}
+
+// --------------------------------------------------------------- h
+//
+// Encodes every task's h (f32, written by the gate/up kernel) as units, one
+// 32-value block per thread: task t's units start at unit t * I / 64, the
+// shared expert's at k_bound * I / 64.
+__global__ __launch_bounds__(256) void encode_h_kernel(DecodeArgs a, uint8_t *__restrict__ hq) {
+    const int blk_r = a.I / 32;
+    const int n_blk = a.k_bound * blk_r + a.n_shared * (a.I_s / 32);
+    const int b = blockIdx.x * 256 + threadIdx.x;
+    if (b >= n_blk) return;
+    const int t = b < a.k_bound * blk_r ? b / blk_r : a.k_bound;
+    const DecodeTask &T = a.tasks[t];
+    if (!T.live) return;
+    const int i = b - t * blk_r;  // block within the task
+    float v[32];
+    load32(T.h + (size_t)i * 32, v);
+    qact_block_store(v, hq + (size_t)(b >> 1) * kQUnitBytes, b & 1);
+}
+
+// --------------------------------------------------------------- down
+//
+// A block owns output row ranges r = blockIdx.x, + gridDim.x, ... of `rb`
+// rows and one group of waves per task: routed task i (the i-th selected
+// expert, ascending) owns waves [i * ks_r, (i + 1) * ks_r), the shared
+// expert the ks_s waves after them.  The block first encodes every task's h
+// into LDS (while the weights of its first ranges load); each wave then
+// keeps its unit of its task's h in registers and streams the task's down
+// rows of each range, NBUF - 1 ranges ahead.  Row slices leave their sums in
+// LDS; after a barrier the block combines each row in the reference's
+// order.  Lanes own one unit (UPL = 1: CG lanes per row slice, 64 / CG slices
+// per wave, or ks = 4 waves of 64 lanes for rows wider than 128 units) or
+// two (UPL = 2, rows of 65..128 units).
+struct DownLane {
+    bool active, tail;
+    int task, kw, slot, rs, cg;
+    bool live[2];
+    const uint8_t *w;  // this lane's first unit of the task's row 0
+    uint32_t stride;
+};
+
+template <int DT, int UPL, int RS, int DW>
+__device__ inline void down_load(const DownLane &L, int range, int n_ranges, int rb, uint32_t (&w)[RS][UPL][DW]) {
+    if (!L.active || range >= n_ranges) return;
+    constexpr int UB = WUnit<DT>::bytes;
+    const uint8_t *p = L.w + (size_t)(range * rb + L.slot * L.rs) * L.stride;
+#pragma unroll
+    for (int i = 0; i < RS; i++)
+#pragma unroll
+        for (int j = 0; j < UPL; j++)
+            if (i < L.rs && L.live[j]) load_wunit<DT, DW>(p + (size_t)i * L.stride + (size_t)j * 64 * UB, w[i][j]);
+}
+
+template <int DT, int UPL, int RS, int DW>
+__device__ inline void down_compute(const DownLane &L, const uint32_t (&w)[RS][UPL][DW],
+                                    const uint32_t (&xa)[UPL][kQUnitDw], float (*part)[32][4]) {
+    if (!L.active) return;
+#pragma unroll
+    for (int i = 0; i < RS; i++) {
+        float acc = 0.0f;
+#pragma unroll
+        for (int j = 0; j < UPL; j++)
+            if (i < L.rs && L.live[j]) acc += qdot<DT, DW>(w[i][j], xa[j]);
+        acc = slice_sum(acc, L.cg);
+        if (L.tail && i < L.rs) part[L.task][L.slot * L.rs + i][L.kw] = acc;
+    }
+}
+
+template <int DT>
+__device__ inline void down_lane(const DecodeTask *tasks, int k_bound, int wv, int ks_r, int ks_s, int rb,
+                                 DownLane &L) {
+    const int routed_waves = k_bound * ks_r;
+    const bool shared = wv >= routed_waves;
+    L.task = shared ? k_bound : wv / ks_r;
+    const DecodeTask &T = tasks[L.task];
+    L.active = T.live != 0;
+    L.tail = false;
+    L.live[0] = L.live[1] = false;
+    L.rs = 0;
+    L.cg = 64;
+    L.kw = L.slot = 0;
+    if (!L.active) return;
+    const int units = T.dcols / 64, lane = threadIdx.x & 63;
+    const int ks = shared ? ks_s : ks_r;
+    L.kw = (shared ? wv - routed_waves : wv) % ks;
+    L.cg = ks > 1 ? 64 : lanes_for(units);
+    L.slot = lane / L.cg;
+    L.rs = rb / (64 / L.cg);
+    L.tail = lane % L.cg == L.cg - 1;
+    const int u0 = L.kw * 64 + lane % L.cg;
+    L.live[0] = u0 < units;
+    L.live[1] = u0 + 64 < units;
+    L.w = T.d + (size_t)u0 * WUnit<DT>::bytes;
+    L.stride = T.ds;
+}
+
+// Combine `n` rows of the partial sums in part (row q of part is row
+// q % rb of the range the block took at iteration it0 + q / rb).
+__device__ inline void down_combine(const DecodeArgs &a, const DecodeTask *tasks, int nh, float (*part)[32][4],
+                                    int it0, int n, int rb, int ks_r, int ks_s) {
+    for (int q = threadIdx.x; q < n; q += blockDim.x) {
+        const int range = blockIdx.x + (it0 + q / rb) * gridDim.x;
+        const int j = range * rb + q % rb;
+        float out = 0.0f;
+        for (int t = 0; t < nh; t++) {
+            float v = 0.0f;
+            for (int k = 0; k < ks_r; k++) v += part[t][q][k];
+            const float prod = tasks[t].w * v;
+            out = out + prod;
+        }
+        if (a.n_shared) {
+            float v = 0.0f;
+            for (int k = 0; k < ks_s; k++) v += part[a.k_bound][q][k];
+            if (a.has_gate) v = v * tasks[a.k_bound].w;
+            out = out + v;
+        }
+        a.out[j] = out;
+        if (a.residual) a.residual[j] = a.residual[j] + out;
+    }
+}
+
+template <int DT_R, int DT_S, int UPL, int RS, int NBUF, int NTHR>
+__global__ __launch_bounds__(NTHR) void decode_down_kernel(DecodeArgs a, const uint8_t *__restrict__ hq, int rb,
+                                                           int ks_r, int ks_s, int n_ranges) {
+    __shared__ float part[2][kDecodeMaxWaves][32][4];
+    __shared__ DecodeTask tasks[kDecodeMaxWaves];
+    // Wave-uniform, so the branches on `shared` are scalar branches.
+    const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    constexpr bool one_fmt = DT_R == DT_S;
+    const bool shared = !one_fmt && wv >= a.k_bound * ks_r;
+    constexpr int DWR = WUnit<DT_R>::dw, DWS = WUnit<DT_S>::dw;
+    constexpr int DW = DWR > DWS ? DWR : DWS;
+    const int ntask = a.k_bound + a.n_shared;
+
+    if ((int)threadIdx.x < ntask) tasks[threadIdx.x] = a.tasks[threadIdx.x];
+    __syncthreads();
+    DownLane L;
+    if (shared)
+        down_lane<DT_S>(tasks, a.k_bound, wv, ks_r, ks_s, rb, L);
+    else
+        down_lane<DT_R>(tasks, a.k_bound, wv, ks_r, ks_s, rb, L);
+    // The lane's units of its task's encoded h first, then the weights.
+    uint32_t xa[UPL][kQUnitDw];
+    if (L.active) {
+        const uint8_t *hu = hq + (size_t)L.task * (a.I / 64) * kQUnitBytes;
+        const int u0 = L.kw * 64 + (threadIdx.x & 63) % L.cg;
+#pragma unroll
+        for (int j = 0; j < UPL; j++)
+            if (L.live[j]) load_qunit(hu + (size_t)(u0 + 64 * j) * kQUnitBytes, xa[j]);
+    }
+    uint32_t w[NBUF][RS][UPL][DW];
+    auto load = [&](int it, uint32_t (&buf)[RS][UPL][DW]) {
+        const int range = blockIdx.x + it * gridDim.x;
+        if (shared)
+            down_load<DT_S, UPL, RS, DW>(L, range, n_ranges, rb, buf);
+        else
+            down_load<DT_R, UPL, RS, DW>(L, range, n_ranges, rb, buf);
+    };
+#pragma unroll
+    for (int b = 0; b + 1 < NBUF; b++) load(b, w[b]);
+
+    // Selected experts (live routed tasks come first).
+    int nh = 0;
+    while (nh < a.k_bound && tasks[nh].live) nh++;
+    // Row sums collect in a 32-row chunk of part; a full chunk (or the last
+    // range) is combined after one barrier, while the next chunk fills the
+    // other half.
+    const int n_it = (n_ranges - (int)blockIdx.x + (int)gridDim.x - 1) / (int)gridDim.x;
+    int it = 0, it0 = 0, sel = 0;
+    for (bool more = it < n_it; more;) {
+#pragma unroll
+        for (int b = 0; b < NBUF; b++) {
+            load(it + NBUF - 1, w[(b + NBUF - 1) % NBUF]);
+            if (it >= n_it) {
+                more = false;
+                break;
+            }
+            float(*pp)[32][4] = reinterpret_cast<float(*)[32][4]>(&part[sel][0][(it - it0) * rb][0]);
+            if (shared)
+                down_compute<DT_S, UPL, RS, DW>(L, w[b], xa, pp);
+            else
+                down_compute<DT_R, UPL, RS, DW>(L, w[b], xa, pp);
+            it++;
+            if ((it - it0) * rb == 32 || it == n_it) {
+                __syncthreads();
+                down_combine(a, tasks, nh, part[sel], it0, (it - it0) * rb, rb, ks_r, ks_s);
+                it0 = it;
+                sel ^= 1;
+            }
+        }
+    }
+}
+
+// --------------------------------------------------------------- launchers
+
+int cus_of_current_device() {
+    static int cus[64] = {};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+    if (!cus[dev]) {
+        int n = 0;
+        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+        cus[dev] = n;
+    }
+    return cus[dev];
+}
+
+// Resident blocks of `kernel` per CU at `threads` threads and `lds` bytes
+// of dynamic LDS (at least 1), remembered per (kernel, threads, lds); lifts
+// the kernel's dynamic LDS limit to `lds` first.
+int occupancy(const void *kernel, int threads, size_t lds) {
+    struct Entry {
+        const void *k;
+        int threads;
+        size_t lds;
+        int n;
+    };
+    static std::mutex mu;
+    static std::vector<Entry> seen;
+    std::lock_guard<std::mutex> g(mu);
+    for (const Entry &e : seen)
+        if (e.k == kernel && e.threads == threads && e.lds == lds) return e.n;
+    (void)hipFuncSetAttribute(kernel, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    int n = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, kernel, threads, lds) != hipSuccess || n < 1) n = 1;
+    seen.push_back({kernel, threads, lds, n});
+    return n;
+}
+
+bool qfmt(int dt) { return dt == MOE_DT_Q4_0 || dt == MOE_DT_Q5_0 || dt == MOE_DT_Q8_0; }
+int lanes_for_host(int units) { return units <= 16 ? 16 : units <= 32 ? 32 : 64; }
+int upl_of(int units) { return units > 64 && units <= 128 ? 2 : 1; }
+int dw_of(int dt) { return dt == MOE_DT_Q8_0 ? 17 : dt == MOE_DT_Q5_0 ? 11 : 9; }
+
+// Down projection: waves per row and row slices per wave group.
+int down_ks(int units) { return units > 128 ? 4 : 1; }
+int down_slices(int units) { return units > 64 ? 1 : 64 / lanes_for_host(units); }
+
+constexpr int kUpBuffers = 4;
+constexpr int kDownBuffers = 3;
+
+template <int DT, int UPL>
+hipError_t up_go(const DecodeArgs &a, const float *x, int n_steps, int spr, hipStream_t s) {
+    auto k = decode_up_kernel<DT, UPL, kUpBuffers>;
+    const size_t lds = (size_t)(a.H / 64) * kQUnitBytes;
+    const int per_cu = occupancy((const void *)k, 256, lds);
+    const int nb = std::max(1, std::min((n_steps + 3) / 4, cus_of_current_device() * per_cu));
+    hipLaunchKernelGGL(k, dim3(nb), dim3(256), lds, s, a, x, spr, n_steps);
+    return hipGetLastError();
+}
+
+// Rows per lane slice of the down kernel for a format pair: what fits the
+// register budget beside the activations, NBUF buffers deep.
+int down_rs(int dt_r, int dt_s, int upl, bool big_block) {
+    const int dw = std::max(dw_of(dt_r), dw_of(dt_s));
+    const int budget = big_block ? 60 : 140;  // registers for the weight ring
+    int rs = 4;
+    while (rs > 1 && kDownBuffers * rs * upl * dw > budget) rs /= 2;
+    return rs;
+}
+
+}  // namespace
+
+bool decode_supported(int H, int I, int I_s, int dt_routed, int dt_shared) {
+    auto width = [](int cols) { return cols > 0 && cols % 64 == 0 && cols / 64 <= 256; };
+    if (!width(H) || H / 64 > 128 || !width(I) || !qfmt(dt_routed)) return false;
+    if (I_s > 0) {
+        if (!width(I_s) || !qfmt(dt_shared)) return false;
+        // One down launch: both formats in one kernel, and the same units per lane.
+        const bool fmt = dt_shared == dt_routed || (dt_routed == MOE_DT_Q4_0 && dt_shared == MOE_DT_Q5_0);
+        if (!fmt || upl_of(I / 64) != upl_of(I_s / 64)) return false;
+    }
+    return true;
+}
+
+bool decode_fits(int I, int I_s, int k, int has_shared, int dt_routed, int dt_shared) {
+    const int waves = k * down_ks(I / 64) + (has_shared ? down_ks(I_s / 64) : 0);
+    if (waves > kDecodeMaxWaves) return false;
+    if (!has_shared) return true;
+    // Every task's row slices must split a range evenly.
+    const int lo = std::min(down_slices(I / 64), down_slices(I_s / 64));
+    const int hi = std::max(down_slices(I / 64), down_slices(I_s / 64));
+    return hi / lo <= down_rs(dt_routed, dt_shared, upl_of(I / 64), waves > 8);
+}
+
+hipError_t launch_decode_up(const DecodeArgs &a, const float *x, int dt_routed, int dt_shared, hipStream_t s) {
+    const int units = a.H / 64, upl = upl_of(units);
+    const int slices = 64 / lanes_for_host(units);
+    auto go = [&](int dt, const DecodeArgs &d, int n_steps, int spr) -> hipError_t {
+        switch (dt * 4 + upl) {
+        case MOE_DT_Q4_0 * 4 + 1: return up_go<MOE_DT_Q4_0, 1>(d, x, n_steps, spr, s);
+        case MOE_DT_Q4_0 * 4 + 2: return up_go<MOE_DT_Q4_0, 2>(d, x, n_steps, spr, s);
+        case MOE_DT_Q5_0 * 4 + 1: return up_go<MOE_DT_Q5_0, 1>(d, x, n_steps, spr, s);
+        case MOE_DT_Q5_0 * 4 + 2: return up_go<MOE_DT_Q5_0, 2>(d, x, n_steps, spr, s);
+        case MOE_DT_Q8_0 * 4 + 1: return up_go<MOE_DT_Q8_0, 1>(d, x, n_steps, spr, s);
+        case MOE_DT_Q8_0 * 4 + 2: return up_go<MOE_DT_Q8_0, 2>(d, x, n_steps, spr, s);
+        default: return hipErrorInvalidValue;
+        }
+    };
+    if (a.I % slices != 0 || (a.n_shared && a.I_s % slices != 0)) return hipErrorInvalidValue;
+    const int spr = a.I / slices;
+    if (!a.n_shared || dt_shared == dt_routed) return go(dt_routed, a, a.k_bound * spr + a.n_shared * (a.I_s / slices), spr);
+    // A shared expert in another format: its own launch.
+    DecodeArgs r = a;
+    r.n_shared = 0;
+    hipError_t e = go(dt_routed, r, a.k_bound * spr, spr);
+    if (e != hipSuccess) return e;
+    DecodeArgs sh = a;
+    sh.k_bound = 0;
+    sh.tasks = a.tasks + a.k_bound;  // the shared expert's entry
+    return go(dt_shared, sh, a.I_s / slices, 1);
+}
+
+hipError_t launch_decode_down(const DecodeArgs &a, uint8_t *hq, int dt_routed, int dt_shared, hipStream_t s) {
+    const int ur = a.I / 64, us = a.n_shared ? a.I_s / 64 : ur;
+    const int upl = upl_of(ur);
+    const int ks_r = down_ks(ur), ks_s = a.n_shared ? down_ks(us) : 1;
+    const int waves = a.k_bound * ks_r + a.n_shared * ks_s;
+    if (waves > kDecodeMaxWaves || (a.n_shared && upl_of(us) != upl)) return hipErrorInvalidValue;
+    {
+        const int n_blk = a.k_bound * (a.I / 32) + a.n_shared * (a.I_s / 32);
+        hipLaunchKernelGGL(encode_h_kernel, dim3((n_blk + 255) / 256), dim3(256), 0, s, a, hq);
+        const hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return e;
+    }
+    const bool big = waves > 8;
+    const int ns_r = down_slices(ur), ns_s = a.n_shared ? down_slices(us) : ns_r;
+    const int lo = std::min(ns_r, ns_s), hi = std::max(ns_r, ns_s);
+    const int ds = a.n_shared ? dt_shared : dt_routed;
+    const int RS = down_rs(dt_routed, ds, upl, big);
+    if (hi / lo > RS) return hipErrorInvalidValue;
+    const int rb = RS * lo;  // every task's slices get rb / ns <= RS rows
+    if (rb > 32 || a.H % rb != 0) return hipErrorInvalidValue;
+    const int n_ranges = a.H / rb;
+    const int threads = 64 * waves;
+    auto launch = [&](auto kern) -> hipError_t {
+        const int per_cu = occupancy((const void *)kern, threads, 0);
+        const int nb = std::max(1, std::min(n_ranges, cus_of_current_device() * per_cu));
+        hipLaunchKernelGGL(kern, dim3(nb), dim3(threads), 0, s, a, hq, rb, ks_r, ks_s, n_ranges);
+        return hipGetLastError();
+    };
+#define MOE_DOWN_RS(R, S, U, N)                                                                                        \
+    switch (RS) {                                                                                                      \
+    case 1: return launch(decode_down_kernel<R, S, U, 1, kDownBuffers, N>);                                           \
+    case 2: return launch(decode_down_kernel<R, S, U, 2, kDownBuffers, N>);                                           \
+    default: return launch(decode_down_kernel<R, S, U, 4, kDownBuffers, N>);                                          \
+    }
+#define MOE_DOWN(R, S)                                                                                                 \
+    if (upl == 2) {                                                                                                    \
+        if (big) { MOE_DOWN_RS(R, S, 2, 1024) } else { MOE_DOWN_RS(R, S, 2, 512) }                                    \
+    } else {                                                                                                           \
+        if (big) { MOE_DOWN_RS(R, S, 1, 1024) } else { MOE_DOWN_RS(R, S, 1, 512) }                                    \
+    }
+    if (dt_routed == MOE_DT_Q4_0 && ds == MOE_DT_Q4_0) {
+        MOE_DOWN(MOE_DT_Q4_0, MOE_DT_Q4_0)
+    } else if (dt_routed == MOE_DT_Q4_0 && ds == MOE_DT_Q5_0) {
+        MOE_DOWN(MOE_DT_Q4_0, MOE_DT_Q5_0)
+    } else if (dt_routed == MOE_DT_Q5_0 && ds == MOE_DT_Q5_0) {
+        MOE_DOWN(MOE_DT_Q5_0, MOE_DT_Q5_0)
+    } else if (dt_routed == MOE_DT_Q8_0 && ds == MOE_DT_Q8_0) {
+        MOE_DOWN(MOE_DT_Q8_0, MOE_DT_Q8_0)
+    }
+#undef MOE_DOWN
+#undef MOE_DOWN_RS
+    return hipErrorInvalidValue;
+}
+
+}  // namespace moe

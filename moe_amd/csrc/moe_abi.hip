@@ -13,6 +13,7 @@
 #include <vector>
 
 #include "moe_internal.h"
+#include "qact.h"
 
 using namespace moe;
 
@@ -51,7 +52,7 @@ struct Region {
 };
 
 // Forward path for a call.
-enum Path { kExact = 1, kGemv = 2, kMfma = 3 };
+enum Path { kExact = 1, kGemv = 2, kMfma = 3, kDecode = 4 };
 
 }  // namespace
 
@@ -68,7 +69,7 @@ struct moe_layer {
     int gate = 0, norm_topk = 1, n_group = 1, topk_group = 1;
     float routed_scale = 1.0f;
     bool has_shared = false, has_shared_gate = false;
-    bool fast_ok = false, mfma_ok = false;
+    bool fast_ok = false, mfma_ok = false, decode_ok = false;
     int mode = 0;  // 0 auto, else a Path
     // routing override
     float temp = 0.0f;
@@ -202,6 +203,9 @@ int reserve(moe_layer *L, int max_t, int k) {
         {(void **)&w.pos, T * k * 4},
         {(void **)&w.hits, (E + 2) * 4},
         {(void **)&w.tiles, 2 * max_tiles * 4},
+        {(void **)&w.dtasks, (size_t)(k + 1) * sizeof(DecodeTask)},
+        {(void **)&w.hq, ((size_t)k * (I / 64) + Is / 64 + 1) * kQUnitBytes},
+        {(void **)&w.route_count, 4},
         {(void **)&w.ntiles, 4},
         {(void **)&w.xh, T * H * 2},
         {(void **)&w.h, T * k * I * 4},
@@ -224,6 +228,11 @@ int reserve(moe_layer *L, int max_t, int k) {
     }
     w.base = base;
     w.bytes = total;
+    if ((e = hipMemset(w.route_count, 0, 4)) != hipSuccess) {
+        hipFree(base);
+        return fail(MOE_EHIP, "workspace counter: %s", hipGetErrorString(e));
+    }
+
     // Old workspace may still be in use by queued work on some stream.
     hipDeviceSynchronize();
     free_ws(L->ws);
@@ -372,12 +381,12 @@ int moe_layer_create(moe_ctx *ctx, const moe_layer_desc *d, moe_layer **out) {
     for (int e = 0; e < E; e++)
         for (int m = 0; m < 3; m++) {
             const MatDev &a = L->experts_host[e].m[m], &b = e0.m[m];
-            fast &= fast_mat(a) && a.dt == b.dt;
+            fast &= fast_mat(a) && a.dt == b.dt && a.dt != MOE_DT_F32;
         }
     fast &= e0.m[0].dt == e0.m[1].dt;
     if (L->has_shared) {
         const ExpertDev &s = L->experts_host[E];
-        for (int m = 0; m < 3; m++) fast &= fast_mat(s.m[m]);
+        for (int m = 0; m < 3; m++) fast &= fast_mat(s.m[m]) && s.m[m].dt != MOE_DT_F32;
         fast &= s.m[0].dt == s.m[1].dt;
     }
     L->fast_ok = fast;
@@ -385,6 +394,13 @@ int moe_layer_create(moe_ctx *ctx, const moe_layer_desc *d, moe_layer **out) {
     for (int e = 0; e < E + (L->has_shared ? 1 : 0); e++)
         for (int m = 0; m < 3; m++) fmt &= mfma_format_ok(L->experts_host[e].m[m].dt);
     L->mfma_ok = fast && fmt && H % 64 == 0 && I % 64 == 0 && (!L->has_shared || L->I_s % 64 == 0);
+    L->decode_ok = fast && decode_supported(H, I, L->has_shared ? L->I_s : 0, e0.m[0].dt,
+                                            L->has_shared ? L->experts_host[E].m[0].dt : e0.m[0].dt);
+    if (L->has_shared) {
+        const ExpertDev &s = L->experts_host[E];
+        L->decode_ok &= s.m[0].dt == s.m[2].dt;
+    }
+    L->decode_ok &= e0.m[0].dt == e0.m[2].dt;
 
     // Device-side tables.
     hipError_t he;
@@ -460,7 +476,8 @@ int moe_layer_set_routing(moe_layer *L, const moe_routing *r) {
 }
 
 int moe_layer_set_mode(moe_layer *L, int mode) {
-    if (!L || mode < 0 || mode > kMfma) return fail(MOE_EINVAL, "moe_layer_set_mode: mode %d", mode);
+    if (!L || mode < 0 || mode > kDecode) return fail(MOE_EINVAL, "moe_layer_set_mode: mode %d", mode);
+    if (mode == kDecode && !L->decode_ok) return fail(MOE_EUNSUP, "this layer's shapes do not fit the one-token kernels");
     if (mode == kGemv && !L->fast_ok) return fail(MOE_EUNSUP, "this layer's shapes do not fit the GEMV kernels");
     if (mode == kMfma && !L->mfma_ok) return fail(MOE_EUNSUP, "this layer's shapes do not fit the MFMA kernels");
     L->mode = mode;
@@ -494,28 +511,14 @@ static GateParams gate_params(const moe_layer *L, int k) {
 }
 
 // Router, gating and dispatch; shared by forward and route.
-static int route_and_dispatch(moe_layer *L, const float *x, int t, int k, int bm, moe_route *routes, uint32_t *hits,
-                              const uint32_t *prev, uint64_t *stats, float *logits_out, hipStream_t s) {
+static int route_and_dispatch(moe_layer *L, const float *x, int t, int k, int bm, bool decode, moe_route *routes,
+                              uint32_t *hits, const uint32_t *prev, uint64_t *stats, float *logits_out,
+                              hipStream_t s) {
     Workspace &w = L->ws;
     const int n_rows = L->E + (L->has_shared_gate ? 1 : 0);
     hipError_t e = hipSuccess;
-    int rc = stage(L, 0, s, [&] {
-        e = launch_router(L->router, x, t, n_rows, L->E, L->H, L->temp, w.logits, s);
-        return e == hipSuccess ? MOE_OK : hip_fail(e, "router kernel");
-    });
-    if (rc) return rc;
     unsigned long long *st = stats ? reinterpret_cast<unsigned long long *>(stats) : w.stats;
     GateParams p = gate_params(L, k);
-    rc = stage(L, 1, s, [&] {
-        e = launch_gating(w.logits, n_rows, t, p, w.sel, w.wsel, w.shgate, st, s);
-        return e == hipSuccess ? MOE_OK : hip_fail(e, "gating kernel");
-    });
-    if (rc) return rc;
-    if (logits_out) {
-        if ((e = hipMemcpy2DAsync(logits_out, (size_t)L->E * 4, w.logits, (size_t)n_rows * 4, (size_t)L->E * 4, t,
-                                  hipMemcpyDeviceToDevice, s)) != hipSuccess)
-            return hip_fail(e, "logits copy");
-    }
     DispatchArgs a{};
     a.sel = w.sel;
     a.wsel = w.wsel;
@@ -537,6 +540,42 @@ static int route_and_dispatch(moe_layer *L, const float *x, int t, int k, int bm
     a.routes = routes;
     a.hits_out = hits;
     a.stats = st;
+    a.shgate_out = w.shgate;
+    if (decode) {
+        a.dtasks = w.dtasks;
+        a.experts = L->experts_dev;
+        a.h = w.h;
+        a.hs = w.hs;
+        a.shgate = L->has_shared_gate ? w.shgate : nullptr;
+        a.I = L->I;
+        a.dk_bound = k;
+    }
+    auto copy_logits = [&]() -> int {
+        if (!logits_out) return MOE_OK;
+        if ((e = hipMemcpy2DAsync(logits_out, (size_t)L->E * 4, w.logits, (size_t)n_rows * 4, (size_t)L->E * 4, t,
+                                  hipMemcpyDeviceToDevice, s)) != hipSuccess)
+            return hip_fail(e, "logits copy");
+        return MOE_OK;
+    };
+    if (t == 1 && route_one_ok(L->H)) {
+        // One token: router, gating and dispatch in a single launch.
+        int rc = stage(L, 0, s, [&] {
+            e = launch_route_one(L->router, x, n_rows, L->E, L->H, L->temp, w.logits, p, a, w.route_count, s);
+            return e == hipSuccess ? MOE_OK : hip_fail(e, "one-token route kernel");
+        });
+        return rc ? rc : copy_logits();
+    }
+    int rc = stage(L, 0, s, [&] {
+        e = launch_router(L->router, x, t, n_rows, L->E, L->H, L->temp, w.logits, s);
+        return e == hipSuccess ? MOE_OK : hip_fail(e, "router kernel");
+    });
+    if (rc) return rc;
+    rc = stage(L, 1, s, [&] {
+        e = launch_gating(w.logits, n_rows, t, p, w.sel, w.wsel, w.shgate, st, s);
+        return e == hipSuccess ? MOE_OK : hip_fail(e, "gating kernel");
+    });
+    if (rc) return rc;
+    if ((rc = copy_logits())) return rc;
     return stage(L, 2, s, [&] {
         e = launch_dispatch(a, s);
         return e == hipSuccess ? MOE_OK : hip_fail(e, "dispatch kernel");
@@ -549,7 +588,7 @@ int moe_layer_route(moe_layer *L, const float *x, int32_t t, moe_route *routes, 
     const int k = effective_k(L);
     int rc = reserve(L, t, k);
     if (rc) return rc;
-    return route_and_dispatch(L, x, t, k, 0, routes, nullptr, nullptr, nullptr, logits, (hipStream_t)stream);
+    return route_and_dispatch(L, x, t, k, 0, false, routes, nullptr, nullptr, nullptr, logits, (hipStream_t)stream);
 }
 
 int moe_layer_forward(moe_layer *L, const float *x, int32_t t, float *out, float *residual, moe_route *routes,
@@ -570,14 +609,46 @@ int moe_layer_forward(moe_layer *L, const float *x, int32_t t, float *out, float
     } else if (L->fast_ok) {
         const double avg = (double)t * k / L->E;
         path = (L->mfma_ok && avg >= 3.0) ? kMfma : kGemv;
+        if (t == 1 && L->decode_ok) path = kDecode;
+    }
+    if (path == kDecode) {
+        const int dt_r = L->experts_host[0].m[0].dt;
+        const int dt_s = L->has_shared ? L->experts_host[L->E].m[0].dt : dt_r;
+        if (t != 1 || !decode_fits(L->I, L->I_s, k, L->has_shared, dt_r, dt_s)) path = kGemv;
     }
     const int bm = path == kMfma ? mfma_tile_m() : 0;
-    if ((rc = route_and_dispatch(L, x, t, k, bm, routes, hits, prev, stats, nullptr, s))) return rc;
+    if ((rc = route_and_dispatch(L, x, t, k, bm, path == kDecode, routes, hits, prev, stats, nullptr, s))) return rc;
 
     const ExpertDev &e0 = L->experts_host[0];
     const ExpertDev *sh = L->has_shared ? &L->experts_host[L->E] : nullptr;
     hipError_t e = hipSuccess;
     int ksplit = 1;
+    if (path == kDecode) {
+        DecodeArgs d{};
+        d.tasks = w.dtasks;
+        d.hits = w.hits;
+        d.h = w.h;
+        d.hs = w.hs;
+        d.has_gate = L->has_shared_gate ? 1 : 0;
+        d.out = out;
+        d.residual = residual;
+        d.H = L->H;
+        d.I = L->I;
+        d.I_s = L->I_s;
+        d.E = L->E;
+        d.k_bound = k;
+        d.n_shared = L->has_shared ? 1 : 0;
+        const int dt_r = e0.m[0].dt, dt_s = sh ? sh->m[0].dt : dt_r;
+        rc = stage(L, 3, s, [&] {
+            e = launch_decode_up(d, x, dt_r, dt_s, s);
+            return e == hipSuccess ? MOE_OK : hip_fail(e, "one-token gate/up kernel");
+        });
+        if (rc) return rc;
+        return stage(L, 4, s, [&] {
+            e = launch_decode_down(d, w.hq, dt_r, dt_s, s);
+            return e == hipSuccess ? MOE_OK : hip_fail(e, "one-token down kernel");
+        });
+    }
     if (path == kMfma) {
         MfmaArgs m{};
         m.experts = L->experts_dev;

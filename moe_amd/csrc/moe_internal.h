@@ -40,6 +40,18 @@ struct ExpertDev {
     int32_t _pad;
 };
 
+// One-token experts: the work of one selected expert (or of the shared
+// expert), as the dispatch kernel lays it out for the one-token kernels.
+struct DecodeTask {
+    const uint8_t *g, *u, *d;     // gate, up and down row 0
+    float *h;                     // the expert's h row
+    uint32_t gs, us, ds;          // row strides
+    int32_t dcols;                // down width (I, or I_s for the shared expert)
+    float w;                      // routing weight (shared expert: its sigmoid gate, or 1)
+    int32_t live;                 // 0: slot not taken (fewer experts selected than k)
+    int32_t _pad[2];
+};
+
 // Routing parameters the gating kernel needs.
 struct GateParams {
     int32_t n_experts;
@@ -71,6 +83,9 @@ struct Workspace {
     int32_t *pos = nullptr;       // [T*k] permuted row of (t, slot)
     int32_t *hits = nullptr;      // [E+2] n, then experts ascending
     int32_t *tiles = nullptr;     // [2 * max_tiles] (group, m0) pairs for the MFMA path
+    DecodeTask *dtasks = nullptr; // [k + 1] one-token task table
+    uint8_t *hq = nullptr;        // [k * I / 64 + I_s / 64] units of h (one-token path)
+    unsigned *route_count = nullptr;  // [1] finished router blocks (one-token route), zero between calls
     int32_t *ntiles = nullptr;    // [1]
     uint16_t *xh = nullptr;       // [T, H] f16 activations (MFMA path)
     float *h = nullptr;           // [T*k, I] routed SwiGLU activations (f32, or f16 on the MFMA path)
@@ -111,8 +126,21 @@ struct DispatchArgs {
     moe_route *routes;            // [T, k] or null
     uint32_t *hits_out;           // [E+1] or null
     unsigned long long *stats;    // [4]
+    float *shgate_out;            // [T] gating output (one-token route kernel)
+    // One token (T = 1) on the one-token kernels: their task table.
+    DecodeTask *dtasks;           // [dk_bound + has_shared] or null
+    const ExpertDev *experts;     // device table [E+1]
+    float *h, *hs;                // h rows the tasks point at
+    const float *shgate;          // [1] or null
+    int I, dk_bound;
 };
 hipError_t launch_dispatch(const DispatchArgs &a, hipStream_t s);
+
+// Router + gating + dispatch of one token in one launch (n_rows blocks; the
+// last to finish gates and dispatches).  `counter` is zero between calls.
+bool route_one_ok(int H);
+hipError_t launch_route_one(const float *W, const float *x, int n_rows, int E, int H, float temp, float *logits,
+                            const GateParams &p, const DispatchArgs &d, unsigned *counter, hipStream_t s);
 
 // y = the gates' exp (glibc expf port) over n values; diagnostics.
 hipError_t launch_expf(const float *x, float *y, size_t n, hipStream_t s);
@@ -145,6 +173,28 @@ hipError_t launch_gemv_down_combine(const GemvArgs &a, const ExpertDev &host_e0,
 
 // Exact-order expert GEMVs (bit-identical to the reference's dot).
 hipError_t launch_gemv_exact(bool up, const GemvArgs &a, hipStream_t s);
+
+// One-token experts on integer dot products (two-level int8 activations).
+struct DecodeArgs {
+    const DecodeTask *tasks;      // [k_bound + n_shared], written by the dispatch kernel
+    const int32_t *hits;          // [E+2]
+    float *h, *hs;                // h: routed [k, I], shared [I_s]
+    int has_gate;                 // the shared expert has a sigmoid gate
+    float *y, *ys;                // routed [k, H], shared [H]
+    float *out, *residual;        // [H] (residual may be null)
+    int H, I, I_s, E;
+    int k_bound;                  // routed tasks launched (>= hits[0])
+    int n_shared;                 // 1 if the shared expert is part of the launch
+};
+// Whether the one-token kernels take these widths and formats, and whether
+// a down-projection block holds k routed experts (and the shared one).
+constexpr int kDecodeMaxWaves = 16;  // waves of a down-projection block
+bool decode_supported(int H, int I, int I_s, int dt_routed, int dt_shared);
+bool decode_fits(int I, int I_s, int k, int has_shared, int dt_routed, int dt_shared);
+hipError_t launch_decode_up(const DecodeArgs &a, const float *x, int dt_routed, int dt_shared, hipStream_t s);
+// Encodes h (into hq: [(k + 1) * max(I, I_s) / 64] units) and runs the down
+// projection and combine.
+hipError_t launch_decode_down(const DecodeArgs &a, uint8_t *hq, int dt_routed, int dt_shared, hipStream_t s);
 
 // Prefill-path grouped GEMMs on MFMA (f16 operands, f32 accumulation).
 struct MfmaArgs {

@@ -235,6 +235,9 @@ struct GateScratch {
     float rank[EPL * 64];
     float gs[64];
     int idx[kMaxTopK];
+    float w[kMaxTopK];          // the selected experts' weights
+    int32_t key[64];            // rank keys (EPL == 1)
+    int32_t bypos[kMaxTopK + 1];  // key at each sorted position <= k (EPL == 1)
     float bcast;
 };
 
@@ -354,32 +357,54 @@ __device__ void gate_token(const float *__restrict__ lg, int t, const GateParams
             S.rank[e] = rank[i];
         }
     }
-    // Selection: k+1 rounds of (key desc, index asc) argmax.  The extra round
-    // finds the best unselected rank for the tie check.
+    // Selection in the stable descending order (key desc, index asc); the
+    // tie check compares neighbours among the first min(k + 1, E).
     const int k = p.top_k;
-    long long cand[EPL];
-#pragma unroll
-    for (int i = 0; i < EPL; i++) {
-        const int e = lane * EPL + i;
-        cand[i] = e < E ? pack_key(tkey(rank[i]), e) : kTaken;
-    }
     int tie = 0;
-    int32_t prev_key = 0;
-    const int rounds = k < E ? k + 1 : k;
-    for (int r = 0; r < rounds; r++) {
-        long long best = kTaken;
+    if constexpr (EPL == 1) {
+        // One expert per lane: its sorted position is the number of experts
+        // ahead of it.
+        const int32_t my = tkey(rank[0]);
+        if (lane < E) S.key[lane] = my;
+        wave_sync();
+        int pos = 0;
+        if (lane < E)
+            for (int e2 = 0; e2 < E; e2++) {
+                const int32_t k2 = S.key[e2];
+                pos += (k2 > my) || (k2 == my && e2 < lane);
+            }
+        if (lane < E && pos < k) S.idx[pos] = lane;
+        if (lane < E && pos <= k) S.bypos[pos] = my;
+        wave_sync();
+        const int last = k < E ? k : E - 1;
+        if (lane >= 1 && lane <= last && S.bypos[lane] == S.bypos[lane - 1]) tie = 1;
+        tie = __any(tie) ? 1 : 0;
+    } else {
+        // k + 1 rounds of argmax; the extra round finds the best unselected
+        // rank for the tie check.
+        long long cand[EPL];
 #pragma unroll
-        for (int i = 0; i < EPL; i++) best = cand[i] > best ? cand[i] : best;
-        best = wave_max64(best);
-        const int e = (int)(0xffffffffu - (uint32_t)(best & 0xffffffffll));
-        const int32_t key = (int32_t)(best >> 32);
-        if (r > 0 && key == prev_key) tie = 1;
-        prev_key = key;
-        if (r < k) {
-            if (lane == 0) S.idx[r] = e;
+        for (int i = 0; i < EPL; i++) {
+            const int e = lane * EPL + i;
+            cand[i] = e < E ? pack_key(tkey(rank[i]), e) : kTaken;
+        }
+        int32_t prev_key = 0;
+        const int rounds = k < E ? k + 1 : k;
+        for (int r = 0; r < rounds; r++) {
+            long long best = kTaken;
 #pragma unroll
-            for (int i = 0; i < EPL; i++)
-                if (lane * EPL + i == e) cand[i] = kTaken;
+            for (int i = 0; i < EPL; i++) best = cand[i] > best ? cand[i] : best;
+            best = wave_max64(best);
+            const int e = (int)(0xffffffffu - (uint32_t)(best & 0xffffffffll));
+            const int32_t key = (int32_t)(best >> 32);
+            if (r > 0 && key == prev_key) tie = 1;
+            prev_key = key;
+            if (r < k) {
+                if (lane == 0) S.idx[r] = e;
+#pragma unroll
+                for (int i = 0; i < EPL; i++)
+                    if (lane * EPL + i == e) cand[i] = kTaken;
+            }
         }
     }
     wave_sync();
@@ -414,6 +439,7 @@ __device__ void gate_token(const float *__restrict__ lg, int t, const GateParams
             wv = wv * p.routed_scale;
             sel[(size_t)t * k + j] = idx[j];
             wsel[(size_t)t * k + j] = wv;
+            S.w[j] = wv;
         }
         if (p.has_shared_gate) {
             float nv = -lg[E];
@@ -468,7 +494,7 @@ __device__ inline int block_scan_excl(int v, int *wave_sums, int *total) {
 // per-expert token order (src/model.rs:902-924).  Positions come from
 // per-wave 64-bit ballots, so tokens keep ascending order within an expert
 // without relying on atomic ordering.
-__global__ __launch_bounds__(kDispatchThreads) void dispatch_kernel(DispatchArgs a) {
+__device__ void dispatch_block(const DispatchArgs &a) {
     __shared__ int cnt[kMaxExperts];
     __shared__ int off[kMaxExperts];
     __shared__ int run[kMaxExperts];
@@ -522,6 +548,34 @@ __global__ __launch_bounds__(kDispatchThreads) void dispatch_kernel(DispatchArgs
     if (tid == 0) {
         a.hits[0] = nh;
         if (a.hits_out) a.hits_out[0] = (uint32_t)nh;
+    }
+    if (a.dtasks) {
+        // One token: selected expert number hp in ascending order is task hp,
+        // with its permuted row o and the weight of the slot that chose it.
+        if (c > 0 && hp < a.dk_bound) {
+            DecodeTask d{};
+            const ExpertDev &x = a.experts[e];
+            d.g = x.m[0].ptr, d.u = x.m[1].ptr, d.d = x.m[2].ptr;
+            d.gs = x.m[0].stride, d.us = x.m[1].stride, d.ds = x.m[2].stride;
+            d.dcols = x.m[2].cols;
+            d.h = a.h + (size_t)o * a.I;
+            for (int s = 0; s < k; s++)
+                if (a.sel[s] == e) d.w = a.wsel[s];
+            d.live = 1;
+            a.dtasks[hp] = d;
+        }
+        for (int t = nh + tid; t < a.dk_bound; t += kDispatchThreads) a.dtasks[t] = DecodeTask{};
+        if (tid == 0 && a.has_shared) {
+            DecodeTask d{};
+            const ExpertDev &x = a.experts[E];
+            d.g = x.m[0].ptr, d.u = x.m[1].ptr, d.d = x.m[2].ptr;
+            d.gs = x.m[0].stride, d.us = x.m[1].stride, d.ds = x.m[2].stride;
+            d.dcols = x.m[2].cols;
+            d.h = a.hs;
+            d.w = a.shgate ? a.shgate[0] : 1.0f;
+            d.live = 1;
+            a.dtasks[a.dk_bound] = d;
+        }
     }
     if (a.bm > 0) {
         const int nt = (c + a.bm - 1) / a.bm;
@@ -587,6 +641,173 @@ __global__ __launch_bounds__(kDispatchThreads) void dispatch_kernel(DispatchArgs
     }
 }
 
+__global__ __launch_bounds__(kDispatchThreads) void dispatch_kernel(DispatchArgs a) { dispatch_block(a); }
+
+// The dispatch of a single token by one wavefront: the same outputs as
+// dispatch_block for T = 1.  idx/w are the token's k selections (distinct
+// experts) in slot order; `bits` is LDS scratch for an E-bit set.
+__device__ void dispatch_one(const DispatchArgs &a, const int *idx, const float *w, unsigned long long *bits) {
+    const int lane = threadIdx.x & 63;
+    const int E = a.E, k = a.k;
+    const int nw = (E + 63) / 64;
+    if (lane < nw) bits[lane] = 0ull;
+    wave_sync();
+    if (lane < k) atomicOr(&bits[idx[lane] >> 6], 1ull << (idx[lane] & 63));
+    wave_sync();
+    // Selected experts before e (ascending): its permuted row, and hit slot.
+    auto below = [&](int e) {
+        int n = 0;
+        for (int q = 0; q < (e >> 6); q++) n += __popcll(bits[q]);
+        const unsigned long long m = (e & 63) ? ((1ull << (e & 63)) - 1) : 0ull;
+        return n + __popcll(bits[e >> 6] & m);
+    };
+    int nsel = 0;
+    for (int q = 0; q < nw; q++) nsel += __popcll(bits[q]);
+    unsigned long long bytes = 0, reused = 0;
+    for (int e = lane; e < E; e += 64) {
+        const int c = (int)((bits[e >> 6] >> (e & 63)) & 1ull);
+        const int o = below(e);
+        a.counts[e] = c;
+        a.offsets[e] = o;
+        if (c) {
+            a.hits[1 + o] = e;
+            if (a.hits_out) a.hits_out[1 + o] = (uint32_t)e;
+            bytes += a.expert_bytes[e];
+            if (a.prev) {
+                bool in_prev = false;
+                for (uint32_t j = 0; j < a.prev[0]; j++) in_prev |= a.prev[1 + j] == (uint32_t)e;
+                reused += in_prev ? 1ull : 0ull;
+            }
+            if (a.bm > 0) {
+                a.tiles[2 * o] = e;
+                a.tiles[2 * o + 1] = 0;
+            }
+            if (a.dtasks && o < a.dk_bound) {
+                DecodeTask d{};
+                const ExpertDev &x = a.experts[e];
+                d.g = x.m[0].ptr, d.u = x.m[1].ptr, d.d = x.m[2].ptr;
+                d.gs = x.m[0].stride, d.us = x.m[1].stride, d.ds = x.m[2].stride;
+                d.dcols = x.m[2].cols;
+                d.h = a.h + (size_t)o * a.I;
+                for (int s = 0; s < k; s++)
+                    if (idx[s] == e) d.w = w[s];
+                d.live = 1;
+                a.dtasks[o] = d;
+            }
+        }
+    }
+    if (lane < k) {
+        const int e = idx[lane], o = below(e);
+        a.perm_tok[o] = 0;
+        a.perm_w[o] = w[lane];
+        a.pos[lane] = o;
+        if (a.routes) {
+            a.routes[lane].expert = (uint32_t)e;
+            a.routes[lane].weight = w[lane];
+        }
+    }
+    if (a.dtasks)
+        for (int t = nsel + lane; t < a.dk_bound; t += 64) a.dtasks[t] = DecodeTask{};
+    // Wave sums of the byte and reuse counts.
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) {
+        bytes += __shfl_xor(bytes, m, 64);
+        reused += __shfl_xor(reused, m, 64);
+    }
+    if (lane == 0) {
+        a.offsets[E] = nsel;
+        a.offsets[E + 1] = nsel + (a.has_shared ? 1 : 0);
+        a.counts[E] = a.has_shared ? 1 : 0;
+        a.hits[0] = nsel;
+        if (a.hits_out) a.hits_out[0] = (uint32_t)nsel;
+        if (a.bm > 0) {
+            int nt = nsel;
+            if (a.has_shared) {
+                a.tiles[2 * nt] = E;
+                a.tiles[2 * nt + 1] = 0;
+                nt++;
+            }
+            a.ntiles[0] = nt;
+        }
+        a.stats[0] += (unsigned long long)k;
+        a.stats[1] += reused;
+        a.stats[2] += bytes;
+        if (a.dtasks && a.has_shared) {
+            DecodeTask d{};
+            const ExpertDev &x = a.experts[E];
+            d.g = x.m[0].ptr, d.u = x.m[1].ptr, d.d = x.m[2].ptr;
+            d.gs = x.m[0].stride, d.us = x.m[1].stride, d.ds = x.m[2].stride;
+            d.dcols = x.m[2].cols;
+            d.h = a.hs;
+            d.w = a.shgate ? a.shgate[0] : 1.0f;
+            d.live = 1;
+            a.dtasks[a.dk_bound] = d;
+        }
+    }
+}
+
+// ------------------------------------------------------------ one token
+//
+// Router, gating and dispatch of a single token in one launch.  Block r
+// computes logit r (dot_avx2's 16 lane chains over the staged row, as in
+// router_lds_kernel); the last block to finish, counted with one device
+// atomic after a release fence, gates the token and dispatches it.  The
+// counter is returned to zero by that block, and no block waits on another.
+template <int EPL>
+__global__ __launch_bounds__(kDispatchThreads) void route_one_kernel(const float *__restrict__ W,
+                                                                     const float *__restrict__ x, int n_rows, int E,
+                                                                     int H, float temp, float *__restrict__ logits,
+                                                                     GateParams p, DispatchArgs d,
+                                                                     unsigned *__restrict__ counter) {
+    extern __shared__ float lds[];  // router row r, then x
+    __shared__ GateScratch<EPL> S;
+    __shared__ int s_last;
+    const int r = blockIdx.x;
+    stage_to_lds(W + (size_t)r * H, lds, H);
+    stage_to_lds(x, lds + H, H);
+    __syncthreads();
+    if (threadIdx.x < 16) {
+        const int j = threadIdx.x;
+        const float *a = lds, *b = lds + H;
+        const int n16 = H / 16;
+        float acc = 0.0f;
+        int c = 0;
+        // Sixteen steps of the chain per batch, their LDS reads issued first.
+        for (; c + 16 <= n16; c += 16) {
+            float av[16], bv[16];
+#pragma unroll
+            for (int u = 0; u < 16; u++) av[u] = a[16 * (c + u) + j], bv[u] = b[16 * (c + u) + j];
+#pragma unroll
+            for (int u = 0; u < 16; u++) acc = fmaf(av[u], bv[u], acc);
+        }
+        for (; c < n16; c++) acc = fmaf(a[16 * c + j], b[16 * c + j], acc);
+        if ((H % 16) >= 8 && j < 8) acc = fmaf(a[16 * n16 + j], b[16 * n16 + j], acc);
+        float v = reduce16_avx2(acc);
+        if (j == 0) {
+            v = dot_tail(v, a, b, 16 * n16 + ((H % 16) >= 8 ? 8 : 0), H);
+            if (temp > 0.0f && r < E) v = v / temp;
+            logits[r] = v;
+        }
+    }
+    // Thread 0 wrote the logit: it releases it with the count, and in the
+    // last block acquires the others' before the barrier hands them on.
+    if (threadIdx.x == 0) {
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+        const bool last = atomicAdd(counter, 1u) == (unsigned)(gridDim.x - 1);
+        if (last) __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+        s_last = last;
+    }
+    __syncthreads();
+    if (!s_last || threadIdx.x >= 64) return;
+    // The last block's first wavefront gates and dispatches the token.
+    __shared__ unsigned long long bits[kMaxExperts / 64];
+    gate_token<EPL>(logits, 0, p, S, const_cast<int32_t *>(d.sel), const_cast<float *>(d.wsel), d.shgate_out,
+                    d.stats);
+    wave_sync();
+    dispatch_one(d, S.idx, S.w, bits);
+    if (threadIdx.x == 0) *counter = 0u;
+}
+
 __global__ void expf_kernel(const float *__restrict__ x, float *__restrict__ y, size_t n) {
     size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
     size_t stride = (size_t)gridDim.x * blockDim.x;
@@ -640,6 +861,27 @@ hipError_t launch_gating(const float *logits, int ld, int T, const GateParams &p
     else
         hipLaunchKernelGGL(gating_kernel<8>, grid, dim3(256), 0, s, logits, ld, T, p, sel, wsel, shgate, stats);
     return hipGetLastError();
+}
+
+bool route_one_ok(int H) { return H > 0 && (size_t)2 * H * 4 <= 64 * 1024; }
+
+hipError_t launch_route_one(const float *W, const float *x, int n_rows, int E, int H, float temp, float *logits,
+                            const GateParams &p, const DispatchArgs &d, unsigned *counter, hipStream_t s) {
+    const size_t lds = (size_t)2 * H * 4;
+    auto go = [&](auto kern) {
+        static bool raised = false;  // dynamic LDS beside the static dispatch tables
+        if (!raised) {
+            (void)hipFuncSetAttribute((const void *)kern, hipFuncAttributeMaxDynamicSharedMemorySize, 64 * 1024);
+            raised = true;
+        }
+        hipLaunchKernelGGL(kern, dim3(n_rows), dim3(kDispatchThreads), lds, s, W, x, n_rows, E, H, temp, logits, p,
+                           d, counter);
+        return hipGetLastError();
+    };
+    if (p.n_experts <= 64) return go(route_one_kernel<1>);
+    if (p.n_experts <= 128) return go(route_one_kernel<2>);
+    if (p.n_experts <= 256) return go(route_one_kernel<4>);
+    return go(route_one_kernel<8>);
 }
 
 hipError_t launch_dispatch(const DispatchArgs &a, hipStream_t s) {

@@ -108,6 +108,8 @@ LAYER_CASES = [
     ("qwen3", 1, None), ("qwen3", 128, None), ("qwen3", 2048, None),
     ("v2_lite", 1, None), ("v2_lite", 32, None), ("v2_lite", 33, 2), ("v2_lite", 256, None),
     ("deepseek_v3", 1, None), ("deepseek_v3", 64, None),
+    # one-token kernels forced (4) and the register GEMV at T = 1 (2)
+    ("tiny_mixtral", 1, 4), ("tiny_mixtral", 1, 2), ("mixtral", 1, 2), ("qwen3", 1, 2), ("deepseek_v3", 1, 2),
 ]
 
 
@@ -128,6 +130,62 @@ def test_layer_parity(ctx, oracle, name, t, mode):
     err = rel_err(g["out"], out)
     log(f"{name} T={t} mode={mode}: max rel err {err:.2e}")
     assert err <= TOL, f"{name} T={t}: max rel err {err:.3e} > {TOL}"
+
+
+DECODE_TOL = 1e-4  # one-token kernels: 2^-16 activation steps, exact integer dots
+
+
+@pytest.mark.parametrize("name,scale", [
+    ("tiny_mixtral", {}), ("mixtral", {}), ("qwen3", {}), ("v2_lite", {}), ("deepseek_v3", {}),
+    ("deepseek_v3", dict(hidden=512, inter=128, shared_inter=128)),
+    ("v2_lite", dict(hidden=1024, inter=256, shared_inter=512)),
+    ("mixtral", dict(hidden=1024, inter=5120)),   # down rows of 80 units: two per lane
+    ("qwen3", dict(hidden=6144, inter=512)),      # gate/up rows of 96 units: two per lane
+])
+def test_decode_repeated_calls(ctx, oracle, name, scale):
+    """The one-token kernels over several tokens in a row: each call's output
+    within DECODE_TOL of the CPU path, so the per-range counters the down
+    kernel uses return to zero after every call."""
+    from moe_amd import synth
+
+    host, gl, ol = layer_pair(ctx, oracle, name, **scale)
+    H = host.shape.hidden
+    worst = 0.0
+    for i in range(3):
+        x = synth.activations(SEED + 100 + i, 1, H)
+        out, sel, w, hits, stats = ol.forward(x)
+        g = run_gpu(gl, x, mode=4)
+        assert_routing_equal(g, sel, w, f"{name} call {i}")
+        err = rel_err(g["out"], out)
+        worst = max(worst, err)
+        assert err <= DECODE_TOL, f"{name} call {i}: max rel err {err:.3e}"
+    gl.set_mode(0)
+    log(f"{name} {scale or ''} one-token x3: max rel err {worst:.2e}")
+
+
+@pytest.mark.parametrize("kind", ["disabled", "forced", "top1", "topE", "forced2"])
+def test_decode_interventions(ctx, oracle, kind):
+    """Interventions change k and the hit list at T = 1; the one-token
+    kernels follow them."""
+    from moe_amd import synth
+    from moe_amd.layer import Routing
+
+    host, gl, ol = layer_pair(ctx, oracle, "tiny_mixtral")
+    x = synth.activations(SEED + 5, 1, 512)
+    base_sel, *_ = ol.route(x)
+    victim, target = int(base_sel[0, 0]), int((base_sel[0, 0] + 3) % 8)
+    spec = dict(disabled=dict(disabled=[victim]), forced=dict(forced=[target]), top1=dict(top_k=1),
+                topE=dict(top_k=8), forced2=dict(forced=[target, (target + 1) % 8]))[kind]
+    out, sel, w, hits, stats = ol.forward(x, oracle.OracleLayer.routing(**spec))
+    r_gpu = Routing(disabled=[(0, e) for e in spec.get("disabled", [])],
+                    forced=[(0, e) for e in spec.get("forced", [])], top_k=spec.get("top_k", 0))
+    try:
+        g = run_gpu(gl, x, mode=4, routing=r_gpu)
+    finally:
+        gl.set_routing(None)
+        gl.set_mode(0)
+    assert_routing_equal(g, sel, w, kind)
+    assert rel_err(g["out"], out) <= DECODE_TOL
 
 
 @pytest.mark.parametrize("name,t", [("tiny_mixtral", 1), ("tiny_mixtral", 16), ("tiny_mixtral", 5)])

@@ -33,6 +33,7 @@
 #include <mutex>
 #include <vector>
 
+#include "gmem.h"
 #include "moe_internal.h"
 #include "qact.h"
 
@@ -73,16 +74,19 @@ __device__ inline void load_wunit(const uint8_t *p, uint32_t (&d)[DN]) {
     constexpr int N = WUnit<DT>::dw;
 #pragma unroll
     for (int i = 0; i + 4 <= N; i += 4) {
-        const u32x4a4 v = *reinterpret_cast<const u32x4a4 *>(q + i);
+        const u32x4_dw v = gload_x4(q + i);
         d[i] = v.x, d[i + 1] = v.y, d[i + 2] = v.z, d[i + 3] = v.w;
     }
 #pragma unroll
-    for (int i = N & ~3; i < N; i++) d[i] = q[i];
+    for (int i = N & ~3; i < N; i++) d[i] = gload(q + i);
 }
 
-// The activation unit (144 bytes, 16-byte aligned) into 36 registers.
+// The activation unit (144 bytes, 16-byte aligned) into 36 registers, from
+// address space AS (1: global, 3: LDS).
+template <int AS>
 __device__ inline void load_qunit(const uint8_t *p, uint32_t (&x)[kQUnitDw]) {
-    const u32x4 *q = reinterpret_cast<const u32x4 *>(__builtin_assume_aligned(p, 16));
+    typedef const __attribute__((address_space(AS))) u32x4 *v4p;
+    const v4p q = (v4p)p;
 #pragma unroll
     for (int i = 0; i < kQUnitDw / 4; i++) {
         const u32x4 v = q[i];
@@ -180,21 +184,13 @@ __device__ inline float silu_mul(float g, float u) { return (g / (1.0f + __expf(
 // for rows of 65..128 units: units c and c + 64 of lane c).
 __device__ inline int lanes_for(int units) { return units <= 16 ? 16 : units <= 32 ? 32 : 64; }
 
-// Encode rows of f32 activations into units in LDS: n_blk 32-value blocks,
-// block b read from src_of(b) and stored as block b of `dst`, one block per
-// thread.
-template <typename Src>
-__device__ inline void encode_to_lds(uint8_t *dst, int n_blk, Src src_of) {
-    for (int b = threadIdx.x; b < n_blk; b += blockDim.x)
-        qact_block_store(src_of(b), dst + (size_t)(b >> 1) * kQUnitBytes, b & 1);
-}
-
 // Loads the 32 floats at src into registers (16-byte aligned).
+typedef float f32x4 __attribute__((ext_vector_type(4)));
 __device__ inline void load32(const float *src, float (&v)[32]) {
-    const float4 *s4 = reinterpret_cast<const float4 *>(src);
+    const f32x4 *s4 = reinterpret_cast<const f32x4 *>(src);
 #pragma unroll
     for (int i = 0; i < 8; i++) {
-        const float4 f = s4[i];
+        const f32x4 f = gload(s4 + i);
         v[4 * i] = f.x, v[4 * i + 1] = f.y, v[4 * i + 2] = f.z, v[4 * i + 3] = f.w;
     }
 }
@@ -258,7 +254,7 @@ __device__ inline void up_compute(const UpStep &st, const bool (&live)[UPL], con
         if (live[j]) g += qdot<DT, DW>(w[0][j], xa[j]), u += qdot<DT, DW>(w[1][j], xa[j]);
     g = slice_sum(g, cg);
     u = slice_sum(u, cg);
-    if (tail) *st.h = silu_mul(g, u);
+    if (tail) gstore(st.h, silu_mul(g, u));
 }
 
 // Steps per routed task `spr`; the shared expert's steps follow the routed
@@ -295,12 +291,12 @@ __global__ __launch_bounds__(256) void decode_up_kernel(DecodeArgs a, const floa
         up_load<DT, UPL, DW>(st[b], live, w[b]);
     }
     if ((int)threadIdx.x < n_xb)
-        qact_block_store(xv, xs + (size_t)(threadIdx.x >> 1) * kQUnitBytes, threadIdx.x & 1);
+        qact_block_put<3>(qact_block(xv), xs + (size_t)(threadIdx.x >> 1) * kQUnitBytes, threadIdx.x & 1);
     __syncthreads();
     uint32_t xa[UPL][kQUnitDw];
 #pragma unroll
     for (int j = 0; j < UPL; j++)
-        if (live[j]) load_qunit(xs + (size_t)(c + 64 * j) * kQUnitBytes, xa[j]);
+        if (live[j]) load_qunit<3>(xs + (size_t)(c + 64 * j) * kQUnitBytes, xa[j]);
 
     for (int s = s0; s < n_steps;) {
 #pragma unroll
@@ -331,7 +327,7 @@ __global__ __launch_bounds__(256) void encode_h_kernel(DecodeArgs a, uint8_t *__
     const int i = b - t * blk_r;  // block within the task
     float v[32];
     load32(T.h + (size_t)i * 32, v);
-    qact_block_store(v, hq + (size_t)(b >> 1) * kQUnitBytes, b & 1);
+    qact_block_put<1>(qact_block(v), hq + (size_t)(b >> 1) * kQUnitBytes, b & 1);
 }
 
 // --------------------------------------------------------------- down
@@ -430,8 +426,8 @@ __device__ inline void down_combine(const DecodeArgs &a, const DecodeTask *tasks
             if (a.has_gate) v = v * tasks[a.k_bound].w;
             out = out + v;
         }
-        a.out[j] = out;
-        if (a.residual) a.residual[j] = a.residual[j] + out;
+        gstore(a.out + j, out);
+        if (a.residual) gstore(a.residual + j, gload(a.residual + j) + out);
     }
 }
 
@@ -462,7 +458,7 @@ __global__ __launch_bounds__(NTHR) void decode_down_kernel(DecodeArgs a, const u
         const int u0 = L.kw * 64 + (threadIdx.x & 63) % L.cg;
 #pragma unroll
         for (int j = 0; j < UPL; j++)
-            if (L.live[j]) load_qunit(hu + (size_t)(u0 + 64 * j) * kQUnitBytes, xa[j]);
+            if (L.live[j]) load_qunit<1>(hu + (size_t)(u0 + 64 * j) * kQUnitBytes, xa[j]);
     }
     uint32_t w[NBUF][RS][UPL][DW];
     auto load = [&](int it, uint32_t (&buf)[RS][UPL][DW]) {

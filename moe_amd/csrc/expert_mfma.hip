@@ -19,6 +19,9 @@
 #include <hip/hip_fp16.h>
 #include <hip/hip_runtime.h>
 
+#include <type_traits>
+
+#include "gmem.h"
 #include "moe_internal.h"
 
 namespace moe {
@@ -26,6 +29,7 @@ namespace {
 
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 typedef float floatx4 __attribute__((ext_vector_type(4)));
+typedef float floatx16 __attribute__((ext_vector_type(16)));
 typedef uint32_t u32x4a __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2a __attribute__((ext_vector_type(2)));
 
@@ -73,19 +77,23 @@ struct Fmt<MOE_DT_Q8_0> {
     static constexpr int bytes = 34, fetch = 9, rec = 9;
 };
 
-// Fetch block b of a 4-byte-aligned row and normalise it to its LDS record:
-// rec[0] = scale (low 16 bits), rec[1..] = the bytes after the scale.
+// The dwords covering block b of a 4-byte-aligned row, as loaded (global
+// loads; nothing waits for them here).
 template <int DT>
-__device__ inline void fetch_block(const uint8_t *row, int b, uint32_t (&rec)[Fmt<DT>::rec]) {
-    constexpr int N = Fmt<DT>::fetch;
-    const int byte0 = b * Fmt<DT>::bytes;
-    const uint32_t *q = reinterpret_cast<const uint32_t *>(__builtin_assume_aligned(row, 4)) + (byte0 >> 2);
-    uint32_t d[N];
+__device__ inline void fetch_raw(const uint8_t *row, int b, uint32_t (&d)[Fmt<DT>::fetch]) {
+    const uint32_t *q =
+        reinterpret_cast<const uint32_t *>(__builtin_assume_aligned(row, 4)) + ((b * Fmt<DT>::bytes) >> 2);
 #pragma unroll
-    for (int i = 0; i < N; i++) d[i] = q[i];
-    const bool odd = (byte0 & 2) != 0;
-    // s = the block starting at byte 0.
-    uint32_t s[N];
+    for (int i = 0; i < Fmt<DT>::fetch; i++) d[i] = gload(q + i);
+}
+
+// Normalise fetched dwords to the block's LDS record: rec[0] = scale (low 16
+// bits), rec[1..] = the bytes after the scale.  `odd`: the block starts 2
+// bytes into its first dword (an odd block index in every format).
+template <int DT>
+__device__ inline void normalise(const uint32_t (&d)[Fmt<DT>::fetch], bool odd, uint32_t (&rec)[Fmt<DT>::rec]) {
+    constexpr int N = Fmt<DT>::fetch;
+    uint32_t s[N];  // the block starting at byte 0
 #pragma unroll
     for (int i = 0; i < N - 1; i++) s[i] = odd ? alignb(d[i + 1], d[i], 2) : d[i];
     s[N - 1] = odd ? (d[N - 1] >> 16) : d[N - 1];
@@ -186,122 +194,167 @@ __global__ __launch_bounds__(256, 2) void mfma_kernel(MfmaArgs a, int mode, int 
 
     // ---- load assignments: thread -> A row am, 32-value block ah of the step;
     //      weight row bn (tile column), block bb of the step.
+    // Every thread issues the same loads on every step (rows past the end
+    // read row 0 and are zeroed when stored), so each wait for a step's data
+    // is an exact count of the loads issued after it.
     const int am = tid >> 1, ab = tid & 1;
     const int arow = src_row[am];
-    const uint16_t *abase = nullptr;
-    if (arow >= 0) abase = UP ? a.xh + (size_t)arow * a.H : (ti.shared ? a.hs : a.h) + (size_t)arow * Icol;
+    const bool avalid = arow >= 0;
+    const uint16_t *abase = UP ? a.xh + (size_t)(avalid ? arow : src_row[0]) * a.H
+                               : (ti.shared ? a.hs : a.h) + (size_t)(avalid ? arow : src_row[0]) * Icol;
     const int bn = tid >> 1, bb = tid & 1;
     const MatDev &BW = (UP && bn >= BN / 2) ? W1 : W0;
     const int brow = UP ? n0 + (bn & (BN / 2 - 1)) : n0 + bn;
     const bool bvalid = brow < BW.rows;
-    const uint8_t *browp = bvalid ? BW.ptr + (size_t)brow * BW.stride : nullptr;
+    const uint8_t *browp = BW.ptr + (size_t)(bvalid ? brow : 0) * BW.stride;
 
-    u32x4a areg[4];
-    uint32_t brec[REC];
-    auto load_step = [&](int k0) {
-        if (abase) {
-            const u32x4a *src = reinterpret_cast<const u32x4a *>(abase + k0 + 32 * ab);
+    // Global loads run NPF steps ahead of the MFMAs through a register ring
+    // of raw dwords; they are normalised when stored to LDS (double
+    // buffered), so nothing waits for a load until its step is stored.
+    constexpr int NPF = 3;
+    constexpr int FD = Fmt<DT>::fetch;
+    u32x4a areg[NPF][4];
+    uint32_t braw[NPF][FD];
+    const bool bodd = (bb & 1) != 0;  // block k0 / 32 + bb, with k0 / 32 even
+    auto load_step = [&](int k0, u32x4a (&ar)[4], uint32_t (&br)[FD]) {
+        const int kc = k0 < kend ? k0 : kbeg;  // past the end: a harmless reload
+        const u32x4a *src = reinterpret_cast<const u32x4a *>(abase + kc + 32 * ab);
 #pragma unroll
-            for (int i = 0; i < 4; i++) areg[i] = src[i];
-        } else {
-#pragma unroll
-            for (int i = 0; i < 4; i++) areg[i] = u32x4a{0u, 0u, 0u, 0u};
-        }
-        if (bvalid) {
-            fetch_block<DT>(browp, k0 / 32 + bb, brec);
-        } else {
-#pragma unroll
-            for (int i = 0; i < REC; i++) brec[i] = 0u;  // scale 0 -> zero weights
-        }
+        for (int i = 0; i < 4; i++) ar[i] = gload(src + i);
+        fetch_raw<DT>(browp, kc / 32 + bb, br);
     };
     // Chunk c of a 32-value block holds elements 8c..8c+7; its two halves go
     // to the K-permuted slots 16 (c & 1) + 4 (c >> 1) and that + 8.
-    auto store_step = [&](int buf) {
+    auto store_step = [&](int buf, const u32x4a (&ar)[4], const uint32_t (&br)[FD]) {
         _Float16 *arow_lds = &As[buf][am * LDA + 32 * ab];
 #pragma unroll
         for (int c = 0; c < 4; c++) {
             const int p0 = 16 * (c & 1) + 4 * (c >> 1);
-            *reinterpret_cast<u32x2a *>(arow_lds + p0) = u32x2a{areg[c].x, areg[c].y};
-            *reinterpret_cast<u32x2a *>(arow_lds + p0 + 8) = u32x2a{areg[c].z, areg[c].w};
+            const u32x4a v = avalid ? ar[c] : u32x4a{0u, 0u, 0u, 0u};
+            *reinterpret_cast<u32x2a *>(arow_lds + p0) = u32x2a{v.x, v.y};
+            *reinterpret_cast<u32x2a *>(arow_lds + p0 + 8) = u32x2a{v.z, v.w};
         }
+        uint32_t rec[REC];
+        normalise<DT>(br, bodd, rec);
+        if (!bvalid) rec[0] = 0u;  // scale 0: a zero weight row
         uint32_t *brow_lds = &Bs[buf][bn * BREC + bb * REC];
 #pragma unroll
-        for (int i = 0; i < REC; i++) brow_lds[i] = brec[i];
+        for (int i = 0; i < REC; i++) brow_lds[i] = rec[i];
     };
 
-    floatx4 acc[8][2];
+    // Wave wv owns all 128 tokens and one 32-column tile: up -> lanes with
+    // l % 32 < 16 take gate rows 16 wv .. +16 and the others the same up rows
+    // (tile rows 64 + ...); down -> columns 32 wv .. +32.  Each
+    // V_MFMA_F32_32X32X16_F16 takes A lane l = row l % 32, K slots
+    // 8 (l / 32) .. +8 and B lane l = column l % 32, the same K slots; D lane l
+    // element v = row 8 (v / 4) + 4 (l / 32) + v % 4, column l % 32.  Within a
+    // 32-value block, MFMA m covers permuted slots 16 m .. 16 m + 15, so lane
+    // half h reads slot group q = 2 m + h: the eight codes of dword q.  A
+    // dequantised B fragment feeds the 32-token MFMAs of the tile's live rows.
+    floatx16 acc[4];
 #pragma unroll
-    for (int i = 0; i < 8; i++)
-#pragma unroll
-        for (int j = 0; j < 2; j++) acc[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
+    for (int t = 0; t < 4; t++) acc[t] = floatx16{};
+    const int l32 = lane & 31, hf = lane >> 5;
+    const int bcol = UP ? ((l32 < 16 ? 0 : 64) + 16 * wv + (l32 & 15)) : (32 * wv + l32);
 
-    // Wave wv owns tile columns: up -> gate cols 16 wv .. +16 (j = 0) and the
-    // same up cols (tile col 64 + ..., j = 1); down -> cols 32 wv + 16 j.
-    const int msub = (valid + 15) / 16;
-    const int q = lane >> 4, r16 = lane & 15;
-    int bcol[2];
+    // The K loop for MT live 32-token tiles (chosen once per block).
+    auto run = [&](auto mt_c) {
+        constexpr int MT = decltype(mt_c)::value;
+        auto compute = [&](int buf) {
 #pragma unroll
-    for (int j = 0; j < 2; j++) bcol[j] = UP ? (64 * j + 16 * wv + r16) : (32 * wv + 16 * j + r16);
-
-    load_step(kbeg);
-    store_step(0);
-    __syncthreads();
-    int buf = 0;
-    for (int k0 = kbeg; k0 < kend; k0 += BK) {
-        const bool more = k0 + BK < kend;
-        if (more) load_step(k0 + BK);
+            for (int kb = 0; kb < 2; kb++) {
 #pragma unroll
-        for (int kb = 0; kb < 2; kb++) {
-            half8 bf[2];
+                for (int m = 0; m < 2; m++) {
+                    const int q = 2 * m + hf;
+                    const half8 bf = dequant_q<DT>(&Bs[buf][bcol * BREC + kb * REC], q);
 #pragma unroll
-            for (int j = 0; j < 2; j++) bf[j] = dequant_q<DT>(&Bs[buf][bcol[j] * BREC + kb * REC], q);
-#pragma unroll
-            for (int i = 0; i < 8; i++) {
-                if (i < msub) {
-                    const half8 af = *reinterpret_cast<const half8 *>(&As[buf][(16 * i + r16) * LDA + 32 * kb + 8 * q]);
-#pragma unroll
-                    for (int j = 0; j < 2; j++)
-                        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af, bf[j], acc[i][j], 0, 0, 0);
+                    for (int t = 0; t < MT; t++) {
+                        const half8 af =
+                            *reinterpret_cast<const half8 *>(&As[buf][(32 * t + l32) * LDA + 32 * kb + 8 * q]);
+                        acc[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af, bf, acc[t], 0, 0, 0);
+                    }
                 }
             }
-        }
-        if (more) store_step(buf ^ 1);
+        };
+        // Step s (K offset kbeg + s * BK) is loaded into ring slot s % NPF,
+        // stored to LDS buffer s % 2 after step s - 1's MFMAs, computed after.
+#pragma unroll
+        for (int s = 0; s < NPF; s++) load_step(kbeg + s * BK, areg[s], braw[s]);
+        store_step(0, areg[0], braw[0]);
         __syncthreads();
-        buf ^= 1;
+        const int nsteps = (kend - kbeg) / BK;
+        // Full groups of NPF steps, none of them the last: a branch-free body,
+        // so every wait is an exact count of the younger loads.
+        const int full = nsteps > NPF ? (nsteps - 1) / NPF : 0;
+        for (int g = 0; g < full; g++) {
+#pragma unroll
+            for (int r = 0; r < NPF; r++) {
+                const int st = g * NPF + r;  // ring slot r == st % NPF
+                // refill slot r with step st + NPF: its data went to LDS at the
+                // end of step st - 1
+                // step st + 1 goes to the other LDS buffer first (its data
+                // arrived; that buffer's last readers passed the previous
+                // barrier), then the MFMAs of step st run over the stores
+                store_step((st + 1) & 1, areg[(r + 1) % NPF], braw[(r + 1) % NPF]);
+                load_step(kbeg + (st + NPF) * BK, areg[r], braw[r]);
+                compute(st & 1);
+                __syncthreads();
+            }
+        }
+        // The remaining 1..NPF steps, already loaded: full * NPF + NPF - 1 >=
+        // nsteps - 1.
+#pragma unroll
+        for (int r = 0; r < NPF; r++) {
+            const int st = full * NPF + r;
+            if (st < nsteps) {
+                if (st + 1 < nsteps) store_step((st + 1) & 1, areg[(r + 1) % NPF], braw[(r + 1) % NPF]);
+                compute(st & 1);
+                __syncthreads();
+            }
+        }
+    };
+    const int mt = (valid + 31) / 32;
+    switch (mt) {
+    case 1: run(std::integral_constant<int, 1>{}); break;
+    case 2: run(std::integral_constant<int, 2>{}); break;
+    case 3: run(std::integral_constant<int, 3>{}); break;
+    default: run(std::integral_constant<int, 4>{}); break;
     }
+    bool mlive[4];
+#pragma unroll
+    for (int t = 0; t < 4; t++) mlive[t] = t < mt;
 
-    // ---- epilogue: lane holds C[16 i + 4 q + v][bcol[j]].
+    // ---- epilogue: lane holds C[32 t + 8 (v / 4) + 4 hf + v % 4][bcol].
     if (UP) {
+        // Gate lanes (l % 32 < 16) fetch the matching up value from lane + 16.
         uint16_t *hout = ti.shared ? a.hs : a.h;
-        const int col = n0 + 16 * wv + r16;
-        if (col < W0.rows) {
+        const int col = n0 + 16 * wv + (l32 & 15);
+        const bool gl = l32 < 16 && col < W0.rows;
 #pragma unroll
-            for (int i = 0; i < 8; i++) {
-                if (i >= msub) continue;
+        for (int t = 0; t < 4; t++) {
+            if (!mlive[t]) continue;
 #pragma unroll
-                for (int v = 0; v < 4; v++) {
-                    const int d = dst_row[16 * i + 4 * q + v];
-                    if (d < 0) continue;
-                    const float g = acc[i][0][v], u = acc[i][1][v];
-                    const float hv = (g / (1.0f + __expf(-g))) * u;
-                    hout[(size_t)d * Icol + col] = __half_as_ushort(__float2half_rn(hv));
-                }
+            for (int v = 0; v < 16; v++) {
+                const float g = acc[t][v];
+                const float u = __shfl_down(g, 16, 32);
+                const int d = dst_row[32 * t + 8 * (v / 4) + 4 * hf + (v % 4)];
+                if (!gl || d < 0) continue;
+                const float hv = (g / (1.0f + __expf(-g))) * u;
+                hout[(size_t)d * Icol + col] = __half_as_ushort(__float2half_rn(hv));
             }
         }
     } else {
         float *yout = ti.shared ? a.ys : a.y;
         if (ti.ksplit) yout = ti.shared ? a.ys2 : a.y2;
+        const int col = n0 + 32 * wv + l32;
+        if (col < W0.rows) {
 #pragma unroll
-        for (int j = 0; j < 2; j++) {
-            const int col = n0 + 32 * wv + 16 * j + r16;
-            if (col >= W0.rows) continue;
+            for (int t = 0; t < 4; t++) {
+                if (!mlive[t]) continue;
 #pragma unroll
-            for (int i = 0; i < 8; i++) {
-                if (i >= msub) continue;
-#pragma unroll
-                for (int v = 0; v < 4; v++) {
-                    const int d = dst_row[16 * i + 4 * q + v];
-                    if (d >= 0) yout[(size_t)d * a.H + col] = acc[i][j][v];
+                for (int v = 0; v < 16; v++) {
+                    const int d = dst_row[32 * t + 8 * (v / 4) + 4 * hf + (v % 4)];
+                    if (d >= 0) yout[(size_t)d * a.H + col] = acc[t][v];
                 }
             }
         }

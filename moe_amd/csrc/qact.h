@@ -32,101 +32,54 @@ __device__ inline void qact_encode(float v, float inv, int &hi, int &lo) {
 }
 __device__ inline float qact_inv(float amax) { return amax > 0.0f ? 127.0f / amax : 0.0f; }
 
-// The 32 lanes of a half wave hold the values of block g of one row (lane i
-// value i): quantise them and store the block into the row's units.
-__device__ inline void qact_store_block(float v, int lane32, uint8_t *row, int g) {
-    float amax = fabsf(v);
-#pragma unroll
-    for (int m = 16; m >= 1; m >>= 1) amax = fmaxf(amax, __shfl_xor(amax, m, 32));
-    int hi, lo;
-    qact_encode(v, qact_inv(amax), hi, lo);
-    int q = 254 * hi + lo;
-#pragma unroll
-    for (int m = 16; m >= 1; m >>= 1) q += __shfl_xor(q, m, 32);
-    uint8_t *u = row + (size_t)(g >> 1) * kQUnitBytes;
-    const int half = (g & 1) * 32;
-    u[half + lane32] = (uint8_t)(int8_t)hi;
-    u[64 + half + lane32] = (uint8_t)(int8_t)lo;
-    if (lane32 == 0) {
-        reinterpret_cast<float *>(u + 128)[g & 1] = qact_s2(amax);
-        reinterpret_cast<int32_t *>(u + 136)[g & 1] = q;
-    }
-}
-
-// One thread encodes the 32 floats at src (16-byte aligned) as block
-// `half` (0 or 1) of the unit at `unit` (16-byte aligned, any address space).
-__device__ inline void qact_block_store(const float *src, uint8_t *unit, int half) {
-    float v[32];
-    const float4 *s4 = reinterpret_cast<const float4 *>(src);
-#pragma unroll
-    for (int i = 0; i < 8; i++) {
-        const float4 f = s4[i];
-        v[4 * i] = f.x, v[4 * i + 1] = f.y, v[4 * i + 2] = f.z, v[4 * i + 3] = f.w;
-    }
+// One thread encodes 32 values as block `half` (0 or 1) of a unit: the
+// unit's hi dwords, lo dwords, s2 and sq for that block.
+struct QBlock {
+    uint32_t hw[8], lw[8];
+    float s2;
+    int32_t sq;
+};
+__device__ inline QBlock qact_block(const float (&v)[32]) {
+    QBlock q;
     float amax = 0.0f;
 #pragma unroll
     for (int i = 0; i < 32; i++) amax = fmaxf(amax, fabsf(v[i]));
     const float inv = qact_inv(amax);
-    uint32_t hw[8], lw[8];
     int sq = 0;
 #pragma unroll
     for (int d = 0; d < 8; d++) {
-        hw[d] = 0, lw[d] = 0;
+        uint32_t hw = 0, lw = 0;
 #pragma unroll
         for (int j = 0; j < 4; j++) {
             int hi, lo;
             qact_encode(v[4 * d + j], inv, hi, lo);
-            hw[d] |= ((uint32_t)hi & 0xffu) << (8 * j);
-            lw[d] |= ((uint32_t)lo & 0xffu) << (8 * j);
+            hw |= ((uint32_t)hi & 0xffu) << (8 * j);
+            lw |= ((uint32_t)lo & 0xffu) << (8 * j);
             sq += 254 * hi + lo;
         }
+        q.hw[d] = hw, q.lw[d] = lw;
     }
-    uint4 *h4 = reinterpret_cast<uint4 *>(unit + 32 * half);
-    uint4 *l4 = reinterpret_cast<uint4 *>(unit + 64 + 32 * half);
-    h4[0] = make_uint4(hw[0], hw[1], hw[2], hw[3]);
-    h4[1] = make_uint4(hw[4], hw[5], hw[6], hw[7]);
-    l4[0] = make_uint4(lw[0], lw[1], lw[2], lw[3]);
-    l4[1] = make_uint4(lw[4], lw[5], lw[6], lw[7]);
-    reinterpret_cast<float *>(unit + 128)[half] = qact_s2(amax);
-    reinterpret_cast<int32_t *>(unit + 136)[half] = sq;
+    q.s2 = qact_s2(amax);
+    q.sq = sq;
+    return q;
 }
 
-// Encode the 64 floats at src (16-byte aligned) as one unit in registers,
-// laid out as the 36 dwords of the stored form.
-__device__ inline void qact_unit_from_f32(const float *src, uint32_t (&xa)[kQUnitDw]) {
-#pragma unroll
-    for (int b = 0; b < 2; b++) {
-        float v[32];
-        const float4 *s4 = reinterpret_cast<const float4 *>(src + 32 * b);
-#pragma unroll
-        for (int i = 0; i < 8; i++) {
-            const float4 f = s4[i];
-            v[4 * i] = f.x, v[4 * i + 1] = f.y, v[4 * i + 2] = f.z, v[4 * i + 3] = f.w;
-        }
-        float amax = 0.0f;
-#pragma unroll
-        for (int i = 0; i < 32; i++) amax = fmaxf(amax, fabsf(v[i]));
-        const float inv = qact_inv(amax);
-        int sq = 0;
-#pragma unroll
-        for (int d = 0; d < 8; d++) {
-            uint32_t hw = 0, lw = 0;
-#pragma unroll
-            for (int j = 0; j < 4; j++) {
-                int hi, lo;
-                qact_encode(v[4 * d + j], inv, hi, lo);
-                hw |= ((uint32_t)hi & 0xffu) << (8 * j);
-                lw |= ((uint32_t)lo & 0xffu) << (8 * j);
-                sq += 254 * hi + lo;
-            }
-            xa[8 * b + d] = hw;
-            xa[16 + 8 * b + d] = lw;
-        }
-        xa[32 + b] = __float_as_uint(qact_s2(amax));
-        xa[34 + b] = (uint32_t)sq;
-        // Keep the two blocks' loads apart: one block of floats live at a time.
-        __builtin_amdgcn_sched_barrier(0);
-    }
+// Store an encoded block into a unit (16-byte aligned) through pointers of
+// address space AS (1: global, 3: LDS).
+typedef uint32_t qa_u32x4 __attribute__((ext_vector_type(4)));
+template <int AS>
+__device__ inline void qact_block_put(const QBlock &q, uint8_t *unit, int half) {
+    typedef __attribute__((address_space(AS))) qa_u32x4 *v4p;
+    typedef __attribute__((address_space(AS))) float *fp;
+    typedef __attribute__((address_space(AS))) int32_t *ip;
+    v4p h4 = (v4p)(unit + 32 * half);
+    v4p l4 = (v4p)(unit + 64 + 32 * half);
+    h4[0] = qa_u32x4{q.hw[0], q.hw[1], q.hw[2], q.hw[3]};
+    h4[1] = qa_u32x4{q.hw[4], q.hw[5], q.hw[6], q.hw[7]};
+    l4[0] = qa_u32x4{q.lw[0], q.lw[1], q.lw[2], q.lw[3]};
+    l4[1] = qa_u32x4{q.lw[4], q.lw[5], q.lw[6], q.lw[7]};
+    ((fp)(unit + 128))[half] = q.s2;
+    ((ip)(unit + 136))[half] = q.sq;
 }
 
 }  // namespace moe

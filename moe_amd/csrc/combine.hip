@@ -37,13 +37,13 @@ __global__ __launch_bounds__(256) void combine_kernel(CombineArgs a) {
         float acc = 0.0f;
         for (int s = 0; s < k; s++) {
             float yv = a.y[(size_t)ps[s] * a.H + c];
-            if (a.y2) yv = yv + a.y2[(size_t)ps[s] * a.H + c];
+            for (int q = 1; q < a.parts; q++) yv = yv + a.y[q * a.ypart + (size_t)ps[s] * a.H + c];
             const float prod = ws[s] * yv;
             acc = acc + prod;
         }
         if (a.has_shared) {
             float v = a.ys[(size_t)t * a.H + c];
-            if (a.ys2) v = v + a.ys2[(size_t)t * a.H + c];
+            for (int q = 1; q < a.parts; q++) v = v + a.ys[q * a.yspart + (size_t)t * a.H + c];
             if (a.shgate) v = v * g;
             acc = acc + v;
         }

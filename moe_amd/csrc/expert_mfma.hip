@@ -34,7 +34,7 @@ typedef uint32_t u32x4a __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2a __attribute__((ext_vector_type(2)));
 
 constexpr int BM = 128;        // tokens per tile
-constexpr int BN = 128;        // output columns per tile
+constexpr int BW = 256;        // weight rows per tile (up: 128 gate + 128 up rows)
 constexpr int BK = 64;         // K values per step (two 32-value blocks)
 constexpr int LDA = BK + 8;    // A row stride in halves (144 bytes)
 
@@ -104,24 +104,49 @@ __device__ inline void normalise(const uint32_t (&d)[Fmt<DT>::fetch], bool odd, 
 
 // Lane group q's eight values of a block record, as one MFMA operand:
 // slots 0..3 = elements 4q..4q+3, slots 4..7 = elements 16+4q..16+4q+3.
+// rec_codes reads the record dwords that hold them; dequant_codes turns them
+// into f16 (d * q rounded once).
 template <int DT>
-__device__ inline half8 dequant_q(const uint32_t *rec, int q) {
-    const __half2 d2 = as_h2((rec[0] & 0xffffu) * 0x10001u);
+struct Codes;
+template <>
+struct Codes<MOE_DT_Q4_0> {
+    static constexpr int n = 1;  // the code dword
+};
+template <>
+struct Codes<MOE_DT_Q5_0> {
+    static constexpr int n = 2;  // high-bit dword, code dword
+};
+template <>
+struct Codes<MOE_DT_Q8_0> {
+    static constexpr int n = 2;  // low-half and high-half code dwords
+};
+template <int DT>
+__device__ inline void rec_codes(const uint32_t *rec, int q, uint32_t (&c)[Codes<DT>::n]) {
+    if constexpr (DT == MOE_DT_Q4_0) {
+        c[0] = rec[1 + q];
+    } else if constexpr (DT == MOE_DT_Q5_0) {
+        c[0] = rec[1], c[1] = rec[2 + q];
+    } else {
+        c[0] = rec[1 + q], c[1] = rec[5 + q];
+    }
+}
+template <int DT>
+__device__ inline half8 dequant_codes(uint32_t scale, const uint32_t (&c)[Codes<DT>::n], int q) {
+    const __half2 d2 = as_h2((scale & 0xffffu) * 0x10001u);
     uint32_t o[4];
     if constexpr (DT == MOE_DT_Q4_0) {
-        const uint32_t c = rec[1 + q];
         const __half2 off2 = __floats2half2_rn(1032.0f, 1032.0f);
-        codes4(c & 0x0f0f0f0fu, off2, d2, o[0], o[1]);
-        codes4((c >> 4) & 0x0f0f0f0fu, off2, d2, o[2], o[3]);
+        codes4(c[0] & 0x0f0f0f0fu, off2, d2, o[0], o[1]);
+        codes4((c[0] >> 4) & 0x0f0f0f0fu, off2, d2, o[2], o[3]);
     } else if constexpr (DT == MOE_DT_Q5_0) {
-        const uint32_t hb = rec[1], c = rec[2 + q];
+        const uint32_t hb = c[0];
         const __half2 off2 = __floats2half2_rn(1040.0f, 1040.0f);
-        codes4((c & 0x0f0f0f0fu) | spread4((hb >> (4 * q)) & 0xfu), off2, d2, o[0], o[1]);
-        codes4(((c >> 4) & 0x0f0f0f0fu) | spread4((hb >> (16 + 4 * q)) & 0xfu), off2, d2, o[2], o[3]);
+        codes4((c[1] & 0x0f0f0f0fu) | spread4((hb >> (4 * q)) & 0xfu), off2, d2, o[0], o[1]);
+        codes4(((c[1] >> 4) & 0x0f0f0f0fu) | spread4((hb >> (16 + 4 * q)) & 0xfu), off2, d2, o[2], o[3]);
     } else {  // Q8_0: int8 codes, read as uint8 + 128
         const __half2 off2 = __floats2half2_rn(1152.0f, 1152.0f);
-        codes4(rec[1 + q] ^ 0x80808080u, off2, d2, o[0], o[1]);
-        codes4(rec[5 + q] ^ 0x80808080u, off2, d2, o[2], o[3]);
+        codes4(c[0] ^ 0x80808080u, off2, d2, o[0], o[1]);
+        codes4(c[1] ^ 0x80808080u, off2, d2, o[2], o[3]);
     }
     half8 r;
     __builtin_memcpy(&r, o, 16);
@@ -129,10 +154,11 @@ __device__ inline half8 dequant_q(const uint32_t *rec, int q) {
 }
 
 // Tile coordinates.  mode 0: routed tiles from the dispatch list; mode 1: the
-// shared expert over all T tokens.  Blocks are remapped so that each XCD
-// (linear block id mod 8) walks a contiguous range of tiles, M fastest: the
-// M-tiles of one expert that share a weight tile run together on one XCD and
-// meet that tile in its L2.
+// shared expert over all T tokens.  The grid is walked in the order
+// (expert, N tile, M tile), M fastest, and each XCD (linear block id mod 8)
+// takes a contiguous range of that order: an expert's weight tile is read
+// from HBM once and met in L2 by the expert's other M tiles, and the
+// expert's activations stay in that XCD's L2 while its N tiles go by.
 struct TileInfo {
     int g, m0, n, row0, ntile, ksplit;
     bool shared;
@@ -141,20 +167,32 @@ __device__ inline bool tile_of(const MfmaArgs &a, int mode, int gx, TileInfo &ti
     const int gy = gridDim.y, gz = gridDim.z;
     const int total = gx * gy;
     const int lin = blockIdx.x + gx * blockIdx.y;
-    // XCD remap (only when the grid divides evenly).
-    int t = lin;
-    if ((total & 7) == 0) t = (lin & 7) * (total >> 3) + (lin >> 3);
-    const int tx = t % gx, ty = t / gx;
-    ti.ntile = ty;
     ti.ksplit = gz > 1 ? (int)blockIdx.z : 0;
-    if (mode == 1) {
-        ti.g = a.E, ti.m0 = tx * BM, ti.n = a.T, ti.row0 = 0, ti.shared = true;
-        return ti.m0 < a.T;
+    const int mt_sh = (a.T + BM - 1) / BM;
+    const int valid = mode == 1 ? mt_sh * gy : a.ntiles[0] * gy;  // <= total
+    // XCD x (= lin mod 8) takes t in [x * per, (x + 1) * per) in order.
+    int t = lin;
+    if ((total & 7) == 0) {
+        const int per = (valid + 7) >> 3;
+        const int j = lin >> 3;
+        if (j >= per) return false;
+        t = (lin & 7) * per + j;
     }
-    if (tx >= a.ntiles[0]) return false;
-    const int g = a.tiles[2 * tx];
+    if (t >= valid) return false;
+    if (mode == 1) {
+        ti.ntile = t / mt_sh;
+        ti.g = a.E, ti.m0 = (t % mt_sh) * BM, ti.n = a.T, ti.row0 = 0, ti.shared = true;
+        return true;
+    }
+    // Tiles of one group are contiguous: t / gy lies inside t's group.
+    const int ie = t / gy;
+    const int f = a.tiles[4 * ie + 2], mt = a.tiles[4 * ie + 3];
+    const int local = t - f * gy;
+    const int i = f + local % mt;
+    ti.ntile = local / mt;
+    const int g = a.tiles[4 * i];
     if (g >= a.E) return false;
-    ti.g = g, ti.m0 = a.tiles[2 * tx + 1], ti.n = a.counts[g], ti.row0 = a.offsets[g], ti.shared = false;
+    ti.g = g, ti.m0 = a.tiles[4 * i + 1], ti.n = a.counts[g], ti.row0 = a.offsets[g], ti.shared = false;
     return true;
 }
 
@@ -163,7 +201,7 @@ __global__ __launch_bounds__(256, 2) void mfma_kernel(MfmaArgs a, int mode, int 
     constexpr int REC = Fmt<DT>::rec;
     constexpr int BREC = 2 * REC + 1;  // dwords per weight row per step (+1 spreads banks)
     __shared__ __attribute__((aligned(16))) _Float16 As[2][BM * LDA];
-    __shared__ __attribute__((aligned(16))) uint32_t Bs[2][BN * BREC];
+    __shared__ __attribute__((aligned(16))) uint32_t Bs[2][BW * BREC];
     __shared__ int src_row[BM];
     __shared__ int dst_row[BM];
 
@@ -172,7 +210,7 @@ __global__ __launch_bounds__(256, 2) void mfma_kernel(MfmaArgs a, int mode, int 
     const ExpertDev &ex = a.experts[ti.g];
     const MatDev &W0 = UP ? ex.m[0] : ex.m[2];
     const MatDev &W1 = UP ? ex.m[1] : ex.m[2];
-    const int n0 = ti.ntile * (UP ? BN / 2 : BN);
+    const int n0 = ti.ntile * (UP ? BW / 2 : BW);  // first gate row (up) or output column (down)
     if (n0 >= W0.rows) return;
     const int Ktot = W0.cols;
     const int kspan = Ktot / ksplit;  // a multiple of BK (checked on the host)
@@ -192,40 +230,40 @@ __global__ __launch_bounds__(256, 2) void mfma_kernel(MfmaArgs a, int mode, int 
     }
     __syncthreads();
 
-    // ---- load assignments: thread -> A row am, 32-value block ah of the step;
-    //      weight row bn (tile column), block bb of the step.
-    // Every thread issues the same loads on every step (rows past the end
-    // read row 0 and are zeroed when stored), so each wait for a step's data
-    // is an exact count of the loads issued after it.
+    // ---- staging: thread -> A row am, 32-value block ab of the step; weight
+    //      row bn (LDS row; up: gate rows 0..127, up rows 128..255), both
+    //      blocks of the step.  Every thread issues the same loads on every
+    //      step (rows past the end read row 0 and are zeroed when stored), so
+    //      each wait for a step's data counts exactly the loads after it.
     const int am = tid >> 1, ab = tid & 1;
     const int arow = src_row[am];
     const bool avalid = arow >= 0;
     const uint16_t *abase = UP ? a.xh + (size_t)(avalid ? arow : src_row[0]) * a.H
                                : (ti.shared ? a.hs : a.h) + (size_t)(avalid ? arow : src_row[0]) * Icol;
-    const int bn = tid >> 1, bb = tid & 1;
-    const MatDev &BW = (UP && bn >= BN / 2) ? W1 : W0;
-    const int brow = UP ? n0 + (bn & (BN / 2 - 1)) : n0 + bn;
-    const bool bvalid = brow < BW.rows;
-    const uint8_t *browp = BW.ptr + (size_t)(bvalid ? brow : 0) * BW.stride;
+    const int bn = tid;
+    const MatDev &WB = (UP && bn >= BW / 2) ? W1 : W0;
+    const int brow = UP ? n0 + (bn & (BW / 2 - 1)) : n0 + bn;
+    const bool bvalid = brow < WB.rows;
+    const uint8_t *browp = WB.ptr + (size_t)(bvalid ? brow : 0) * WB.stride;
 
-    // Global loads run NPF steps ahead of the MFMAs through a register ring
-    // of raw dwords; they are normalised when stored to LDS (double
-    // buffered), so nothing waits for a load until its step is stored.
-    constexpr int NPF = 3;
+    // Global loads are held as raw dwords and normalised when stored to LDS.
     constexpr int FD = Fmt<DT>::fetch;
-    u32x4a areg[NPF][4];
-    uint32_t braw[NPF][FD];
-    const bool bodd = (bb & 1) != 0;  // block k0 / 32 + bb, with k0 / 32 even
-    auto load_step = [&](int k0, u32x4a (&ar)[4], uint32_t (&br)[FD]) {
+    constexpr int FQ = Codes<DT>::n;
+    u32x4a areg[4];
+    uint32_t braw[2][FD];
+    auto load_step = [&](int k0, u32x4a (&ar)[4], uint32_t (&br)[2][FD]) {
         const int kc = k0 < kend ? k0 : kbeg;  // past the end: a harmless reload
         const u32x4a *src = reinterpret_cast<const u32x4a *>(abase + kc + 32 * ab);
 #pragma unroll
         for (int i = 0; i < 4; i++) ar[i] = gload(src + i);
-        fetch_raw<DT>(browp, kc / 32 + bb, br);
+#pragma unroll
+        for (int bb = 0; bb < 2; bb++) fetch_raw<DT>(browp, kc / 32 + bb, br[bb]);
     };
     // Chunk c of a 32-value block holds elements 8c..8c+7; its two halves go
-    // to the K-permuted slots 16 (c & 1) + 4 (c >> 1) and that + 8.
-    auto store_step = [&](int buf, const u32x4a (&ar)[4], const uint32_t (&br)[FD]) {
+    // to the K-permuted slots 16 (c & 1) + 4 (c >> 1) and that + 8.  Block bb
+    // of a step has parity bb (k0 / 32 is even), so it starts 2 bytes into
+    // its first dword exactly when bb == 1.
+    auto store_step = [&](int buf, const u32x4a (&ar)[4], const uint32_t (&br)[2][FD]) {
         _Float16 *arow_lds = &As[buf][am * LDA + 32 * ab];
 #pragma unroll
         for (int c = 0; c < 4; c++) {
@@ -234,84 +272,86 @@ __global__ __launch_bounds__(256, 2) void mfma_kernel(MfmaArgs a, int mode, int 
             *reinterpret_cast<u32x2a *>(arow_lds + p0) = u32x2a{v.x, v.y};
             *reinterpret_cast<u32x2a *>(arow_lds + p0 + 8) = u32x2a{v.z, v.w};
         }
-        uint32_t rec[REC];
-        normalise<DT>(br, bodd, rec);
-        if (!bvalid) rec[0] = 0u;  // scale 0: a zero weight row
-        uint32_t *brow_lds = &Bs[buf][bn * BREC + bb * REC];
 #pragma unroll
-        for (int i = 0; i < REC; i++) brow_lds[i] = rec[i];
+        for (int bb = 0; bb < 2; bb++) {
+            uint32_t rec[REC];
+            normalise<DT>(br[bb], bb == 1, rec);
+            if (!bvalid) rec[0] = 0u;  // scale 0: a zero weight row
+            uint32_t *brow_lds = &Bs[buf][bn * BREC + bb * REC];
+#pragma unroll
+            for (int i = 0; i < REC; i++) brow_lds[i] = rec[i];
+        }
     };
 
-    // Wave wv owns all 128 tokens and one 32-column tile: up -> lanes with
-    // l % 32 < 16 take gate rows 16 wv .. +16 and the others the same up rows
-    // (tile rows 64 + ...); down -> columns 32 wv .. +32.  Each
-    // V_MFMA_F32_32X32X16_F16 takes A lane l = row l % 32, K slots
-    // 8 (l / 32) .. +8 and B lane l = column l % 32, the same K slots; D lane l
-    // element v = row 8 (v / 4) + 4 (l / 32) + v % 4, column l % 32.  Within a
-    // 32-value block, MFMA m covers permuted slots 16 m .. 16 m + 15, so lane
-    // half h reads slot group q = 2 m + h: the eight codes of dword q.  A
-    // dequantised B fragment feeds the 32-token MFMAs of the tile's live rows.
-    floatx16 acc[4];
+    // Wave wv owns all 128 tokens and two 32-column tiles j: up -> gate rows
+    // 32 wv .. +32 (j = 0) and the same up rows (j = 1); down -> output
+    // columns 64 wv + 32 j .. +32.  Each V_MFMA_F32_32X32X16_F16 takes A lane
+    // l = row l % 32, K slots 8 (l / 32) .. +8 and B lane l = column l % 32,
+    // the same K slots; D lane l element v = row 8 (v / 4) + 4 (l / 32) + v % 4,
+    // column l % 32.  Within a 32-value block, MFMA m covers permuted slots
+    // 16 m .. 16 m + 15, so lane half h reads slot group q = 2 m + h: the
+    // eight codes of dword q.  An activation fragment feeds two MFMAs (j), a
+    // dequantised weight fragment the MT 32-token tiles.
+    floatx16 acc[4][2];
 #pragma unroll
-    for (int t = 0; t < 4; t++) acc[t] = floatx16{};
+    for (int t = 0; t < 4; t++)
+#pragma unroll
+        for (int j = 0; j < 2; j++) acc[t][j] = floatx16{};
     const int l32 = lane & 31, hf = lane >> 5;
-    const int bcol = UP ? ((l32 < 16 ? 0 : 64) + 16 * wv + (l32 & 15)) : (32 * wv + l32);
+    int bcol[2];
+#pragma unroll
+    for (int j = 0; j < 2; j++) bcol[j] = UP ? (128 * j + 32 * wv + l32) : (64 * wv + 32 * j + l32);
 
     // The K loop for MT live 32-token tiles (chosen once per block).
     auto run = [&](auto mt_c) {
         constexpr int MT = decltype(mt_c)::value;
+        // A step is four fragment groups g = (kb, m): group g + 1's
+        // activation fragments and weight codes are read from LDS while group
+        // g's MFMAs run.
         auto compute = [&](int buf) {
+            half8 af[2][MT];
+            uint32_t bsc[2][2], bq[2][2][FQ];
+            auto read_group = [&](int g, half8 (&A)[MT], uint32_t (&sc)[2], uint32_t (&bqv)[2][FQ]) {
+                const int kb = g >> 1, q = 2 * (g & 1) + hf;
 #pragma unroll
-            for (int kb = 0; kb < 2; kb++) {
+                for (int t = 0; t < MT; t++)
+                    A[t] = *reinterpret_cast<const half8 *>(&As[buf][(32 * t + l32) * LDA + 32 * kb + 8 * q]);
 #pragma unroll
-                for (int m = 0; m < 2; m++) {
-                    const int q = 2 * m + hf;
-                    const half8 bf = dequant_q<DT>(&Bs[buf][bcol * BREC + kb * REC], q);
+                for (int j = 0; j < 2; j++) {
+                    const uint32_t *rec = &Bs[buf][bcol[j] * BREC + kb * REC];
+                    sc[j] = rec[0];
+                    rec_codes<DT>(rec, q, bqv[j]);
+                }
+            };
+            read_group(0, af[0], bsc[0], bq[0]);
 #pragma unroll
-                    for (int t = 0; t < MT; t++) {
-                        const half8 af =
-                            *reinterpret_cast<const half8 *>(&As[buf][(32 * t + l32) * LDA + 32 * kb + 8 * q]);
-                        acc[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af, bf, acc[t], 0, 0, 0);
-                    }
+            for (int g = 0; g < 4; g++) {
+                const int c = g & 1;
+                if (g + 1 < 4) read_group(g + 1, af[c ^ 1], bsc[c ^ 1], bq[c ^ 1]);
+                // keep those reads ahead of this group's MFMAs
+                __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+                for (int j = 0; j < 2; j++) {
+                    const half8 bf = dequant_codes<DT>(bsc[c][j], bq[c][j], 2 * (g & 1) + hf);
+#pragma unroll
+                    for (int t = 0; t < MT; t++)
+                        acc[t][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[c][t], bf, acc[t][j], 0, 0, 0);
                 }
             }
         };
-        // Step s (K offset kbeg + s * BK) is loaded into ring slot s % NPF,
-        // stored to LDS buffer s % 2 after step s - 1's MFMAs, computed after.
-#pragma unroll
-        for (int s = 0; s < NPF; s++) load_step(kbeg + s * BK, areg[s], braw[s]);
-        store_step(0, areg[0], braw[0]);
+        // Double buffering: step s + 1's loads are issued before step s's
+        // MFMAs and stored to the other LDS buffer after them.
+        load_step(kbeg, areg, braw);
+        store_step(0, areg, braw);
         __syncthreads();
         const int nsteps = (kend - kbeg) / BK;
-        // Full groups of NPF steps, none of them the last: a branch-free body,
-        // so every wait is an exact count of the younger loads.
-        const int full = nsteps > NPF ? (nsteps - 1) / NPF : 0;
-        for (int g = 0; g < full; g++) {
-#pragma unroll
-            for (int r = 0; r < NPF; r++) {
-                const int st = g * NPF + r;  // ring slot r == st % NPF
-                // refill slot r with step st + NPF: its data went to LDS at the
-                // end of step st - 1
-                // step st + 1 goes to the other LDS buffer first (its data
-                // arrived; that buffer's last readers passed the previous
-                // barrier), then the MFMAs of step st run over the stores
-                store_step((st + 1) & 1, areg[(r + 1) % NPF], braw[(r + 1) % NPF]);
-                load_step(kbeg + (st + NPF) * BK, areg[r], braw[r]);
-                compute(st & 1);
-                __syncthreads();
-            }
+        for (int st = 0; st + 1 < nsteps; st++) {
+            load_step(kbeg + (st + 1) * BK, areg, braw);
+            compute(st & 1);
+            store_step((st + 1) & 1, areg, braw);
+            __syncthreads();
         }
-        // The remaining 1..NPF steps, already loaded: full * NPF + NPF - 1 >=
-        // nsteps - 1.
-#pragma unroll
-        for (int r = 0; r < NPF; r++) {
-            const int st = full * NPF + r;
-            if (st < nsteps) {
-                if (st + 1 < nsteps) store_step((st + 1) & 1, areg[(r + 1) % NPF], braw[(r + 1) % NPF]);
-                compute(st & 1);
-                __syncthreads();
-            }
-        }
+        compute((nsteps - 1) & 1);
     };
     const int mt = (valid + 31) / 32;
     switch (mt) {
@@ -320,41 +360,38 @@ __global__ __launch_bounds__(256, 2) void mfma_kernel(MfmaArgs a, int mode, int 
     case 3: run(std::integral_constant<int, 3>{}); break;
     default: run(std::integral_constant<int, 4>{}); break;
     }
-    bool mlive[4];
-#pragma unroll
-    for (int t = 0; t < 4; t++) mlive[t] = t < mt;
 
-    // ---- epilogue: lane holds C[32 t + 8 (v / 4) + 4 hf + v % 4][bcol].
+    // ---- epilogue: lane holds C[32 t + 8 (v / 4) + 4 hf + v % 4][bcol[j]].
     if (UP) {
-        // Gate lanes (l % 32 < 16) fetch the matching up value from lane + 16.
         uint16_t *hout = ti.shared ? a.hs : a.h;
-        const int col = n0 + 16 * wv + (l32 & 15);
-        const bool gl = l32 < 16 && col < W0.rows;
-#pragma unroll
-        for (int t = 0; t < 4; t++) {
-            if (!mlive[t]) continue;
-#pragma unroll
-            for (int v = 0; v < 16; v++) {
-                const float g = acc[t][v];
-                const float u = __shfl_down(g, 16, 32);
-                const int d = dst_row[32 * t + 8 * (v / 4) + 4 * hf + (v % 4)];
-                if (!gl || d < 0) continue;
-                const float hv = (g / (1.0f + __expf(-g))) * u;
-                hout[(size_t)d * Icol + col] = __half_as_ushort(__float2half_rn(hv));
-            }
-        }
-    } else {
-        float *yout = ti.shared ? a.ys : a.y;
-        if (ti.ksplit) yout = ti.shared ? a.ys2 : a.y2;
         const int col = n0 + 32 * wv + l32;
         if (col < W0.rows) {
 #pragma unroll
             for (int t = 0; t < 4; t++) {
-                if (!mlive[t]) continue;
+                if (t >= mt) continue;
 #pragma unroll
                 for (int v = 0; v < 16; v++) {
                     const int d = dst_row[32 * t + 8 * (v / 4) + 4 * hf + (v % 4)];
-                    if (d >= 0) yout[(size_t)d * a.H + col] = acc[t][v];
+                    if (d < 0) continue;
+                    const float g = acc[t][0][v], u = acc[t][1][v];
+                    const float hv = (g / (1.0f + __expf(-g))) * u;
+                    hout[(size_t)d * Icol + col] = __half_as_ushort(__float2half_rn(hv));
+                }
+            }
+        }
+    } else {
+        float *yout = ti.shared ? a.ys + ti.ksplit * a.yspart : a.y + ti.ksplit * a.ypart;
+#pragma unroll
+        for (int j = 0; j < 2; j++) {
+            const int col = n0 + 64 * wv + 32 * j + l32;
+            if (col >= W0.rows) continue;
+#pragma unroll
+            for (int t = 0; t < 4; t++) {
+                if (t >= mt) continue;
+#pragma unroll
+                for (int v = 0; v < 16; v++) {
+                    const int d = dst_row[32 * t + 8 * (v / 4) + 4 * hf + (v % 4)];
+                    if (d >= 0) yout[(size_t)d * a.H + col] = acc[t][j][v];
                 }
             }
         }
@@ -379,16 +416,20 @@ int mfma_tile_m() { return BM; }
 
 bool mfma_format_ok(int dt) { return dt == MOE_DT_Q4_0 || dt == MOE_DT_Q5_0 || dt == MOE_DT_Q8_0; }
 
-// Split K of the down projection in two when its grid would leave CUs idle.
-int mfma_down_ksplit(int m_tiles, int n_rows, int K) {
-    const long long blocks = (long long)m_tiles * ((n_rows + BN - 1) / BN);
-    return (blocks < 512 && K % (2 * BK) == 0) ? 2 : 1;
+// Split K of the down projection (2 or 4 parts) when its grid would leave
+// CUs idle: the fewest parts that give about two blocks per CU.
+int mfma_down_ksplit(int m_tiles, int n_rows, int K, int K_shared) {
+    const long long blocks = (long long)m_tiles * ((n_rows + BW - 1) / BW);
+    int ks = 1;
+    while (ks < kMaxKSplit && blocks * ks < 512) ks *= 2;
+    while (ks > 1 && (K % (ks * BK) != 0 || (K_shared > 0 && K_shared % (ks * BK) != 0))) ks /= 2;
+    return ks;
 }
 
 hipError_t launch_mfma(bool up, const MfmaArgs &a, int /*bm*/, const ExpertDev &e0, const ExpertDev *sh,
                        hipStream_t s) {
     const MatDev &m = up ? e0.m[0] : e0.m[2];
-    const int cols = up ? BN / 2 : BN;
+    const int cols = up ? BW / 2 : BW;
     const int ks = up ? 1 : a.ksplit;
     dim3 grid(a.max_tiles, (m.rows + cols - 1) / cols, ks);
     hipError_t err = up ? launch_dt<true>(m.dt, grid, a, 0, ks, s) : launch_dt<false>(m.dt, grid, a, 0, ks, s);

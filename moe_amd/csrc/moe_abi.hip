@@ -191,6 +191,11 @@ int reserve(moe_layer *L, int max_t, int k) {
     };
     Workspace w;
     w.max_t = max_t;
+    // Room for the K parts of a split MFMA down projection.  Splitting only
+    // pays for small grids, so parts after the first are bounded in rows.
+    const size_t extra = L->mfma_ok ? (kMaxKSplit - 1) * std::min<size_t>(T * k, 8192) : 0;
+    w.y_rows = T * k + extra;
+    w.ys_rows = T + extra;
     Item items[] = {
         {(void **)&w.logits, T * (E + 1) * 4},
         {(void **)&w.sel, T * k * 4},
@@ -202,7 +207,7 @@ int reserve(moe_layer *L, int max_t, int k) {
         {(void **)&w.perm_w, T * k * 4},
         {(void **)&w.pos, T * k * 4},
         {(void **)&w.hits, (E + 2) * 4},
-        {(void **)&w.tiles, 2 * max_tiles * 4},
+        {(void **)&w.tiles, 4 * max_tiles * 4},
         {(void **)&w.dtasks, (size_t)(k + 1) * sizeof(DecodeTask)},
         {(void **)&w.hq, ((size_t)k * (I / 64) + Is / 64 + 1) * kQUnitBytes},
         {(void **)&w.route_count, 4},
@@ -210,10 +215,8 @@ int reserve(moe_layer *L, int max_t, int k) {
         {(void **)&w.xh, T * H * 2},
         {(void **)&w.h, T * k * I * 4},
         {(void **)&w.hs, T * Is * 4},
-        {(void **)&w.y, T * k * H * 4},
-        {(void **)&w.ys, T * H * 4},
-        {(void **)&w.y2, T * k * H * 4},
-        {(void **)&w.ys2, T * H * 4},
+        {(void **)&w.y, w.y_rows * H * 4},
+        {(void **)&w.ys, w.ys_rows * H * 4},
         {(void **)&w.stats, 4 * 8},
     };
     size_t total = 0;
@@ -668,10 +671,12 @@ int moe_layer_forward(moe_layer *L, const float *x, int32_t t, float *out, float
         m.I_s = L->I_s;
         m.E = L->E;
         m.max_tiles = t * k / bm + std::min(L->E, t * k) + 1;
-        m.y2 = w.y2;
-        m.ys2 = w.ys2;
-        m.ksplit = mfma_down_ksplit((t * k + bm - 1) / bm + std::min(L->E, t * k) / 2, L->H, L->I);
-        if (L->has_shared && m.ksplit == 2 && L->I_s % 128 != 0) m.ksplit = 1;
+        m.ypart = (size_t)t * k * L->H;
+        m.yspart = (size_t)t * L->H;
+        m.ksplit = mfma_down_ksplit((t * k + bm - 1) / bm + std::min(L->E, t * k) / 2, L->H, L->I,
+                                    L->has_shared ? L->I_s : 0);
+        while (m.ksplit > 1 && ((size_t)m.ksplit * t * k > w.y_rows || (size_t)m.ksplit * t > w.ys_rows))
+            m.ksplit /= 2;
         ksplit = m.ksplit;
         rc = stage(L, 3, s, [&] {
             if ((e = launch_to_f16(x, w.xh, (size_t)t * L->H, s)) != hipSuccess) return hip_fail(e, "f16 conversion");
@@ -726,8 +731,9 @@ int moe_layer_forward(moe_layer *L, const float *x, int32_t t, float *out, float
     CombineArgs c{};
     c.y = w.y;
     c.ys = w.ys;
-    c.y2 = ksplit == 2 ? w.y2 : nullptr;
-    c.ys2 = ksplit == 2 ? w.ys2 : nullptr;
+    c.parts = ksplit;
+    c.ypart = (size_t)t * k * L->H;
+    c.yspart = (size_t)t * L->H;
     c.pos = w.pos;
     c.sel = w.sel;
     c.wsel = w.wsel;

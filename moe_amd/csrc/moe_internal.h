@@ -82,7 +82,7 @@ struct Workspace {
     float *perm_w = nullptr;      // [T*k]
     int32_t *pos = nullptr;       // [T*k] permuted row of (t, slot)
     int32_t *hits = nullptr;      // [E+2] n, then experts ascending
-    int32_t *tiles = nullptr;     // [2 * max_tiles] (group, m0) pairs for the MFMA path
+    int32_t *tiles = nullptr;     // [4 * max_tiles] (group, m0, group's first tile, group's tiles) for the MFMA path
     DecodeTask *dtasks = nullptr; // [k + 1] one-token task table
     uint8_t *hq = nullptr;        // [k * I / 64 + I_s / 64] units of h (one-token path)
     unsigned *route_count = nullptr;  // [1] finished router blocks (one-token route), zero between calls
@@ -90,10 +90,9 @@ struct Workspace {
     uint16_t *xh = nullptr;       // [T, H] f16 activations (MFMA path)
     float *h = nullptr;           // [T*k, I] routed SwiGLU activations (f32, or f16 on the MFMA path)
     float *hs = nullptr;          // [T, I_s] shared-expert activations
-    float *y = nullptr;           // [T*k, H] routed expert outputs
-    float *ys = nullptr;          // [T, H] shared-expert outputs
-    float *y2 = nullptr;          // second K half of y (split down projection)
-    float *ys2 = nullptr;         // second K half of ys
+    float *y = nullptr;           // [parts][T*k, H] routed expert outputs (parts: split K of the down projection)
+    float *ys = nullptr;          // [parts][T, H] shared-expert outputs
+    size_t y_rows = 0, ys_rows = 0;  // rows y and ys have room for
     unsigned long long *stats = nullptr;  // [4] fallback when the caller passes none
     void *base = nullptr;         // single allocation backing all of the above
     size_t bytes = 0;
@@ -204,14 +203,15 @@ struct MfmaArgs {
     const uint16_t *xh;           // [T, H] f16
     uint16_t *h, *hs;             // f16 [T*k, I], [T, I_s]
     float *y, *ys;                // f32 [T*k, H], [T, H]
-    float *y2, *ys2;              // second K half of the down projection (ksplit == 2)
+    size_t ypart, yspart;         // elements between the K parts of y, ys
     int T, H, I, I_s, E;
     int max_tiles;
-    int ksplit;                   // down projection: 1, or 2 halves of K
+    int ksplit;                   // down projection: K parts (1, 2 or 4), part p written at y + p * ypart
 };
 int mfma_tile_m();
 bool mfma_format_ok(int dt);
-int mfma_down_ksplit(int m_tiles, int n_rows, int K);
+constexpr int kMaxKSplit = 4;
+int mfma_down_ksplit(int m_tiles, int n_rows, int K, int K_shared);
 // up: gate/up + SwiGLU; down: down projection.  Routed tiles come from the
 // dispatch list; the shared expert (sh != null) gets its own launch.
 hipError_t launch_mfma(bool up, const MfmaArgs &a, int bm, const ExpertDev &e0, const ExpertDev *sh, hipStream_t s);
@@ -220,7 +220,8 @@ hipError_t launch_mfma(bool up, const MfmaArgs &a, int bm, const ExpertDev &e0, 
 // (src/model.rs:936-942, 956-970, 680-683).
 struct CombineArgs {
     const float *y, *ys;
-    const float *y2, *ys2;        // or null: second K half, added before weighting
+    int parts;                    // K parts of y and ys, summed in order before weighting
+    size_t ypart, yspart;         // elements between parts
     const int32_t *pos;
     const int32_t *sel;
     const float *wsel;

@@ -582,16 +582,20 @@ __device__ void dispatch_block(const DispatchArgs &a) {
         int tt;
         const int tb = block_scan_excl(nt, wave_sums, &tt);
         for (int i = 0; i < nt; i++) {
-            a.tiles[2 * (tb + i)] = e;
-            a.tiles[2 * (tb + i) + 1] = i * a.bm;
+            a.tiles[4 * (tb + i)] = e;
+            a.tiles[4 * (tb + i) + 1] = i * a.bm;
+            a.tiles[4 * (tb + i) + 2] = tb;
+            a.tiles[4 * (tb + i) + 3] = nt;
         }
         if (tid == 0) {
             int ntot = tt;
             if (a.has_shared) {
                 const int ns = (T + a.bm - 1) / a.bm;
                 for (int i = 0; i < ns; i++) {
-                    a.tiles[2 * (tt + i)] = E;
-                    a.tiles[2 * (tt + i) + 1] = i * a.bm;
+                    a.tiles[4 * (tt + i)] = E;
+                    a.tiles[4 * (tt + i) + 1] = i * a.bm;
+                    a.tiles[4 * (tt + i) + 2] = tt;
+                    a.tiles[4 * (tt + i) + 3] = ns;
                 }
                 ntot += ns;
             }
@@ -679,8 +683,10 @@ __device__ void dispatch_one(const DispatchArgs &a, const int *idx, const float 
                 reused += in_prev ? 1ull : 0ull;
             }
             if (a.bm > 0) {
-                a.tiles[2 * o] = e;
-                a.tiles[2 * o + 1] = 0;
+                a.tiles[4 * o] = e;
+                a.tiles[4 * o + 1] = 0;
+                a.tiles[4 * o + 2] = o;
+                a.tiles[4 * o + 3] = 1;
             }
             if (a.dtasks && o < a.dk_bound) {
                 DecodeTask d{};
@@ -723,8 +729,10 @@ __device__ void dispatch_one(const DispatchArgs &a, const int *idx, const float 
         if (a.bm > 0) {
             int nt = nsel;
             if (a.has_shared) {
-                a.tiles[2 * nt] = E;
-                a.tiles[2 * nt + 1] = 0;
+                a.tiles[4 * nt] = E;
+                a.tiles[4 * nt + 1] = 0;
+                a.tiles[4 * nt + 2] = nt;
+                a.tiles[4 * nt + 3] = 1;
                 nt++;
             }
             a.ntiles[0] = nt;

@@ -1,21 +1,32 @@
 // expert_mfma.hip — grouped SwiGLU expert GEMMs on gfx950 matrix cores.
 //
-// One block computes a 128-token x 128-column tile of one expert:
-//   up   : 64 gate rows and the same 64 up rows of the expert, K = H; the
+// One block computes a tile of up to 256 tokens x 256 weight rows of one
+// expert:
+//   up   : 128 gate rows and the same 128 up rows of the expert, K = H; the
 //          epilogue forms h = silu(G) * U and stores it as f16.
-//   down : 128 rows of W_down, K = I (optionally split in two halves, each
-//          half writing its own output buffer); output y in f32.
-// Four waves each own all 128 tokens x 32 columns, so every weight value is
-// dequantised exactly once per block and goes straight into MFMA operand
-// registers: raw weight blocks are staged in LDS (one 4-byte-aligned record
-// per 32-value block: scale dword, then code dwords) and each lane turns its
-// eight codes of a block into f16 (d * q rounded once).  Activations are
-// staged in LDS with K permuted inside each 32-value block so that a lane's
-// eight K positions are {4q..4q+3, 16+4q..16+4q+3}, the values whose codes
-// share one dword of a Q4_0/Q5_0 block.  Both LDS stages are double
-// buffered; the next K step's global loads are issued before the current
-// step's MFMAs (V_MFMA_F32_16X16X32_F16, f32 accumulation).  16-row
-// sub-tiles past the expert's last token are skipped.
+//   down : 256 rows of W_down, K = I (optionally split into 2 or 4 K parts,
+//          each written to its own part of y); output y in f32.
+// Four waves, one per SIMD.  Wave w owns every token row of the tile and 64
+// weight rows, so each weight value is dequantised exactly once per tile, in
+// the registers of the wave that multiplies it (f16, d * q rounded once), and
+// the 256 x 64 f32 accumulators live in the wave's AGPRs
+// (V_MFMA_F32_32X32X16_F16).  An expert's tokens normally fit one tile, so a
+// weight row is dequantised once per expert.
+//
+// Operands reach LDS by DMA (global_load_lds), never through VGPRs:
+//   activations  16-byte chunks of each token row; the chunk index is XORed
+//                with the row's low three bits, so the 16-byte fragment reads
+//                of eight consecutive rows hit eight different bank groups;
+//   weights      the raw bytes of two quantised blocks per row per K step, in
+//                per-wave regions (32 rows each) that only the owning wave
+//                reads.
+// A three-stage ring keeps the loads of two K steps in flight behind the step
+// being multiplied.  The DMAs are issued from inline assembly, because the
+// compiler makes every LDS read that follows an LDS DMA wait for all
+// outstanding loads; the kernel instead waits with exact vmcnt counts: in the
+// middle of step s a wave waits for its own loads of step s + 1 and
+// dequantises that step's first block ahead of time, and one barrier per step
+// publishes the other waves' activation chunks.
 #include <hip/hip_fp16.h>
 #include <hip/hip_runtime.h>
 
@@ -28,15 +39,13 @@ namespace moe {
 namespace {
 
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));
-typedef float floatx4 __attribute__((ext_vector_type(4)));
 typedef float floatx16 __attribute__((ext_vector_type(16)));
-typedef uint32_t u32x4a __attribute__((ext_vector_type(4)));
-typedef uint32_t u32x2a __attribute__((ext_vector_type(2)));
 
-constexpr int BM = 128;        // tokens per tile
-constexpr int BW = 256;        // weight rows per tile (up: 128 gate + 128 up rows)
-constexpr int BK = 64;         // K values per step (two 32-value blocks)
-constexpr int LDA = BK + 8;    // A row stride in halves (144 bytes)
+constexpr int BM = 256;              // tokens per tile
+constexpr int BW = 256;              // weight rows per tile (up: 128 gate + 128 up rows)
+constexpr int BK = 64;               // K values per step (two 32-value blocks)
+constexpr int NS = 3;                // LDS ring stages
+constexpr int A_STAGE = BM * BK * 2;  // bytes of activations per stage
 
 __device__ inline uint32_t alignb(uint32_t hi, uint32_t lo, uint32_t s) { return __builtin_amdgcn_alignbyte(hi, lo, s); }
 __device__ inline uint32_t perm(uint32_t hi, uint32_t lo, uint32_t sel) { return __builtin_amdgcn_perm(hi, lo, sel); }
@@ -59,98 +68,186 @@ __device__ inline void codes4(uint32_t v, __half2 off2, __half2 d2, uint32_t &w0
     w01 = h2_bits(__hmul2(__hsub2(as_h2(perm(0x64646464u, v, 0x04010400u)), off2), d2));
     w23 = h2_bits(__hmul2(__hsub2(as_h2(perm(0x64646464u, v, 0x04030402u)), off2), d2));
 }
+__device__ inline half8 pack8(const uint32_t (&o)[4]) {
+    half8 r;
+    __builtin_memcpy(&r, o, 16);
+    return r;
+}
 
-// Per-format layout of one 32-value block: bytes in the checkpoint, dwords
-// fetched from a 4-byte-aligned address, dwords of the LDS record.
+// Bytes of one 32-value block, and dwords per weight row per K step (two
+// blocks; a row's step always starts 4-byte aligned since K % 64 == 0).
 template <int DT>
 struct Fmt;
 template <>
 struct Fmt<MOE_DT_Q4_0> {
-    static constexpr int bytes = 18, fetch = 5, rec = 5;
+    static constexpr int bytes = 18, rd = 9;
 };
 template <>
 struct Fmt<MOE_DT_Q5_0> {
-    static constexpr int bytes = 22, fetch = 6, rec = 6;
+    static constexpr int bytes = 22, rd = 11;
 };
 template <>
 struct Fmt<MOE_DT_Q8_0> {
-    static constexpr int bytes = 34, fetch = 9, rec = 9;
+    static constexpr int bytes = 34, rd = 17;
 };
-
-// The dwords covering block b of a 4-byte-aligned row, as loaded (global
-// loads; nothing waits for them here).
+// Weight DMA.  A row's step (rd dwords) is split into nx4 16-byte lanes
+// (dwords 0 .. 4 nx4 - 1) and nd dword lanes (the rest).  One 32-row region
+// is laid out as
+//   X part  lane q = 32 x + r  (x < nx4) at 16 q: dwords 4x .. 4x+3 of row r
+//   D part  lane q = 32 e + r  (e < nd)  at X + 4 q: dword 4 nx4 + e of row r
+// and filled by nx4 / 2 dwordx4 DMAs plus ceil(nd / 2) dword DMAs (lanes
+// past nd load row 0 into the padding at the region's end).  Dword d of row
+// r of the region therefore sits at loc(d, r) below.
 template <int DT>
-__device__ inline void fetch_raw(const uint8_t *row, int b, uint32_t (&d)[Fmt<DT>::fetch]) {
-    const uint32_t *q =
-        reinterpret_cast<const uint32_t *>(__builtin_assume_aligned(row, 4)) + ((b * Fmt<DT>::bytes) >> 2);
-#pragma unroll
-    for (int i = 0; i < Fmt<DT>::fetch; i++) d[i] = gload(q + i);
-}
-
-// Normalise fetched dwords to the block's LDS record: rec[0] = scale (low 16
-// bits), rec[1..] = the bytes after the scale.  `odd`: the block starts 2
-// bytes into its first dword (an odd block index in every format).
-template <int DT>
-__device__ inline void normalise(const uint32_t (&d)[Fmt<DT>::fetch], bool odd, uint32_t (&rec)[Fmt<DT>::rec]) {
-    constexpr int N = Fmt<DT>::fetch;
-    uint32_t s[N];  // the block starting at byte 0
-#pragma unroll
-    for (int i = 0; i < N - 1; i++) s[i] = odd ? alignb(d[i + 1], d[i], 2) : d[i];
-    s[N - 1] = odd ? (d[N - 1] >> 16) : d[N - 1];
-    rec[0] = s[0] & 0xffffu;
-#pragma unroll
-    for (int i = 1; i < Fmt<DT>::rec; i++) rec[i] = alignb(s[i], s[i - 1], 2);
-}
-
-// Lane group q's eight values of a block record, as one MFMA operand:
-// slots 0..3 = elements 4q..4q+3, slots 4..7 = elements 16+4q..16+4q+3.
-// rec_codes reads the record dwords that hold them; dequant_codes turns them
-// into f16 (d * q rounded once).
-template <int DT>
-struct Codes;
-template <>
-struct Codes<MOE_DT_Q4_0> {
-    static constexpr int n = 1;  // the code dword
-};
-template <>
-struct Codes<MOE_DT_Q5_0> {
-    static constexpr int n = 2;  // high-bit dword, code dword
-};
-template <>
-struct Codes<MOE_DT_Q8_0> {
-    static constexpr int n = 2;  // low-half and high-half code dwords
-};
-template <int DT>
-__device__ inline void rec_codes(const uint32_t *rec, int q, uint32_t (&c)[Codes<DT>::n]) {
-    if constexpr (DT == MOE_DT_Q4_0) {
-        c[0] = rec[1 + q];
-    } else if constexpr (DT == MOE_DT_Q5_0) {
-        c[0] = rec[1], c[1] = rec[2 + q];
-    } else {
-        c[0] = rec[1 + q], c[1] = rec[5 + q];
+struct BLay {
+    static constexpr int rd = Fmt<DT>::rd;
+    static constexpr int nx4 = rd / 4;             // 2, 2, 4 (even)
+    static constexpr int nd = rd - 4 * nx4;        // 1, 3, 1
+    static constexpr int ix = nx4 / 2;             // dwordx4 DMAs per region
+    static constexpr int id = (nd + 1) / 2;        // dword DMAs per region
+    static constexpr int inst = ix + id;
+    static constexpr int xbytes = 512 * nx4;
+    static constexpr int region = xbytes + 256 * id;  // bytes
+    static constexpr int stage = 8 * region;
+    static_assert(nx4 % 2 == 0, "whole dwordx4 DMAs per region");
+    __device__ static constexpr uint32_t loc(int d, int r) {
+        return d < 4 * nx4 ? (uint32_t)(512 * (d >> 2) + 16 * r + 4 * (d & 3))
+                           : (uint32_t)(xbytes + 128 * (d - 4 * nx4) + 4 * r);
     }
-}
+};
 template <int DT>
-__device__ inline half8 dequant_codes(uint32_t scale, const uint32_t (&c)[Codes<DT>::n], int q) {
-    const __half2 d2 = as_h2((scale & 0xffffu) * 0x10001u);
+constexpr int lds_bytes() {
+    return NS * (A_STAGE + BLay<DT>::stage) + 2 * BM * 4;
+}
+
+// ---- LDS DMA and exact waits ------------------------------------------------
+// global_load_lds writes lane l's 16 (or 4) bytes to LDS address m0 + 16 l
+// (4 l); lanes with EXEC clear write nothing.  Addresses are an SGPR base
+// plus a 32-bit VGPR offset; the base and the LDS address are wave-uniform
+// (readfirstlane states that to the compiler, which may not prove it).
+//
+// The compiler cannot see that the assembly below is a vector memory load
+// that reads an SGPR base and M0, so it would not insert the wait states the
+// hardware needs between a VALU write of an SGPR (v_readfirstlane) and a
+// vector memory instruction reading it (5), or between an M0 write and an
+// LDS DMA (1).  The assembly therefore copies the base with s_mov_b64 (a
+// scalar read, which the hardware interlocks) into SGPRs that nothing but
+// scalar instructions ever wrote, and pads one wait state after the copy.
+__device__ inline const void *uniform_ptr(const void *p) {
+    const uint64_t v = reinterpret_cast<uint64_t>(p);
+    const uint64_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)v);
+    const uint64_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(v >> 32));
+    return reinterpret_cast<const void *>(lo | (hi << 32));
+}
+__device__ inline void dma16(const void *base, uint32_t off, uint32_t lds) {
+    uint64_t sb;
+    asm volatile(
+        "s_mov_b64 %0, %2\n\t"
+        "s_nop 0\n\t"
+        "global_load_lds_dwordx4 %1, %0"
+        : "=&s"(sb)
+        : "v"(off), "s"(uniform_ptr(base)), "{m0}"(__builtin_amdgcn_readfirstlane((int)lds))
+        : "memory");
+}
+__device__ inline void dma4(const void *base, uint32_t off, uint32_t lds) {
+    uint64_t sb;
+    asm volatile(
+        "s_mov_b64 %0, %2\n\t"
+        "s_nop 0\n\t"
+        "global_load_lds_dword %1, %0"
+        : "=&s"(sb)
+        : "v"(off), "s"(uniform_ptr(base)), "{m0}"(__builtin_amdgcn_readfirstlane((int)lds))
+        : "memory");
+}
+template <int N>
+__device__ inline void wait_vm() {
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+// Wait for all but the newest N of this wave's loads and for its LDS reads,
+// then meet the other waves.
+template <int N>
+__device__ inline void wait_vm_barrier() {
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"(N) : "memory");
+}
+__device__ inline uint32_t lds_addr(const void *p) {
+    return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void *)p;
+}
+typedef const __attribute__((address_space(3))) uint8_t *lds_p;
+typedef uint32_t u32x4l __attribute__((ext_vector_type(4)));
+__device__ inline uint32_t lds_u32(lds_p p) { return *(const __attribute__((address_space(3))) uint32_t *)p; }
+__device__ inline half8 lds_h8(lds_p p) { return *(const __attribute__((address_space(3))) half8 *)p; }
+
+// ---- weight fragments -----------------------------------------------------
+// Lane (l32, h) of a wave reads row l32 of a 32-row region.  For K group
+// (block kb, MFMA m) the MFMA takes elements 16 m + 8 h .. + 7 of block kb in
+// natural order; both MFMAs of a block use the same eight code bytes
+// 8 h .. 8 h + 7 of the block's code array (Q4_0/Q5_0: low nibbles for m = 0,
+// high nibbles for m = 1), Q8_0 bytes 16 m + 8 h .. + 7.  Slots<DT> lists the
+// row dwords a lane reads for block kb: dword base + 2 h * hm; their LDS
+// offsets are computed once per lane.  dequant turns the dwords (v, in slot
+// order) into the block's two MFMA operands.
+template <int DT>
+struct Slots;
+template <>
+struct Slots<MOE_DT_Q4_0> {  // kb 0: bytes 0..17 (scale, codes 2..17); kb 1: bytes 18..35
+    static constexpr int n[2] = {4, 3};
+    static constexpr int base[2][7] = {{0, 0, 1, 2}, {4, 5, 6}};
+    static constexpr int hm[2][7] = {{0, 1, 1, 1}, {0, 1, 1}};
+};
+template <>
+struct Slots<MOE_DT_Q5_0> {  // kb 0: scale 0..1, qh 2..5, codes 6..21; kb 1: scale 22..23, qh 24..27, codes 28..43
+    static constexpr int n[2] = {5, 4};
+    static constexpr int base[2][7] = {{0, 1, 1, 2, 3}, {5, 6, 7, 8}};
+    static constexpr int hm[2][7] = {{0, 0, 1, 1, 1}, {0, 0, 1, 1}};
+};
+template <>
+struct Slots<MOE_DT_Q8_0> {  // kb 0: scale 0..1, codes 2..33; kb 1: scale 34..35, codes 36..67
+    static constexpr int n[2] = {7, 5};
+    static constexpr int base[2][7] = {{0, 0, 1, 2, 4, 5, 6}, {8, 9, 10, 13, 14}};
+    static constexpr int hm[2][7] = {{0, 1, 1, 1, 1, 1, 1}, {0, 1, 1, 1, 1}};
+};
+
+template <int DT, int KB>
+__device__ inline void dequant(const uint32_t *v, half8 (&b)[2], int h) {
+    const uint32_t s = KB == 0 ? (v[0] & 0xffffu) : (v[0] >> 16);
+    const __half2 d2 = as_h2(s * 0x10001u);
     uint32_t o[4];
     if constexpr (DT == MOE_DT_Q4_0) {
         const __half2 off2 = __floats2half2_rn(1032.0f, 1032.0f);
-        codes4(c[0] & 0x0f0f0f0fu, off2, d2, o[0], o[1]);
-        codes4((c[0] >> 4) & 0x0f0f0f0fu, off2, d2, o[2], o[3]);
+        const uint32_t w0 = KB == 0 ? alignb(v[2], v[1], 2) : v[1];
+        const uint32_t w1 = KB == 0 ? alignb(v[3], v[2], 2) : v[2];
+        codes4(w0 & 0x0f0f0f0fu, off2, d2, o[0], o[1]);
+        codes4(w1 & 0x0f0f0f0fu, off2, d2, o[2], o[3]);
+        b[0] = pack8(o);
+        codes4((w0 >> 4) & 0x0f0f0f0fu, off2, d2, o[0], o[1]);
+        codes4((w1 >> 4) & 0x0f0f0f0fu, off2, d2, o[2], o[3]);
+        b[1] = pack8(o);
     } else if constexpr (DT == MOE_DT_Q5_0) {
-        const uint32_t hb = c[0];
         const __half2 off2 = __floats2half2_rn(1040.0f, 1040.0f);
-        codes4((c[1] & 0x0f0f0f0fu) | spread4((hb >> (4 * q)) & 0xfu), off2, d2, o[0], o[1]);
-        codes4(((c[1] >> 4) & 0x0f0f0f0fu) | spread4((hb >> (16 + 4 * q)) & 0xfu), off2, d2, o[2], o[3]);
+        const uint32_t qh = KB == 0 ? alignb(v[1], v[0], 2) : v[1];
+        const uint32_t w0 = KB == 0 ? alignb(v[3], v[2], 2) : v[2];
+        const uint32_t w1 = KB == 0 ? alignb(v[4], v[3], 2) : v[3];
+        const uint32_t hb = qh >> (8 * h);  // bit i: element 8 h + i; bit 16 + i: element 16 + 8 h + i
+        codes4((w0 & 0x0f0f0f0fu) | spread4(hb & 0xfu), off2, d2, o[0], o[1]);
+        codes4((w1 & 0x0f0f0f0fu) | spread4((hb >> 4) & 0xfu), off2, d2, o[2], o[3]);
+        b[0] = pack8(o);
+        codes4(((w0 >> 4) & 0x0f0f0f0fu) | spread4((hb >> 16) & 0xfu), off2, d2, o[0], o[1]);
+        codes4(((w1 >> 4) & 0x0f0f0f0fu) | spread4((hb >> 20) & 0xfu), off2, d2, o[2], o[3]);
+        b[1] = pack8(o);
     } else {  // Q8_0: int8 codes, read as uint8 + 128
         const __half2 off2 = __floats2half2_rn(1152.0f, 1152.0f);
-        codes4(c[0] ^ 0x80808080u, off2, d2, o[0], o[1]);
-        codes4(c[1] ^ 0x80808080u, off2, d2, o[2], o[3]);
+#pragma unroll
+        for (int m = 0; m < 2; m++) {
+            const uint32_t *c = v + 1 + (KB == 0 ? 3 : 2) * m;
+            const uint32_t w0 = KB == 0 ? alignb(c[1], c[0], 2) : c[0];
+            const uint32_t w1 = KB == 0 ? alignb(c[2], c[1], 2) : c[1];
+            codes4(w0 ^ 0x80808080u, off2, d2, o[0], o[1]);
+            codes4(w1 ^ 0x80808080u, off2, d2, o[2], o[3]);
+            b[m] = pack8(o);
+        }
     }
-    half8 r;
-    __builtin_memcpy(&r, o, 16);
-    return r;
 }
 
 // Tile coordinates.  mode 0: routed tiles from the dispatch list; mode 1: the
@@ -197,13 +294,11 @@ __device__ inline bool tile_of(const MfmaArgs &a, int mode, int gx, TileInfo &ti
 }
 
 template <int DT, bool UP>
-__global__ __launch_bounds__(256, 2) void mfma_kernel(MfmaArgs a, int mode, int gx, int ksplit) {
-    constexpr int REC = Fmt<DT>::rec;
-    constexpr int BREC = 2 * REC + 1;  // dwords per weight row per step (+1 spreads banks)
-    __shared__ __attribute__((aligned(16))) _Float16 As[2][BM * LDA];
-    __shared__ __attribute__((aligned(16))) uint32_t Bs[2][BW * BREC];
-    __shared__ int src_row[BM];
-    __shared__ int dst_row[BM];
+__global__ __launch_bounds__(256, 1) void mfma_kernel(MfmaArgs a, int mode, int gx, int ksplit) {
+    using BL = BLay<DT>;
+    extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+    int *src_row = reinterpret_cast<int *>(smem + NS * (A_STAGE + BL::stage));
+    int *dst_row = src_row + BM;
 
     TileInfo ti;
     if (!tile_of(a, mode, gx, ti)) return;
@@ -214,12 +309,15 @@ __global__ __launch_bounds__(256, 2) void mfma_kernel(MfmaArgs a, int mode, int 
     if (n0 >= W0.rows) return;
     const int Ktot = W0.cols;
     const int kspan = Ktot / ksplit;  // a multiple of BK (checked on the host)
-    const int kbeg = ti.ksplit * kspan, kend = kbeg + kspan;
-    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    const int kbeg = ti.ksplit * kspan;
+    const int nsteps = kspan / BK;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int Icol = ti.shared ? a.I_s : a.I;
     const int valid = min(BM, ti.n - ti.m0);
+    const int mt = (valid + 31) / 32;
 
-    if (tid < BM) {
+    {
         int s = -1, d = -1;
         if (tid < valid) {
             d = ti.row0 + ti.m0 + tid;
@@ -230,144 +328,232 @@ __global__ __launch_bounds__(256, 2) void mfma_kernel(MfmaArgs a, int mode, int 
     }
     __syncthreads();
 
-    // ---- staging: thread -> A row am, 32-value block ab of the step; weight
-    //      row bn (LDS row; up: gate rows 0..127, up rows 128..255), both
-    //      blocks of the step.  Every thread issues the same loads on every
-    //      step (rows past the end read row 0 and are zeroed when stored), so
-    //      each wait for a step's data counts exactly the loads after it.
-    const int am = tid >> 1, ab = tid & 1;
-    const int arow = src_row[am];
-    const bool avalid = arow >= 0;
-    const uint16_t *abase = UP ? a.xh + (size_t)(avalid ? arow : src_row[0]) * a.H
-                               : (ti.shared ? a.hs : a.h) + (size_t)(avalid ? arow : src_row[0]) * Icol;
-    const int bn = tid;
-    const MatDev &WB = (UP && bn >= BW / 2) ? W1 : W0;
-    const int brow = UP ? n0 + (bn & (BW / 2 - 1)) : n0 + bn;
-    const bool bvalid = brow < WB.rows;
-    const uint8_t *browp = WB.ptr + (size_t)(bvalid ? brow : 0) * WB.stride;
+    const uint32_t lds0 = lds_addr(smem);
+    const uint32_t ldsB = lds0 + NS * A_STAGE;
+    const lds_p sm = (lds_p)smem;
+    const int l32 = lane & 31, hf = lane >> 5;
 
-    // Global loads are held as raw dwords and normalised when stored to LDS.
-    constexpr int FD = Fmt<DT>::fetch;
-    constexpr int FQ = Codes<DT>::n;
-    u32x4a areg[4];
-    uint32_t braw[2][FD];
-    auto load_step = [&](int k0, u32x4a (&ar)[4], uint32_t (&br)[2][FD]) {
-        const int kc = k0 < kend ? k0 : kbeg;  // past the end: a harmless reload
-        const u32x4a *src = reinterpret_cast<const u32x4a *>(abase + kc + 32 * ab);
+    // Activation DMA: instruction u of wave wv covers rows 8 i .. 8 i + 7,
+    // i = wv + 4 u; lane l takes row r = 8 i + l / 8 and stores slot l % 8 of
+    // that row's 128 bytes, which holds logical chunk (l % 8) ^ ((r / 2) % 8).
+    // Rows past the tile's tokens repeat token row 0 (their outputs are never
+    // stored).
+    const uint8_t *abase = reinterpret_cast<const uint8_t *>(UP ? a.xh : (ti.shared ? a.hs : a.h));
+    const uint32_t arow_bytes = (uint32_t)(UP ? a.H : Icol) * 2;
+    // Weight DMA: region j of wave wv holds 32 weight rows.  woff: per DMA
+    // (the region's dwordx4 DMAs, then its dword DMAs) the lane's byte offset
+    // in the weight matrix, without the step's K offset.
+    const uint8_t *wbase[2];
+    uint32_t woff[2][BL::inst];
 #pragma unroll
-        for (int i = 0; i < 4; i++) ar[i] = gload(src + i);
+    for (int j = 0; j < 2; j++) {
+        const MatDev &W = (UP && j == 1) ? W1 : W0;
+        wbase[j] = W.ptr;
+        const int row0 = UP ? n0 + 32 * wv : n0 + 64 * wv + 32 * j;
+        int row = row0 + (lane & 31);
+        if (row >= W.rows) row = 0;
 #pragma unroll
-        for (int bb = 0; bb < 2; bb++) fetch_raw<DT>(browp, kc / 32 + bb, br[bb]);
-    };
-    // Chunk c of a 32-value block holds elements 8c..8c+7; its two halves go
-    // to the K-permuted slots 16 (c & 1) + 4 (c >> 1) and that + 8.  Block bb
-    // of a step has parity bb (k0 / 32 is even), so it starts 2 bytes into
-    // its first dword exactly when bb == 1.
-    auto store_step = [&](int buf, const u32x4a (&ar)[4], const uint32_t (&br)[2][FD]) {
-        _Float16 *arow_lds = &As[buf][am * LDA + 32 * ab];
-#pragma unroll
-        for (int c = 0; c < 4; c++) {
-            const int p0 = 16 * (c & 1) + 4 * (c >> 1);
-            const u32x4a v = avalid ? ar[c] : u32x4a{0u, 0u, 0u, 0u};
-            *reinterpret_cast<u32x2a *>(arow_lds + p0) = u32x2a{v.x, v.y};
-            *reinterpret_cast<u32x2a *>(arow_lds + p0 + 8) = u32x2a{v.z, v.w};
+        for (int i = 0; i < BL::inst; i++) {
+            const int q = 64 * (i < BL::ix ? i : i - BL::ix) + lane;  // lane within the part
+            uint32_t off;
+            if (i < BL::ix) {
+                off = (uint32_t)row * W.stride + 16u * (uint32_t)(q >> 5);
+            } else {
+                const int e = q >> 5;
+                off = e < BL::nd ? (uint32_t)row * W.stride + (uint32_t)(16 * BL::nx4 + 4 * e) : 0u;
+            }
+            woff[j][i] = off;
         }
-#pragma unroll
-        for (int bb = 0; bb < 2; bb++) {
-            uint32_t rec[REC];
-            normalise<DT>(br[bb], bb == 1, rec);
-            if (!bvalid) rec[0] = 0u;  // scale 0: a zero weight row
-            uint32_t *brow_lds = &Bs[buf][bn * BREC + bb * REC];
-#pragma unroll
-            for (int i = 0; i < REC; i++) brow_lds[i] = rec[i];
-        }
-    };
+    }
 
-    // Wave wv owns all 128 tokens and two 32-column tiles j: up -> gate rows
-    // 32 wv .. +32 (j = 0) and the same up rows (j = 1); down -> output
-    // columns 64 wv + 32 j .. +32.  Each V_MFMA_F32_32X32X16_F16 takes A lane
-    // l = row l % 32, K slots 8 (l / 32) .. +8 and B lane l = column l % 32,
-    // the same K slots; D lane l element v = row 8 (v / 4) + 4 (l / 32) + v % 4,
-    // column l % 32.  Within a 32-value block, MFMA m covers permuted slots
-    // 16 m .. 16 m + 15, so lane half h reads slot group q = 2 m + h: the
-    // eight codes of dword q.  An activation fragment feeds two MFMAs (j), a
-    // dequantised weight fragment the MT 32-token tiles.
-    floatx16 acc[4][2];
+    // Per-lane LDS offsets of the compute side.
+    uint32_t aoff[4];  // group g = 2 kb + m: row l32, logical chunk 2 g + hf
 #pragma unroll
-    for (int t = 0; t < 4; t++)
+    for (int g = 0; g < 4; g++) aoff[g] = (uint32_t)l32 * 128u + ((uint32_t)((2 * g + hf) ^ ((l32 >> 1) & 7)) << 4);
+    using SL = Slots<DT>;
+    const uint32_t brow_x = 16u * l32;                 // row l32's X part within a region
+    const uint32_t brow_d = BL::xbytes + 4u * l32;     // and its D part
+
+    floatx16 acc[8][2];
+#pragma unroll
+    for (int t = 0; t < 8; t++)
 #pragma unroll
         for (int j = 0; j < 2; j++) acc[t][j] = floatx16{};
-    const int l32 = lane & 31, hf = lane >> 5;
-    int bcol[2];
-#pragma unroll
-    for (int j = 0; j < 2; j++) bcol[j] = UP ? (128 * j + 32 * wv + l32) : (64 * wv + 32 * j + l32);
 
-    // The K loop for MT live 32-token tiles (chosen once per block).
     auto run = [&](auto mt_c) {
         constexpr int MT = decltype(mt_c)::value;
-        // A step is four fragment groups g = (kb, m): group g + 1's
-        // activation fragments and weight codes are read from LDS while group
-        // g's MFMAs run.
-        auto compute = [&](int buf) {
-            half8 af[2][MT];
-            uint32_t bsc[2][2], bq[2][2][FQ];
-            auto read_group = [&](int g, half8 (&A)[MT], uint32_t (&sc)[2], uint32_t (&bqv)[2][FQ]) {
-                const int kb = g >> 1, q = 2 * (g & 1) + hf;
+        constexpr int NB = 2 * BL::inst;  // weight DMAs per wave per step
+        constexpr int ND = MT + NB;       // DMAs per wave per step
+        uint32_t aoffg[MT];               // activation source offsets (step 0)
 #pragma unroll
-                for (int t = 0; t < MT; t++)
-                    A[t] = *reinterpret_cast<const half8 *>(&As[buf][(32 * t + l32) * LDA + 32 * kb + 8 * q]);
-#pragma unroll
-                for (int j = 0; j < 2; j++) {
-                    const uint32_t *rec = &Bs[buf][bcol[j] * BREC + kb * REC];
-                    sc[j] = rec[0];
-                    rec_codes<DT>(rec, q, bqv[j]);
-                }
-            };
-            read_group(0, af[0], bsc[0], bq[0]);
-#pragma unroll
-            for (int g = 0; g < 4; g++) {
-                const int c = g & 1;
-                if (g + 1 < 4) read_group(g + 1, af[c ^ 1], bsc[c ^ 1], bq[c ^ 1]);
-                // keep those reads ahead of this group's MFMAs
-                __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-                for (int j = 0; j < 2; j++) {
-                    const half8 bf = dequant_codes<DT>(bsc[c][j], bq[c][j], 2 * (g & 1) + hf);
-#pragma unroll
-                    for (int t = 0; t < MT; t++)
-                        acc[t][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[c][t], bf, acc[t][j], 0, 0, 0);
-                }
+        for (int u = 0; u < MT; u++) {
+            const int r = 8 * (wv + 4 * u) + (lane >> 3);
+            const int sr = src_row[r < valid ? r : 0];
+            aoffg[u] = (uint32_t)sr * arow_bytes + (uint32_t)kbeg * 2u +
+                       (uint32_t)(((lane & 7) ^ ((r >> 1) & 7)) << 4);
+        }
+        // DMA d of step `step` into ring stage `st`: d < MT activations, then
+        // the weight regions.  Steps past the end reload the last step into a
+        // stage nobody reads any more, so every step issues the same DMAs.
+        auto dma = [&](auto d_c, int step, int st) {
+            constexpr int d = decltype(d_c)::value;
+            const int sc = step < nsteps ? step : nsteps - 1;
+            if constexpr (d < MT) {
+                dma16(abase + (size_t)sc * (BK * 2), aoffg[d],
+                      lds0 + (uint32_t)st * A_STAGE + (uint32_t)(wv + 4 * d) * 1024u);
+            } else {
+                constexpr int j = (d - MT) / BL::inst, i = (d - MT) % BL::inst;
+                const uint8_t *wb = wbase[j] + (size_t)(kbeg / 32 + 2 * sc) * Fmt<DT>::bytes;
+                const uint32_t lr = ldsB + (uint32_t)st * BL::stage + (uint32_t)(2 * wv + j) * BL::region;
+                if constexpr (i < BL::ix)
+                    dma16(wb, woff[j][i], lr + 1024u * i);
+                else
+                    dma4(wb, woff[j][i], lr + BL::xbytes + 256u * (i - BL::ix));
             }
         };
-        // Double buffering: step s + 1's loads are issued before step s's
-        // MFMAs and stored to the other LDS buffer after them.
-        load_step(kbeg, areg, braw);
-        store_step(0, areg, braw);
-        __syncthreads();
-        const int nsteps = (kend - kbeg) / BK;
-        for (int st = 0; st + 1 < nsteps; st++) {
-            load_step(kbeg + (st + 1) * BK, areg, braw);
-            compute(st & 1);
-            store_step((st + 1) & 1, areg, braw);
-            __syncthreads();
+        auto dma_from = [&](auto lo_c, auto hi_c, int step, int st, auto self) {
+            constexpr int lo = decltype(lo_c)::value, hi = decltype(hi_c)::value;
+            if constexpr (lo < hi) {
+                dma(std::integral_constant<int, lo>{}, step, st);
+                self(std::integral_constant<int, lo + 1>{}, hi_c, step, st, self);
+            }
+        };
+        auto dma_range = [&](auto lo_c, auto hi_c, int step, int st) { dma_from(lo_c, hi_c, step, st, dma_from); };
+
+        // Row l32's whole step (rd dwords) of both regions, read with 16-byte
+        // LDS reads (both lane halves read the same row, which the LDS
+        // broadcasts); each lane then picks its dwords (Slots: base, or
+        // base + 2 for the upper lane half).
+        half8 bq[2][2][2];  // [kb][j][m]
+        half8 af[2][MT];
+        uint32_t rowv[2][BL::rd];
+        auto read_rows = [&](lds_p stage_b) {
+#pragma unroll
+            for (int j = 0; j < 2; j++) {
+                const uint32_t reg = (uint32_t)(2 * wv + j) * BL::region;
+#pragma unroll
+                for (int x = 0; x < BL::nx4; x++) {
+                    const u32x4l v =
+                        *(const __attribute__((address_space(3))) u32x4l *)(stage_b + reg + brow_x + 512 * x);
+                    rowv[j][4 * x] = v.x, rowv[j][4 * x + 1] = v.y, rowv[j][4 * x + 2] = v.z, rowv[j][4 * x + 3] = v.w;
+                }
+#pragma unroll
+                for (int e = 0; e < BL::nd; e++)
+                    rowv[j][4 * BL::nx4 + e] = lds_u32(stage_b + reg + brow_d + 128 * e);
+            }
+        };
+        auto dequant_raw = [&](auto kb_c, half8 (&B)[2][2]) {
+            constexpr int kb = decltype(kb_c)::value;
+#pragma unroll
+            for (int j = 0; j < 2; j++) {
+                uint32_t v[7];
+#pragma unroll
+                for (int k = 0; k < SL::n[kb]; k++) {
+                    const int b = SL::base[kb][k];
+                    v[k] = SL::hm[kb][k] ? (hf ? rowv[j][b + 2] : rowv[j][b]) : rowv[j][b];
+                }
+                dequant<DT, kb>(v, B[j], hf);
+            }
+        };
+        auto read_a = [&](lds_p sa, int g, half8 (&A)[MT]) {
+            const lds_p p = sa + aoff[g];
+#pragma unroll
+            for (int t = 0; t < MT; t++) A[t] = lds_h8(p + 4096 * t);
+        };
+        auto mfma = [&](const half8 (&A)[MT], const half8 (&B)[2][2], int m, int i) {
+            const int t = i >> 1, j = i & 1;
+            acc[t][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(A[t], B[j][m], acc[t][j], 0, 0, 0);
+        };
+        // One group's 2 MT MFMAs with DMAs [LO, HI) of step `step` spread
+        // between them: a DMA that the memory pipeline cannot take yet stalls
+        // this wave, not the MFMAs already queued.
+        auto mfmas_dma = [&](const half8 (&A)[MT], const half8 (&B)[2][2], int m, auto lo_c, auto hi_c, int step,
+                             int st) {
+            constexpr int LO = decltype(lo_c)::value, HI = decltype(hi_c)::value;
+            auto body = [&](auto i_c, auto self) {
+                constexpr int i = decltype(i_c)::value;
+                if constexpr (i < 2 * MT) {
+                    mfma(A, B, m, i);
+                    dma_range(std::integral_constant<int, LO + i * (HI - LO) / (2 * MT)>{},
+                              std::integral_constant<int, LO + (i + 1) * (HI - LO) / (2 * MT)>{}, step, st);
+                    self(std::integral_constant<int, i + 1>{}, self);
+                }
+            };
+            body(std::integral_constant<int, 0>{}, body);
+        };
+        auto mfmas = [&](const half8 (&A)[MT], const half8 (&B)[2][2], int m) {
+#pragma unroll
+            for (int i = 0; i < 2 * MT; i++) mfma(A, B, m, i);
+        };
+        using I0 = std::integral_constant<int, 0>;
+        using I1 = std::integral_constant<int, 1>;
+        constexpr int MA = MT / 2;  // activation DMAs in group 0; the rest in group 1
+
+        const lds_p smB = sm + NS * A_STAGE;
+        dma_range(I0{}, std::integral_constant<int, ND>{}, 0, 0);
+        dma_range(I0{}, std::integral_constant<int, ND>{}, 1, 1);
+        wait_vm_barrier<ND>();
+        read_a(sm, 0, af[0]);
+        read_rows(smB);
+        dequant_raw(I0{}, bq[0]);
+        int st = 0;
+        // Per step, this wave's loads of step s + 2 go out in order: the
+        // activation DMAs in groups 0 and 1, the weight DMAs in group 3.  The
+        // wait in group 2 therefore leaves exactly the MT activation DMAs of
+        // step s + 2 outstanding.
+        for (int s = 0; s < nsteps; s++) {
+            const lds_p sa = sm + st * A_STAGE;
+            const int st1 = st == 2 ? 0 : st + 1, st2 = st == 0 ? 2 : st - 1;
+            // g = 0 (kb 0, m 0): group 1's activations first.
+            read_a(sa, 1, af[1]);
+            __builtin_amdgcn_sched_barrier(0);
+            mfmas_dma(af[0], bq[0], 0, I0{}, std::integral_constant<int, MA>{}, s + 2, st2);
+            // g = 1 (kb 0, m 1): dequantise block 1, read group 2.
+            dequant_raw(I1{}, bq[1]);
+            read_a(sa, 2, af[0]);
+            mfmas_dma(af[1], bq[0], 1, std::integral_constant<int, MA>{}, std::integral_constant<int, MT>{}, s + 2,
+                      st2);
+            __builtin_amdgcn_sched_barrier(0);
+            // g = 2 (kb 1, m 0): read group 3; then wait for this wave's
+            // loads of step s + 1 and meet the other waves, after which step
+            // s + 1's stage is complete and nobody reads stage s any more.
+            read_a(sa, 3, af[1]);
+            mfmas(af[0], bq[1], 0);
+            __builtin_amdgcn_sched_barrier(0);
+            wait_vm_barrier<MT>();
+            __builtin_amdgcn_sched_barrier(0);
+            // g = 3 (kb 1, m 1): step s + 1's group 0 and weight rows; step
+            // s + 2's weight DMAs.
+            const lds_p sa1 = sm + st1 * A_STAGE;
+            read_a(sa1, 0, af[0]);
+            read_rows(smB + st1 * BL::stage);
+            __builtin_amdgcn_sched_barrier(0);
+            mfmas_dma(af[1], bq[1], 1, std::integral_constant<int, MT>{}, std::integral_constant<int, ND>{}, s + 2,
+                      st2);
+            dequant_raw(I0{}, bq[0]);
+            __builtin_amdgcn_sched_barrier(0);
+            st = st1;
         }
-        compute((nsteps - 1) & 1);
     };
-    const int mt = (valid + 31) / 32;
     switch (mt) {
     case 1: run(std::integral_constant<int, 1>{}); break;
     case 2: run(std::integral_constant<int, 2>{}); break;
     case 3: run(std::integral_constant<int, 3>{}); break;
-    default: run(std::integral_constant<int, 4>{}); break;
+    case 4: run(std::integral_constant<int, 4>{}); break;
+    case 5: run(std::integral_constant<int, 5>{}); break;
+    case 6: run(std::integral_constant<int, 6>{}); break;
+    case 7: run(std::integral_constant<int, 7>{}); break;
+    default: run(std::integral_constant<int, 8>{}); break;
     }
+    wait_vm<0>();
 
-    // ---- epilogue: lane holds C[32 t + 8 (v / 4) + 4 hf + v % 4][bcol[j]].
+    // ---- epilogue: lane holds C[32 t + 8 (v / 4) + 4 hf + v % 4][column l32 of set j].
     if (UP) {
         uint16_t *hout = ti.shared ? a.hs : a.h;
         const int col = n0 + 32 * wv + l32;
         if (col < W0.rows) {
 #pragma unroll
-            for (int t = 0; t < 4; t++) {
+            for (int t = 0; t < 8; t++) {
                 if (t >= mt) continue;
 #pragma unroll
                 for (int v = 0; v < 16; v++) {
@@ -386,7 +572,7 @@ __global__ __launch_bounds__(256, 2) void mfma_kernel(MfmaArgs a, int mode, int 
             const int col = n0 + 64 * wv + 32 * j + l32;
             if (col >= W0.rows) continue;
 #pragma unroll
-            for (int t = 0; t < 4; t++) {
+            for (int t = 0; t < 8; t++) {
                 if (t >= mt) continue;
 #pragma unroll
                 for (int v = 0; v < 16; v++) {
@@ -398,16 +584,23 @@ __global__ __launch_bounds__(256, 2) void mfma_kernel(MfmaArgs a, int mode, int 
     }
 }
 
+template <int DT, bool UP>
+hipError_t launch_one(dim3 grid, const MfmaArgs &a, int mode, int ksplit, hipStream_t s) {
+    static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void *>(&mfma_kernel<DT, UP>),
+                                                       hipFuncAttributeMaxDynamicSharedMemorySize, lds_bytes<DT>());
+    if (attr != hipSuccess) return attr;
+    hipLaunchKernelGGL((mfma_kernel<DT, UP>), grid, dim3(256), lds_bytes<DT>(), s, a, mode, (int)grid.x, ksplit);
+    return hipGetLastError();
+}
+
 template <bool UP>
 hipError_t launch_dt(int dt, dim3 grid, const MfmaArgs &a, int mode, int ksplit, hipStream_t s) {
-    const int gx = (int)grid.x;
     switch (dt) {
-    case MOE_DT_Q8_0: hipLaunchKernelGGL((mfma_kernel<MOE_DT_Q8_0, UP>), grid, dim3(256), 0, s, a, mode, gx, ksplit); break;
-    case MOE_DT_Q4_0: hipLaunchKernelGGL((mfma_kernel<MOE_DT_Q4_0, UP>), grid, dim3(256), 0, s, a, mode, gx, ksplit); break;
-    case MOE_DT_Q5_0: hipLaunchKernelGGL((mfma_kernel<MOE_DT_Q5_0, UP>), grid, dim3(256), 0, s, a, mode, gx, ksplit); break;
+    case MOE_DT_Q8_0: return launch_one<MOE_DT_Q8_0, UP>(grid, a, mode, ksplit, s);
+    case MOE_DT_Q4_0: return launch_one<MOE_DT_Q4_0, UP>(grid, a, mode, ksplit, s);
+    case MOE_DT_Q5_0: return launch_one<MOE_DT_Q5_0, UP>(grid, a, mode, ksplit, s);
     default: return hipErrorInvalidValue;
     }
-    return hipGetLastError();
 }
 
 }  // namespace
@@ -415,6 +608,12 @@ hipError_t launch_dt(int dt, dim3 grid, const MfmaArgs &a, int mode, int ksplit,
 int mfma_tile_m() { return BM; }
 
 bool mfma_format_ok(int dt) { return dt == MOE_DT_Q4_0 || dt == MOE_DT_Q5_0 || dt == MOE_DT_Q8_0; }
+
+// The kernels address activations and weight rows with 32-bit offsets.
+bool mfma_fits(size_t t, size_t k, size_t H, size_t I, size_t I_s) {
+    const size_t lim = (size_t)1 << 32;
+    return t * H * 2 < lim && t * k * I * 2 < lim && t * I_s * 2 < lim;
+}
 
 // Split K of the down projection (2 or 4 parts) when its grid would leave
 // CUs idle: the fewest parts that give about two blocks per CU.

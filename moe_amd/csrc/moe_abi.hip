@@ -395,7 +395,10 @@ int moe_layer_create(moe_ctx *ctx, const moe_layer_desc *d, moe_layer **out) {
     L->fast_ok = fast;
     bool fmt = true;
     for (int e = 0; e < E + (L->has_shared ? 1 : 0); e++)
-        for (int m = 0; m < 3; m++) fmt &= mfma_format_ok(L->experts_host[e].m[m].dt);
+        for (int m = 0; m < 3; m++) {
+            const MatDev &mm = L->experts_host[e].m[m];
+            fmt &= mfma_format_ok(mm.dt) && (size_t)mm.rows * mm.stride < ((size_t)1 << 32);
+        }
     L->mfma_ok = fast && fmt && H % 64 == 0 && I % 64 == 0 && (!L->has_shared || L->I_s % 64 == 0);
     L->decode_ok = fast && decode_supported(H, I, L->has_shared ? L->I_s : 0, e0.m[0].dt,
                                             L->has_shared ? L->experts_host[E].m[0].dt : e0.m[0].dt);
@@ -619,6 +622,7 @@ int moe_layer_forward(moe_layer *L, const float *x, int32_t t, float *out, float
         const int dt_s = L->has_shared ? L->experts_host[L->E].m[0].dt : dt_r;
         if (t != 1 || !decode_fits(L->I, L->I_s, k, L->has_shared, dt_r, dt_s)) path = kGemv;
     }
+    if (path == kMfma && !mfma_fits(t, k, L->H, L->I, L->has_shared ? L->I_s : 0)) path = kGemv;
     const int bm = path == kMfma ? mfma_tile_m() : 0;
     if ((rc = route_and_dispatch(L, x, t, k, bm, path == kDecode, routes, hits, prev, stats, nullptr, s))) return rc;
 

@@ -210,6 +210,7 @@ struct MfmaArgs {
 };
 int mfma_tile_m();
 bool mfma_format_ok(int dt);
+bool mfma_fits(size_t t, size_t k, size_t H, size_t I, size_t I_s);
 constexpr int kMaxKSplit = 4;
 int mfma_down_ksplit(int m_tiles, int n_rows, int K, int K_shared);
 // up: gate/up + SwiGLU; down: down projection.  Routed tiles come from the

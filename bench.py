@@ -126,6 +126,22 @@ def cpu_baseline(host, t_decode: int, t_prefill: int, seconds: float):
     return dec, pre, cores, n
 
 
+def copy_calibration(mib: int) -> int:
+    """Five device-to-device copies of `mib` MiB: each reads and writes exactly
+    mib * 1024 KiB, so a counter run over them gives the factor between the
+    counters' KiB and algorithmic bytes."""
+    import torch
+
+    n = mib * (1 << 20) // 4
+    src = torch.ones(n, dtype=torch.float32, device="cuda:0")
+    dst = torch.empty_like(src)
+    for _ in range(5):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_calibration_kib_per_copy": mib * 1024, "copies": 5}), flush=True)
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
@@ -137,11 +153,16 @@ def main() -> int:
     ap.add_argument("--copies", type=int, default=4, help="distinct weight copies cycled through")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
+                    help="only copy MIB MiB device-to-device 5 times (a plain copy kernel of known size, the "
+                         "reference point for the FETCH_SIZE / WRITE_SIZE counters) and exit")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: this build has no multi-GPU path (every GPU box here has one GPU); "
               "run with --gpus 1", file=sys.stderr)
         return 2
+    if args.copy_calibration:
+        return copy_calibration(args.copy_calibration)
 
     import torch
 

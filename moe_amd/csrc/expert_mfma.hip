@@ -1,6 +1,6 @@
 // expert_mfma.hip — grouped SwiGLU expert GEMMs on gfx950 matrix cores.
 //
-// One block computes a tile of up to 256 tokens x 256 weight rows of one
+// One block computes a tile of up to 160 tokens x 256 weight rows of one
 // expert:
 //   up   : 128 gate rows and the same 128 up rows of the expert, K = H; the
 //          epilogue forms h = silu(G) * U and stores it as f16.
@@ -9,9 +9,11 @@
 // Four waves, one per SIMD.  Wave w owns every token row of the tile and 64
 // weight rows, so each weight value is dequantised exactly once per tile, in
 // the registers of the wave that multiplies it (f16, d * q rounded once), and
-// the 256 x 64 f32 accumulators live in the wave's AGPRs
+// the 160 x 64 f32 accumulators live in the wave's AGPRs
 // (V_MFMA_F32_32X32X16_F16).  An expert's tokens normally fit one tile, so a
-// weight row is dequantised once per expert.
+// weight row is dequantised once per expert.  160 tokens (not more) leaves
+// LDS room for a deep ring: a step multiplies in ~0.4 us while a weight load
+// from HBM takes ~2 us under load, so loads run several steps ahead.
 //
 // Operands reach LDS by DMA (global_load_lds), never through VGPRs:
 //   activations  16-byte chunks of each token row; the chunk index is XORed
@@ -20,8 +22,9 @@
 //   weights      the raw bytes of two quantised blocks per row per K step, in
 //                per-wave regions (32 rows each) that only the owning wave
 //                reads.
-// A three-stage ring keeps the loads of two K steps in flight behind the step
-// being multiplied.  The DMAs are issued from inline assembly, because the
+// An NS-stage ring (5 stages for Q4_0, 4 for Q5_0/Q8_0: as many as LDS
+// holds) keeps the loads of NS - 1 K steps in flight behind the step being
+// multiplied.  The DMAs are issued from inline assembly, because the
 // compiler makes every LDS read that follows an LDS DMA wait for all
 // outstanding loads; the kernel instead waits with exact vmcnt counts: in the
 // middle of step s a wave waits for its own loads of step s + 1 and
@@ -41,10 +44,10 @@ namespace {
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 typedef float floatx16 __attribute__((ext_vector_type(16)));
 
-constexpr int BM = 256;              // tokens per tile
+constexpr int BM = 160;              // tokens per tile
+constexpr int MTMAX = BM / 32;       // 32-token MFMA tiles per block tile
 constexpr int BW = 256;              // weight rows per tile (up: 128 gate + 128 up rows)
 constexpr int BK = 64;               // K values per step (two 32-value blocks)
-constexpr int NS = 3;                // LDS ring stages
 constexpr int A_STAGE = BM * BK * 2;  // bytes of activations per stage
 
 __device__ inline uint32_t alignb(uint32_t hi, uint32_t lo, uint32_t s) { return __builtin_amdgcn_alignbyte(hi, lo, s); }
@@ -115,10 +118,21 @@ struct BLay {
                            : (uint32_t)(xbytes + 128 * (d - 4 * nx4) + 4 * r);
     }
 };
+// Ring stages per format: as many as fit in the 160 KiB of LDS.
+template <int DT>
+constexpr int ring_stages() {
+    return (160 * 1024 - 2 * BM * 4) / (A_STAGE + BLay<DT>::stage);
+}
 template <int DT>
 constexpr int lds_bytes() {
-    return NS * (A_STAGE + BLay<DT>::stage) + 2 * BM * 4;
+    return ring_stages<DT>() * (A_STAGE + BLay<DT>::stage) + 2 * BM * 4;
 }
+static_assert(ring_stages<MOE_DT_Q4_0>() == 5 && ring_stages<MOE_DT_Q5_0>() == 4 &&
+                  ring_stages<MOE_DT_Q8_0>() == 4,
+              "ring depth per format");
+static_assert(lds_bytes<MOE_DT_Q4_0>() <= 160 * 1024 && lds_bytes<MOE_DT_Q5_0>() <= 160 * 1024 &&
+                  lds_bytes<MOE_DT_Q8_0>() <= 160 * 1024,
+              "LDS budget");
 
 // ---- LDS DMA and exact waits ------------------------------------------------
 // global_load_lds writes lane l's 16 (or 4) bytes to LDS address m0 + 16 l
@@ -296,6 +310,7 @@ __device__ inline bool tile_of(const MfmaArgs &a, int mode, int gx, TileInfo &ti
 template <int DT, bool UP>
 __global__ __launch_bounds__(256, 1) void mfma_kernel(MfmaArgs a, int mode, int gx, int ksplit) {
     using BL = BLay<DT>;
+    constexpr int NS = ring_stages<DT>();
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
     int *src_row = reinterpret_cast<int *>(smem + NS * (A_STAGE + BL::stage));
     int *dst_row = src_row + BM;
@@ -317,7 +332,7 @@ __global__ __launch_bounds__(256, 1) void mfma_kernel(MfmaArgs a, int mode, int 
     const int valid = min(BM, ti.n - ti.m0);
     const int mt = (valid + 31) / 32;
 
-    {
+    if (tid < BM) {
         int s = -1, d = -1;
         if (tid < valid) {
             d = ti.row0 + ti.m0 + tid;
@@ -374,9 +389,9 @@ __global__ __launch_bounds__(256, 1) void mfma_kernel(MfmaArgs a, int mode, int 
     const uint32_t brow_x = 16u * l32;                 // row l32's X part within a region
     const uint32_t brow_d = BL::xbytes + 4u * l32;     // and its D part
 
-    floatx16 acc[8][2];
+    floatx16 acc[MTMAX][2];
 #pragma unroll
-    for (int t = 0; t < 8; t++)
+    for (int t = 0; t < MTMAX; t++)
 #pragma unroll
         for (int j = 0; j < 2; j++) acc[t][j] = floatx16{};
 
@@ -490,29 +505,34 @@ __global__ __launch_bounds__(256, 1) void mfma_kernel(MfmaArgs a, int mode, int 
         constexpr int MA = MT / 2;  // activation DMAs in group 0; the rest in group 1
 
         const lds_p smB = sm + NS * A_STAGE;
-        dma_range(I0{}, std::integral_constant<int, ND>{}, 0, 0);
-        dma_range(I0{}, std::integral_constant<int, ND>{}, 1, 1);
-        wait_vm_barrier<ND>();
+        // Prologue: steps 0 .. NS - 2 into stages 0 .. NS - 2, then wait for
+        // step 0.
+        for (int p = 0; p < NS - 1; p++) dma_range(I0{}, std::integral_constant<int, ND>{}, p, p);
+        wait_vm_barrier<(NS - 2) * ND>();
         read_a(sm, 0, af[0]);
         read_rows(smB);
         dequant_raw(I0{}, bq[0]);
         int st = 0;
-        // Per step, this wave's loads of step s + 2 go out in order: the
-        // activation DMAs in groups 0 and 1, the weight DMAs in group 3.  The
-        // wait in group 2 therefore leaves exactly the MT activation DMAs of
-        // step s + 2 outstanding.
+        // Per step, this wave's loads of step s + NS - 1 go out in order: the
+        // activation DMAs in groups 0 and 1, the weight DMAs in group 3, into
+        // the stage step s - 1 used.  At the wait in group 2 this wave's
+        // outstanding loads are those of steps s + 1 .. s + NS - 2 (ND each)
+        // and the MT activation DMAs of step s + NS - 1; leaving all but step
+        // s + 1's outstanding completes step s + 1.
+        constexpr int WAIT = (NS - 3) * ND + MT;
+        static_assert((NS - 1) * ND < 64 && WAIT >= 0, "vmcnt range");
         for (int s = 0; s < nsteps; s++) {
             const lds_p sa = sm + st * A_STAGE;
-            const int st1 = st == 2 ? 0 : st + 1, st2 = st == 0 ? 2 : st - 1;
+            const int st1 = st + 1 == NS ? 0 : st + 1, stn = st == 0 ? NS - 1 : st - 1;
+            const int sn = s + NS - 1;
             // g = 0 (kb 0, m 0): group 1's activations first.
             read_a(sa, 1, af[1]);
             __builtin_amdgcn_sched_barrier(0);
-            mfmas_dma(af[0], bq[0], 0, I0{}, std::integral_constant<int, MA>{}, s + 2, st2);
+            mfmas_dma(af[0], bq[0], 0, I0{}, std::integral_constant<int, MA>{}, sn, stn);
             // g = 1 (kb 0, m 1): dequantise block 1, read group 2.
             dequant_raw(I1{}, bq[1]);
             read_a(sa, 2, af[0]);
-            mfmas_dma(af[1], bq[0], 1, std::integral_constant<int, MA>{}, std::integral_constant<int, MT>{}, s + 2,
-                      st2);
+            mfmas_dma(af[1], bq[0], 1, std::integral_constant<int, MA>{}, std::integral_constant<int, MT>{}, sn, stn);
             __builtin_amdgcn_sched_barrier(0);
             // g = 2 (kb 1, m 0): read group 3; then wait for this wave's
             // loads of step s + 1 and meet the other waves, after which step
@@ -520,30 +540,27 @@ __global__ __launch_bounds__(256, 1) void mfma_kernel(MfmaArgs a, int mode, int 
             read_a(sa, 3, af[1]);
             mfmas(af[0], bq[1], 0);
             __builtin_amdgcn_sched_barrier(0);
-            wait_vm_barrier<MT>();
+            wait_vm_barrier<WAIT>();
             __builtin_amdgcn_sched_barrier(0);
             // g = 3 (kb 1, m 1): step s + 1's group 0 and weight rows; step
-            // s + 2's weight DMAs.
+            // s + NS - 1's weight DMAs.
             const lds_p sa1 = sm + st1 * A_STAGE;
             read_a(sa1, 0, af[0]);
             read_rows(smB + st1 * BL::stage);
             __builtin_amdgcn_sched_barrier(0);
-            mfmas_dma(af[1], bq[1], 1, std::integral_constant<int, MT>{}, std::integral_constant<int, ND>{}, s + 2,
-                      st2);
+            mfmas_dma(af[1], bq[1], 1, std::integral_constant<int, MT>{}, std::integral_constant<int, ND>{}, sn, stn);
             dequant_raw(I0{}, bq[0]);
             __builtin_amdgcn_sched_barrier(0);
             st = st1;
         }
     };
+    static_assert(MTMAX == 5, "one case per 32-token tile count");
     switch (mt) {
     case 1: run(std::integral_constant<int, 1>{}); break;
     case 2: run(std::integral_constant<int, 2>{}); break;
     case 3: run(std::integral_constant<int, 3>{}); break;
     case 4: run(std::integral_constant<int, 4>{}); break;
-    case 5: run(std::integral_constant<int, 5>{}); break;
-    case 6: run(std::integral_constant<int, 6>{}); break;
-    case 7: run(std::integral_constant<int, 7>{}); break;
-    default: run(std::integral_constant<int, 8>{}); break;
+    default: run(std::integral_constant<int, 5>{}); break;
     }
     wait_vm<0>();
 
@@ -553,7 +570,7 @@ __global__ __launch_bounds__(256, 1) void mfma_kernel(MfmaArgs a, int mode, int 
         const int col = n0 + 32 * wv + l32;
         if (col < W0.rows) {
 #pragma unroll
-            for (int t = 0; t < 8; t++) {
+            for (int t = 0; t < MTMAX; t++) {
                 if (t >= mt) continue;
 #pragma unroll
                 for (int v = 0; v < 16; v++) {
@@ -572,7 +589,7 @@ __global__ __launch_bounds__(256, 1) void mfma_kernel(MfmaArgs a, int mode, int 
             const int col = n0 + 64 * wv + 32 * j + l32;
             if (col >= W0.rows) continue;
 #pragma unroll
-            for (int t = 0; t < 8; t++) {
+            for (int t = 0; t < MTMAX; t++) {
                 if (t >= mt) continue;
 #pragma unroll
                 for (int v = 0; v < 16; v++) {

@@ -519,7 +519,7 @@ static GateParams gate_params(const moe_layer *L, int k) {
 // Router, gating and dispatch; shared by forward and route.
 static int route_and_dispatch(moe_layer *L, const float *x, int t, int k, int bm, bool decode, moe_route *routes,
                               uint32_t *hits, const uint32_t *prev, uint64_t *stats, float *logits_out,
-                              hipStream_t s) {
+                              uint16_t *xh, hipStream_t s) {
     Workspace &w = L->ws;
     const int n_rows = L->E + (L->has_shared_gate ? 1 : 0);
     hipError_t e = hipSuccess;
@@ -567,12 +567,13 @@ static int route_and_dispatch(moe_layer *L, const float *x, int t, int k, int bm
         // One token: router, gating and dispatch in a single launch.
         int rc = stage(L, 0, s, [&] {
             e = launch_route_one(L->router, x, n_rows, L->E, L->H, L->temp, w.logits, p, a, w.route_count, s);
+            if (e == hipSuccess && xh) e = launch_to_f16(x, xh, (size_t)L->H, s);
             return e == hipSuccess ? MOE_OK : hip_fail(e, "one-token route kernel");
         });
         return rc ? rc : copy_logits();
     }
     int rc = stage(L, 0, s, [&] {
-        e = launch_router(L->router, x, t, n_rows, L->E, L->H, L->temp, w.logits, s);
+        e = launch_router(L->router, x, t, n_rows, L->E, L->H, L->temp, w.logits, xh, s);
         return e == hipSuccess ? MOE_OK : hip_fail(e, "router kernel");
     });
     if (rc) return rc;
@@ -594,7 +595,8 @@ int moe_layer_route(moe_layer *L, const float *x, int32_t t, moe_route *routes, 
     const int k = effective_k(L);
     int rc = reserve(L, t, k);
     if (rc) return rc;
-    return route_and_dispatch(L, x, t, k, 0, false, routes, nullptr, nullptr, nullptr, logits, (hipStream_t)stream);
+    return route_and_dispatch(L, x, t, k, 0, false, routes, nullptr, nullptr, nullptr, logits, nullptr,
+                              (hipStream_t)stream);
 }
 
 int moe_layer_forward(moe_layer *L, const float *x, int32_t t, float *out, float *residual, moe_route *routes,
@@ -624,7 +626,9 @@ int moe_layer_forward(moe_layer *L, const float *x, int32_t t, float *out, float
     }
     if (path == kMfma && !mfma_fits(t, k, L->H, L->I, L->has_shared ? L->I_s : 0)) path = kGemv;
     const int bm = path == kMfma ? mfma_tile_m() : 0;
-    if ((rc = route_and_dispatch(L, x, t, k, bm, path == kDecode, routes, hits, prev, stats, nullptr, s))) return rc;
+    if ((rc = route_and_dispatch(L, x, t, k, bm, path == kDecode, routes, hits, prev, stats, nullptr,
+                                 path == kMfma ? w.xh : nullptr, s)))
+        return rc;
 
     const ExpertDev &e0 = L->experts_host[0];
     const ExpertDev *sh = L->has_shared ? &L->experts_host[L->E] : nullptr;
@@ -683,7 +687,6 @@ int moe_layer_forward(moe_layer *L, const float *x, int32_t t, float *out, float
             m.ksplit /= 2;
         ksplit = m.ksplit;
         rc = stage(L, 3, s, [&] {
-            if ((e = launch_to_f16(x, w.xh, (size_t)t * L->H, s)) != hipSuccess) return hip_fail(e, "f16 conversion");
             e = launch_mfma(true, m, bm, e0, sh, s);
             return e == hipSuccess ? MOE_OK : hip_fail(e, "MFMA up kernel");
         });

@@ -104,8 +104,9 @@ struct Workspace {
 // Router logits, bit-exact to the reference's dot (src/quant.rs:386-420):
 // logits[t][e] = W[e] . x[t] for e < n_rows, divided by temp (e < E only)
 // when temp > 0.  Row E (if n_rows == E+1) is the shared-expert gate.
+// When xh is given, also writes x rounded to f16 (the MFMA path's operand).
 hipError_t launch_router(const float *W, const float *x, int T, int n_rows, int E, int H, float temp, float *logits,
-                         hipStream_t s);
+                         uint16_t *xh, hipStream_t s);
 
 // Gating + top-k + weights per token (src/model.rs:855-897).
 hipError_t launch_gating(const float *logits, int ld, int T, const GateParams &p, int32_t *sel, float *wsel,

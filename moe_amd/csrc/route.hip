@@ -7,6 +7,8 @@
 // This file is compiled with -ffp-contract=off so that no multiply and add
 // are fused except where fmaf() says so.
 #include <hip/hip_fp16.h>
+#include <cmath>
+#include <algorithm>
 #include <hip/hip_runtime.h>
 
 #include "exact_math.h"
@@ -46,24 +48,28 @@ __device__ inline float dot_tail(float out, const float *a, const float *b, int 
 }
 
 // Copy n floats from global memory to LDS with every thread of the block,
-// eight 16-byte loads in flight per thread before any store.
-__device__ inline void stage_to_lds(const float *__restrict__ src, float *dst, int n) {
+// eight 16-byte loads in flight per thread before any store.  Loads and
+// stores are unconditional (indices past the end re-read and re-write the
+// last vector with its own value), so the compiler cannot sink a load into a
+// branch and serialise the copy.
+__device__ inline void stage_to_lds(const float *__restrict__ src, float *__restrict__ dst, int n) {
     const int tid = threadIdx.x, nt = blockDim.x;
     if ((n & 3) == 0 && (((uintptr_t)src) & 15) == 0) {
         const float4 *s4 = reinterpret_cast<const float4 *>(src);
         float4 *d4 = reinterpret_cast<float4 *>(dst);
         const int n4 = n >> 2;
+        if (n4 == 0) return;
         for (int base = 0; base < n4; base += 8 * nt) {
             float4 v[8];
 #pragma unroll
             for (int u = 0; u < 8; u++) {
                 const int i = base + u * nt + tid;
-                if (i < n4) v[u] = s4[i];
+                v[u] = s4[i < n4 ? i : n4 - 1];
             }
 #pragma unroll
             for (int u = 0; u < 8; u++) {
                 const int i = base + u * nt + tid;
-                if (i < n4) d4[i] = v[u];
+                d4[i < n4 ? i : n4 - 1] = v[u];
             }
         }
     } else {
@@ -71,25 +77,91 @@ __device__ inline void stage_to_lds(const float *__restrict__ src, float *dst, i
     }
 }
 
+// Copy na floats from a and nb floats from b (16-byte aligned, positive
+// multiples of 4) from global memory to LDS, issuing all of a thread's loads
+// (up to U float4 from each source) before its first store: one memory
+// round trip per U * blockDim.x float4 of each source.  The sources are rows
+// of len4 float4; in LDS consecutive rows start stride4 float4 apart.
+// Indices past the end re-read and re-write the last vector, so no access is
+// conditional.
+template <int U>
+__device__ inline void stage2_to_lds(const float *__restrict__ a, float *__restrict__ da, int na,
+                                     const float *__restrict__ b, float *__restrict__ db, int nb, int len4,
+                                     int stride4) {
+    const int tid = threadIdx.x, nt = blockDim.x;
+    const float4 *a4 = reinterpret_cast<const float4 *>(a);
+    const float4 *b4 = reinterpret_cast<const float4 *>(b);
+    const int na4 = na >> 2, nb4 = nb >> 2;
+    const int n4 = na4 > nb4 ? na4 : nb4;
+    auto dst = [&](int i) { return (i / len4) * stride4 + i % len4; };
+    for (int base = 0; base < n4; base += U * nt) {
+        float4 va[U], vb[U];
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            const int i = base + u * nt + tid;
+            va[u] = a4[i < na4 ? i : na4 - 1];
+            vb[u] = b4[i < nb4 ? i : nb4 - 1];
+        }
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            const int i = base + u * nt + tid;
+            reinterpret_cast<float4 *>(da)[dst(i < na4 ? i : na4 - 1)] = va[u];
+            reinterpret_cast<float4 *>(db)[dst(i < nb4 ? i : nb4 - 1)] = vb[u];
+        }
+    }
+}
+
+__host__ __device__ inline int router_lds_stride(int H) { return (H % 64 == 0) ? H + 16 : H; }
+
 // Latency-bound router: a block stages RB router rows and TB token rows in
 // LDS (the whole of H), then thread (pair, j) runs lane j of dot_avx2 for one
 // (row, token) pair — one chain per thread, read eight steps at a time.
-__global__ __launch_bounds__(256) void router_lds_kernel(const float *__restrict__ W, const float *__restrict__ x,
+// Blocks of the first row range also write the tokens' f16 copy (xh, the
+// MFMA path's activations) from LDS when xh is given.
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 2))) void router_lds_kernel(const float *__restrict__ W, const float *__restrict__ x,
                                                          int T, int n_rows, int E, int H, int RB, int TB, float temp,
-                                                         float *__restrict__ logits) {
-    extern __shared__ float lds[];
+                                                         float *__restrict__ logits, __half *__restrict__ xh) {
+    extern __shared__ __attribute__((aligned(16))) float lds[];
     const int r0 = blockIdx.x * RB, t0 = blockIdx.y * TB;
     const int nr = min(RB, n_rows - r0), nt = min(TB, T - t0);
+    // Rows sit LS floats apart: when H % 64 == 0 the extra 16 floats put
+    // the four rows a wavefront reads at once in different bank groups.
+    const int LS = router_lds_stride(H);
     float *wl = lds;
-    float *xl = lds + (size_t)RB * H;
-    stage_to_lds(W + (size_t)r0 * H, wl, nr * H);
-    stage_to_lds(x + (size_t)t0 * H, xl, nt * H);
+    float *xl = lds + (size_t)RB * LS;
+    const bool vec = (H & 3) == 0 && ((uintptr_t)W & 15) == 0 && ((uintptr_t)x & 15) == 0;
+    if (vec) {
+        stage2_to_lds<16>(W + (size_t)r0 * H, wl, nr * H, x + (size_t)t0 * H, xl, nt * H, H >> 2, LS >> 2);
+    } else {
+        for (int r = 0; r < nr; r++) stage_to_lds(W + (size_t)(r0 + r) * H, wl + (size_t)r * LS, H);
+        for (int r = 0; r < nt; r++) stage_to_lds(x + (size_t)(t0 + r) * H, xl + (size_t)r * LS, H);
+    }
     __syncthreads();
     const int tid = threadIdx.x, j = tid & 15, p = tid >> 4;
+    if (xh && blockIdx.x == 0) {
+        if ((H & 7) == 0) {
+            // Eight values per 16-byte store.
+            const int H8 = H >> 3;
+            for (int i = tid; i < nt * H8; i += blockDim.x) {
+                const int r = i / H8, c = (i % H8) * 8;
+                const float *src = xl + (size_t)r * LS + c;
+                uint4 v;
+                uint32_t *vw = reinterpret_cast<uint32_t *>(&v);
+#pragma unroll
+                for (int q = 0; q < 4; q++)
+                    vw[q] = (uint32_t)__half_as_ushort(__float2half_rn(src[2 * q])) |
+                            ((uint32_t)__half_as_ushort(__float2half_rn(src[2 * q + 1])) << 16);
+                *reinterpret_cast<uint4 *>(xh + (size_t)(t0 + r) * H + c) = v;
+            }
+        } else {
+            for (int i = tid; i < nt * H; i += blockDim.x)
+                xh[(size_t)t0 * H + i] = __float2half_rn(xl[(size_t)(i / H) * LS + i % H]);
+        }
+    }
     if (p >= nr * nt) return;  // whole 16-lane groups leave together
     const int rl = p / nt, tl = p % nt;
-    const float *a = wl + (size_t)rl * H;
-    const float *b = xl + (size_t)tl * H;
+    const float *a = wl + (size_t)rl * LS;
+    const float *b = xl + (size_t)tl * LS;
     const int n16 = H / 16;
     const bool has8 = (H % 16) >= 8;
     float acc = 0.0f;
@@ -125,7 +197,7 @@ constexpr int kTT = 32;   // tokens per tile
 constexpr int kKC = 64;   // K chunk
 __global__ __launch_bounds__(256) void router_tiled_kernel(const float *__restrict__ W, const float *__restrict__ x,
                                                            int T, int n_rows, int E, int H, float temp,
-                                                           float *__restrict__ logits) {
+                                                           float *__restrict__ logits, __half *__restrict__ xh) {
     __shared__ __attribute__((aligned(16))) float wt[kRT][kKC + 4];
     __shared__ __attribute__((aligned(16))) float xt[kTT][kKC + 4];
     const int tid = threadIdx.x, j = tid & 15, g = tid >> 4;
@@ -168,6 +240,15 @@ __global__ __launch_bounds__(256) void router_tiled_kernel(const float *__restri
             const int q = tid + 256 * u, rr = q >> 4, kk = (q & 15) * 4;
             *reinterpret_cast<float4 *>(&wt[rr][kk]) = pw[u];
             *reinterpret_cast<float4 *>(&xt[rr][kk]) = px[u];
+            // The first row range writes the f16 copy (launched only when
+            // the chunks cover all of H, i.e. H % 16 == 0).
+            if (xh && blockIdx.x == 0 && t0 + rr < T && k0 + kk < kfull) {
+                __half *o = xh + (size_t)(t0 + rr) * H + k0 + kk;
+                o[0] = __float2half_rn(px[u].x);
+                o[1] = __float2half_rn(px[u].y);
+                o[2] = __float2half_rn(px[u].z);
+                o[3] = __float2half_rn(px[u].w);
+            }
         }
         __syncthreads();
         if (k0 + kKC < kfull) load_chunk(k0 + kKC);
@@ -762,7 +843,7 @@ __device__ void dispatch_one(const DispatchArgs &a, const int *idx, const float 
 // atomic after a release fence, gates the token and dispatches it.  The
 // counter is returned to zero by that block, and no block waits on another.
 template <int EPL>
-__global__ __launch_bounds__(kDispatchThreads) void route_one_kernel(const float *__restrict__ W,
+__global__ __launch_bounds__(kDispatchThreads) __attribute__((amdgpu_waves_per_eu(1, 2))) void route_one_kernel(const float *__restrict__ W,
                                                                      const float *__restrict__ x, int n_rows, int E,
                                                                      int H, float temp, float *__restrict__ logits,
                                                                      GateParams p, DispatchArgs d,
@@ -771,8 +852,12 @@ __global__ __launch_bounds__(kDispatchThreads) void route_one_kernel(const float
     __shared__ GateScratch<EPL> S;
     __shared__ int s_last;
     const int r = blockIdx.x;
-    stage_to_lds(W + (size_t)r * H, lds, H);
-    stage_to_lds(x, lds + H, H);
+    if ((H & 3) == 0 && ((uintptr_t)W & 15) == 0 && ((uintptr_t)x & 15) == 0) {
+        stage2_to_lds<4>(W + (size_t)r * H, lds, H, x, lds + H, H, H >> 2, H >> 2);
+    } else {
+        stage_to_lds(W + (size_t)r * H, lds, H);
+        stage_to_lds(x, lds + H, H);
+    }
     __syncthreads();
     if (threadIdx.x < 16) {
         const int j = threadIdx.x;
@@ -831,28 +916,53 @@ __global__ void to_f16_kernel(const float *__restrict__ x, __half *__restrict__ 
 }  // namespace
 
 hipError_t launch_router(const float *W, const float *x, int T, int n_rows, int E, int H, float temp, float *logits,
-                         hipStream_t s) {
-    const size_t row_bytes = (size_t)H * 4;
-    const size_t budget = 64 * 1024;
-    // Latency kernel: grow the (rows x tokens) block tile while the grid is
-    // larger than two blocks per CU and the tile still fits in LDS.
-    int RB = 1, TB = 1;
-    auto blocks = [&] { return (long long)((n_rows + RB - 1) / RB) * ((T + TB - 1) / TB); };
-    while (blocks() > 512) {
-        if (TB < T && (size_t)(RB + 2 * TB) * row_bytes <= budget && RB * 2 * TB <= 16)
-            TB *= 2;
-        else if (RB < n_rows && (size_t)(2 * RB + TB) * row_bytes <= budget && 2 * RB * TB <= 16)
-            RB *= 2;
-        else
-            break;
-    }
-    if ((size_t)(RB + TB) * row_bytes <= budget && blocks() <= 4096) {
+                         uint16_t *xh_raw, hipStream_t s) {
+    __half *xh = reinterpret_cast<__half *>(xh_raw);
+    const double budget = 160.0 * 1024;
+    const double clk_us = 2400.0;  // cycles per microsecond
+    // Cost model (microseconds) of the row-staging kernel for an RB x TB
+    // tile: per round of resident blocks, one memory round trip (~1 us) per
+    // 16 float4 per thread, the staged bytes through each CU at ~64 B per
+    // cycle, and the H/16-step chain at ~10 cycles per step.
+    int best_rb = 0, best_tb = 0;
+    double best = 1e30;
+    for (int RB = 1; RB <= 16 && RB < 2 * n_rows; RB *= 2)
+        for (int TB = 1; RB * TB <= 16 && TB < 2 * T; TB *= 2) {
+            const double lds = (RB + TB) * (double)router_lds_stride(H) * 4;
+            if (lds > budget) continue;
+            const long long blocks = (long long)((n_rows + RB - 1) / RB) * ((T + TB - 1) / TB);
+            int per_cu = (int)(budget / lds);
+            if (per_cu > 8) per_cu = 8;
+            const double rounds = std::ceil((double)blocks / (256.0 * per_cu));
+            const double trips = std::ceil((double)std::max(RB, TB) * H / 4 / (16 * 256));
+            const double t = rounds * (trips + per_cu * lds / 64.0 / clk_us + (H / 16) * 10.0 / clk_us);
+            if (t < best) best = t, best_rb = RB, best_tb = TB;
+        }
+    // The tiled kernel: 32 x 32 tiles, about three blocks per CU, ~1150
+    // cycles per 64-value K chunk.
+    const double tiled_blocks = (double)((n_rows + kRT - 1) / kRT) * ((T + kTT - 1) / kTT);
+    const double tiled = std::ceil(tiled_blocks / (256.0 * 3)) * (H / 64.0) * 1150.0 / clk_us;
+    if (best_rb > 0 && best <= tiled) {
+        const int RB = best_rb, TB = best_tb;
         dim3 grid((n_rows + RB - 1) / RB, (T + TB - 1) / TB);
-        const size_t lds = (size_t)(RB + TB) * row_bytes;
-        hipLaunchKernelGGL(router_lds_kernel, grid, dim3(256), lds, s, W, x, T, n_rows, E, H, RB, TB, temp, logits);
+        const size_t lds = (size_t)(RB + TB) * router_lds_stride(H) * 4;
+        static bool raised = false;
+        if (!raised) {
+            (void)hipFuncSetAttribute((const void *)router_lds_kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                      160 * 1024);
+            raised = true;
+        }
+        hipLaunchKernelGGL(router_lds_kernel, grid, dim3(256), lds, s, W, x, T, n_rows, E, H, RB, TB, temp, logits,
+                           xh);
     } else {
         dim3 grid((n_rows + kRT - 1) / kRT, (T + kTT - 1) / kTT);
-        hipLaunchKernelGGL(router_tiled_kernel, grid, dim3(256), 0, s, W, x, T, n_rows, E, H, temp, logits);
+        hipLaunchKernelGGL(router_tiled_kernel, grid, dim3(256), 0, s, W, x, T, n_rows, E, H, temp, logits,
+                           (H % 16 == 0) ? xh : nullptr);
+        if (xh && H % 16 != 0) {
+            hipError_t e = hipGetLastError();
+            if (e != hipSuccess) return e;
+            return launch_to_f16(x, xh_raw, (size_t)T * H, s);
+        }
     }
     return hipGetLastError();
 }

@@ -15,8 +15,9 @@
 //    with several rows' weights in flight; each block first encodes x into
 //    LDS.
 //  * decode_down_kernel: a block owns ranges of output rows and one group of
-//    waves per selected expert; it encodes the experts' h into LDS, streams
-//    their down rows and combines each row in LDS: out = sum over the
+//    waves per selected expert; each lane encodes its units of the experts'
+//    h (f32) in registers, streams their down rows and combines each row in
+//    LDS: out = sum over the
 //    selected experts in ascending order of w * y, from +0, separate
 //    multiply and add (src/model.rs:842, 936-942); plus the shared expert
 //    times its sigmoid gate (src/model.rs:956-970); plus the residual add
@@ -311,33 +312,13 @@ __global__ __launch_bounds__(256) void decode_up_kernel(DecodeArgs a, const floa
     }
 }
 
-// --------------------------------------------------------------- h
-//
-// Encodes every task's h (f32, written by the gate/up kernel) as units, one
-// 32-value block per thread: task t's units start at unit t * I / 64, the
-// shared expert's at k_bound * I / 64.
-__global__ __launch_bounds__(256) void encode_h_kernel(DecodeArgs a, uint8_t *__restrict__ hq) {
-    const int blk_r = a.I / 32;
-    const int n_blk = a.k_bound * blk_r + a.n_shared * (a.I_s / 32);
-    const int b = blockIdx.x * 256 + threadIdx.x;
-    if (b >= n_blk) return;
-    const int t = b < a.k_bound * blk_r ? b / blk_r : a.k_bound;
-    const DecodeTask &T = a.tasks[t];
-    if (!T.live) return;
-    const int i = b - t * blk_r;  // block within the task
-    float v[32];
-    load32(T.h + (size_t)i * 32, v);
-    qact_block_put<1>(qact_block(v), hq + (size_t)(b >> 1) * kQUnitBytes, b & 1);
-}
-
 // --------------------------------------------------------------- down
 //
 // A block owns output row ranges r = blockIdx.x, + gridDim.x, ... of `rb`
 // rows and one group of waves per task: routed task i (the i-th selected
 // expert, ascending) owns waves [i * ks_r, (i + 1) * ks_r), the shared
-// expert the ks_s waves after them.  The block first encodes every task's h
-// into LDS (while the weights of its first ranges load); each wave then
-// keeps its unit of its task's h in registers and streams the task's down
+// expert the ks_s waves after them.  Each lane first encodes its unit of its
+// task's h (f32) into registers; each wave then streams the task's down
 // rows of each range, NBUF - 1 ranges ahead.  Row slices leave their sums in
 // LDS; after a barrier the block combines each row in the reference's
 // order.  Lanes own one unit (UPL = 1: CG lanes per row slice, 64 / CG slices
@@ -432,7 +413,7 @@ __device__ inline void down_combine(const DecodeArgs &a, const DecodeTask *tasks
 }
 
 template <int DT_R, int DT_S, int UPL, int RS, int NBUF, int NTHR>
-__global__ __launch_bounds__(NTHR) void decode_down_kernel(DecodeArgs a, const uint8_t *__restrict__ hq, int rb,
+__global__ __launch_bounds__(NTHR) void decode_down_kernel(DecodeArgs a, int rb,
                                                            int ks_r, int ks_s, int n_ranges) {
     __shared__ float part[2][kDecodeMaxWaves][32][4];
     __shared__ DecodeTask tasks[kDecodeMaxWaves];
@@ -451,14 +432,15 @@ __global__ __launch_bounds__(NTHR) void decode_down_kernel(DecodeArgs a, const u
         down_lane<DT_S>(tasks, a.k_bound, wv, ks_r, ks_s, rb, L);
     else
         down_lane<DT_R>(tasks, a.k_bound, wv, ks_r, ks_s, rb, L);
-    // The lane's units of its task's encoded h first, then the weights.
+    // The lane encodes its units of its task's h (f32, from the gate/up
+    // kernel) itself, before its weights stream.
     uint32_t xa[UPL][kQUnitDw];
     if (L.active) {
-        const uint8_t *hu = hq + (size_t)L.task * (a.I / 64) * kQUnitBytes;
+        const float *hv = tasks[L.task].h;
         const int u0 = L.kw * 64 + (threadIdx.x & 63) % L.cg;
 #pragma unroll
         for (int j = 0; j < UPL; j++)
-            if (L.live[j]) load_qunit<1>(hu + (size_t)(u0 + 64 * j) * kQUnitBytes, xa[j]);
+            if (L.live[j]) qact_unit_from_f32(hv + (size_t)(u0 + 64 * j) * 64, xa[j]);
     }
     uint32_t w[NBUF][RS][UPL][DW];
     auto load = [&](int it, uint32_t (&buf)[RS][UPL][DW]) {
@@ -623,18 +605,12 @@ hipError_t launch_decode_up(const DecodeArgs &a, const float *x, int dt_routed, 
     return go(dt_shared, sh, a.I_s / slices, 1);
 }
 
-hipError_t launch_decode_down(const DecodeArgs &a, uint8_t *hq, int dt_routed, int dt_shared, hipStream_t s) {
+hipError_t launch_decode_down(const DecodeArgs &a, int dt_routed, int dt_shared, hipStream_t s) {
     const int ur = a.I / 64, us = a.n_shared ? a.I_s / 64 : ur;
     const int upl = upl_of(ur);
     const int ks_r = down_ks(ur), ks_s = a.n_shared ? down_ks(us) : 1;
     const int waves = a.k_bound * ks_r + a.n_shared * ks_s;
     if (waves > kDecodeMaxWaves || (a.n_shared && upl_of(us) != upl)) return hipErrorInvalidValue;
-    {
-        const int n_blk = a.k_bound * (a.I / 32) + a.n_shared * (a.I_s / 32);
-        hipLaunchKernelGGL(encode_h_kernel, dim3((n_blk + 255) / 256), dim3(256), 0, s, a, hq);
-        const hipError_t e = hipGetLastError();
-        if (e != hipSuccess) return e;
-    }
     const bool big = waves > 8;
     const int ns_r = down_slices(ur), ns_s = a.n_shared ? down_slices(us) : ns_r;
     const int lo = std::min(ns_r, ns_s), hi = std::max(ns_r, ns_s);
@@ -648,7 +624,7 @@ hipError_t launch_decode_down(const DecodeArgs &a, uint8_t *hq, int dt_routed, i
     auto launch = [&](auto kern) -> hipError_t {
         const int per_cu = occupancy((const void *)kern, threads, 0);
         const int nb = std::max(1, std::min(n_ranges, cus_of_current_device() * per_cu));
-        hipLaunchKernelGGL(kern, dim3(nb), dim3(threads), 0, s, a, hq, rb, ks_r, ks_s, n_ranges);
+        hipLaunchKernelGGL(kern, dim3(nb), dim3(threads), 0, s, a, rb, ks_r, ks_s, n_ranges);
         return hipGetLastError();
     };
 #define MOE_DOWN_RS(R, S, U, N)                                                                                        \

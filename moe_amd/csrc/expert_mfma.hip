@@ -308,7 +308,7 @@ __device__ inline bool tile_of(const MfmaArgs &a, int mode, int gx, TileInfo &ti
 }
 
 template <int DT, bool UP>
-__global__ __launch_bounds__(256, 1) void mfma_kernel(MfmaArgs a, int mode, int gx, int ksplit) {
+__global__ __launch_bounds__(256, 1) __attribute__((amdgpu_waves_per_eu(1, 1))) void mfma_kernel(MfmaArgs a, int mode, int gx, int ksplit) {
     using BL = BLay<DT>;
     constexpr int NS = ring_stages<DT>();
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];

@@ -209,7 +209,6 @@ int reserve(moe_layer *L, int max_t, int k) {
         {(void **)&w.hits, (E + 2) * 4},
         {(void **)&w.tiles, 4 * max_tiles * 4},
         {(void **)&w.dtasks, (size_t)(k + 1) * sizeof(DecodeTask)},
-        {(void **)&w.hq, ((size_t)k * (I / 64) + Is / 64 + 1) * kQUnitBytes},
         {(void **)&w.route_count, 4},
         {(void **)&w.ntiles, 4},
         {(void **)&w.xh, T * H * 2},
@@ -656,7 +655,7 @@ int moe_layer_forward(moe_layer *L, const float *x, int32_t t, float *out, float
         });
         if (rc) return rc;
         return stage(L, 4, s, [&] {
-            e = launch_decode_down(d, w.hq, dt_r, dt_s, s);
+            e = launch_decode_down(d, dt_r, dt_s, s);
             return e == hipSuccess ? MOE_OK : hip_fail(e, "one-token down kernel");
         });
     }

@@ -84,7 +84,6 @@ struct Workspace {
     int32_t *hits = nullptr;      // [E+2] n, then experts ascending
     int32_t *tiles = nullptr;     // [4 * max_tiles] (group, m0, group's first tile, group's tiles) for the MFMA path
     DecodeTask *dtasks = nullptr; // [k + 1] one-token task table
-    uint8_t *hq = nullptr;        // [k * I / 64 + I_s / 64] units of h (one-token path)
     unsigned *route_count = nullptr;  // [1] finished router blocks (one-token route), zero between calls
     int32_t *ntiles = nullptr;    // [1]
     uint16_t *xh = nullptr;       // [T, H] f16 activations (MFMA path)
@@ -192,9 +191,8 @@ constexpr int kDecodeMaxWaves = 16;  // waves of a down-projection block
 bool decode_supported(int H, int I, int I_s, int dt_routed, int dt_shared);
 bool decode_fits(int I, int I_s, int k, int has_shared, int dt_routed, int dt_shared);
 hipError_t launch_decode_up(const DecodeArgs &a, const float *x, int dt_routed, int dt_shared, hipStream_t s);
-// Encodes h (into hq: [(k + 1) * max(I, I_s) / 64] units) and runs the down
-// projection and combine.
-hipError_t launch_decode_down(const DecodeArgs &a, uint8_t *hq, int dt_routed, int dt_shared, hipStream_t s);
+// The down projection and combine; every lane encodes its own units of h.
+hipError_t launch_decode_down(const DecodeArgs &a, int dt_routed, int dt_shared, hipStream_t s);
 
 // Prefill-path grouped GEMMs on MFMA (f16 operands, f32 accumulation).
 struct MfmaArgs {

@@ -987,11 +987,7 @@ hipError_t launch_route_one(const float *W, const float *x, int n_rows, int E, i
                             const GateParams &p, const DispatchArgs &d, unsigned *counter, hipStream_t s) {
     const size_t lds = (size_t)2 * H * 4;
     auto go = [&](auto kern) {
-        static bool raised = false;  // dynamic LDS beside the static dispatch tables
-        if (!raised) {
-            (void)hipFuncSetAttribute((const void *)kern, hipFuncAttributeMaxDynamicSharedMemorySize, 64 * 1024);
-            raised = true;
-        }
+        (void)hipFuncSetAttribute((const void *)kern, hipFuncAttributeMaxDynamicSharedMemorySize, 64 * 1024);
         hipLaunchKernelGGL(kern, dim3(n_rows), dim3(kDispatchThreads), lds, s, W, x, n_rows, E, H, temp, logits, p,
                            d, counter);
         return hipGetLastError();

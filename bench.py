@@ -142,6 +142,62 @@ def copy_calibration(mib: int) -> int:
     return 0
 
 
+TRAFFIC_FILE = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", "mixtral_layer_traffic.json")
+
+
+def summarize_pmc(fetch_dir: str, write_dir: str, out_json: str) -> int:
+    """Turn two rocprofv3 counter passes (FETCH_SIZE, WRITE_SIZE; each
+    directory holding bench_counter_collection.csv from this bench and
+    copy_counter_collection.csv from --copy-calibration) into HBM bytes per
+    launch for every kernel, scaled by what each counter reads for the
+    copy: a copy of C KiB should fetch and write C KiB each."""
+    import csv
+    import re
+
+    def per_kernel(path):
+        acc = {}
+        for r in csv.DictReader(open(path)):
+            m = re.search(r"::(\w+_kernel(<[^>]*>)?)", r["Kernel_Name"])
+            name = m.group(1) if m else r["Kernel_Name"][:60]
+            acc.setdefault((name, int(r["Grid_Size"])), []).append(float(r["Counter_Value"]))
+        return {k: sum(v) / len(v) for k, v in acc.items()}
+
+    def copy_factor(path, mib):
+        vals = [float(r["Counter_Value"]) for r in csv.DictReader(open(path)) if "copyBuffer" in r["Kernel_Name"]]
+        return (mib * 1024.0) / (sum(vals) / len(vals))
+
+    mib = 512
+    ff = copy_factor(os.path.join(fetch_dir, "copy_counter_collection.csv"), mib)
+    wf = copy_factor(os.path.join(write_dir, "copy_counter_collection.csv"), mib)
+    fetch = per_kernel(os.path.join(fetch_dir, "bench_counter_collection.csv"))
+    write = per_kernel(os.path.join(write_dir, "bench_counter_collection.csv"))
+    kernels = []
+    for (name, grid), fk in sorted(fetch.items()):
+        wk = write.get((name, grid), 0.0)
+        kernels.append(dict(kernel=name, grid=grid, fetch_kib=round(fk, 1), write_kib=round(wk, 1),
+                            hbm_bytes=round((fk * ff + wk * wf) * 1024)))
+    doc = dict(source="rocprofv3 --pmc FETCH_SIZE, then WRITE_SIZE, over `bench.py --no-cpu --steps 3 --warmup 1` "
+                      f"and `bench.py --copy-calibration {mib}`",
+               fetch_factor=round(ff, 4), write_factor=round(wf, 4), kernels=kernels)
+    with open(out_json, "w") as f:
+        json.dump(doc, f, indent=1)
+    print(json.dumps(dict(written=out_json, fetch_factor=ff, write_factor=wf, kernels=len(kernels))))
+    return 0
+
+
+def traffic_of(kernel_prefix: str):
+    """HBM bytes per launch of the first kernel whose name starts with
+    kernel_prefix, from the committed counter summary (None if absent)."""
+    try:
+        doc = json.load(open(TRAFFIC_FILE))
+    except (OSError, ValueError):
+        return None
+    for k in doc["kernels"]:
+        if k["kernel"].startswith(kernel_prefix):
+            return k["hbm_bytes"]
+    return None
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
@@ -153,6 +209,8 @@ def main() -> int:
     ap.add_argument("--copies", type=int, default=4, help="distinct weight copies cycled through")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--summarize-pmc", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
+                    help="write the HBM traffic summary from two rocprofv3 counter passes and exit")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="only copy MIB MiB device-to-device 5 times (a plain copy kernel of known size, the "
                          "reference point for the FETCH_SIZE / WRITE_SIZE counters) and exit")
@@ -163,6 +221,8 @@ def main() -> int:
         return 2
     if args.copy_calibration:
         return copy_calibration(args.copy_calibration)
+    if args.summarize_pmc:
+        return summarize_pmc(args.summarize_pmc[0], args.summarize_pmc[1], TRAFFIC_FILE)
 
     import torch
 
@@ -235,14 +295,14 @@ def main() -> int:
                    "weight_copies": args.copies},
         "roofline": {"bound": "mfma", "kernel": "expert gate/up (MFMA grouped GEMM)",
                      "achieved": round(achieved, 2), "peak": MFMA_F16_PEAK_TFLOPS, "unit": "TFLOP/s",
-                     "frac": round(achieved / MFMA_F16_PEAK_TFLOPS, 4), "traffic": None,
+                     "frac": round(achieved / MFMA_F16_PEAK_TFLOPS, 4), "traffic": traffic_of("mfma_kernel<2, true>"),
                      "layer_frac": round(layer_tflops / MFMA_F16_PEAK_TFLOPS, 4)},
         "cpu_baseline": cpu,
         "decode": {"tokens": args.decode_tokens, "value": round(args.decode_tokens / (td["ms"] * 1e-3), 1),
                    "unit": "tokens/s", "ms_per_step": round(td["ms"], 5), "dtype": "f32",
                    "roofline": {"bound": "hbm", "kernel": "expert gate/up (GEMV)", "achieved": round(dec_gbs, 1),
                                 "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(dec_gbs / HBM_PEAK_GBS, 4),
-                                "traffic": None, "layer_frac": round(layer_gbs / HBM_PEAK_GBS, 4)},
+                                "traffic": traffic_of("decode_up_kernel"), "layer_frac": round(layer_gbs / HBM_PEAK_GBS, 4)},
                    "stages_us": {k_: round(v * 1e3, 2) for k_, v in td["stages"].items()}},
         "stages_us": {k_: round(v * 1e3, 2) for k_, v in tp["stages"].items()},
     }

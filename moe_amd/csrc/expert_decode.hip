@@ -434,10 +434,16 @@ __global__ __launch_bounds__(NTHR) void decode_down_kernel(DecodeArgs a, int rb,
         down_lane<DT_R>(tasks, a.k_bound, wv, ks_r, ks_s, rb, L);
     // The lane encodes its units of its task's h (f32, from the gate/up
     // kernel) itself, before its weights stream.
+    // With one unit per lane its 64 values load first, then the first
+    // ranges' weights, and the encoding runs while those are in flight
+    // (loads retire in order, so waiting for h does not wait for them).
     uint32_t xa[UPL][kQUnitDw];
-    if (L.active) {
-        const float *hv = tasks[L.task].h;
-        const int u0 = L.kw * 64 + (threadIdx.x & 63) % L.cg;
+    const float *hv = tasks[L.task].h;
+    const int u0 = L.kw * 64 + (threadIdx.x & 63) % L.cg;
+    float hraw[64];
+    if constexpr (UPL == 1) {
+        if (L.active && L.live[0]) qact_unit_load(hv + (size_t)u0 * 64, hraw);
+    } else if (L.active) {
 #pragma unroll
         for (int j = 0; j < UPL; j++)
             if (L.live[j]) qact_unit_from_f32(hv + (size_t)(u0 + 64 * j) * 64, xa[j]);
@@ -452,6 +458,8 @@ __global__ __launch_bounds__(NTHR) void decode_down_kernel(DecodeArgs a, int rb,
     };
 #pragma unroll
     for (int b = 0; b + 1 < NBUF; b++) load(b, w[b]);
+    if constexpr (UPL == 1)
+        if (L.active && L.live[0]) qact_unit_encode(hraw, xa[0]);
 
     // Selected experts (live routed tasks come first).
     int nh = 0;

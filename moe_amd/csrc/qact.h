@@ -65,25 +65,35 @@ __device__ inline QBlock qact_block(const float (&v)[32]) {
 }
 
 // A whole unit in registers, laid out as in memory (hi dwords 0..15, lo
-// dwords 16..31, s2 at 32..33, sq at 34..35), encoded from its 64 values at
-// v (16-byte aligned, global memory): the same bits qact_block_put stores.
+// dwords 16..31, s2 at 32..33, sq at 34..35): the same bits qact_block_put
+// stores.  Loading (64 values, 16-byte aligned, global memory) and encoding
+// are separate so a caller can issue other loads in between.
 typedef float qa_f32x4 __attribute__((ext_vector_type(4)));
-__device__ inline void qact_unit_from_f32(const float *v, uint32_t (&x)[kQUnitDw]) {
+__device__ inline void qact_unit_load(const float *v, float (&f)[64]) {
+    const qa_f32x4 *s4 = reinterpret_cast<const qa_f32x4 *>(v);
+#pragma unroll
+    for (int i = 0; i < 16; i++) {
+        const qa_f32x4 t = s4[i];
+        f[4 * i] = t.x, f[4 * i + 1] = t.y, f[4 * i + 2] = t.z, f[4 * i + 3] = t.w;
+    }
+}
+__device__ inline void qact_unit_encode(const float (&f)[64], uint32_t (&x)[kQUnitDw]) {
 #pragma unroll
     for (int b = 0; b < 2; b++) {
-        float f[32];
-        const qa_f32x4 *s4 = reinterpret_cast<const qa_f32x4 *>(v + 32 * b);
+        float v[32];
 #pragma unroll
-        for (int i = 0; i < 8; i++) {
-            const qa_f32x4 t = s4[i];
-            f[4 * i] = t.x, f[4 * i + 1] = t.y, f[4 * i + 2] = t.z, f[4 * i + 3] = t.w;
-        }
-        const QBlock q = qact_block(f);
+        for (int i = 0; i < 32; i++) v[i] = f[32 * b + i];
+        const QBlock q = qact_block(v);
 #pragma unroll
         for (int d = 0; d < 8; d++) x[8 * b + d] = q.hw[d], x[16 + 8 * b + d] = q.lw[d];
         x[32 + b] = __float_as_uint(q.s2);
         x[34 + b] = (uint32_t)q.sq;
     }
+}
+__device__ inline void qact_unit_from_f32(const float *v, uint32_t (&x)[kQUnitDw]) {
+    float f[64];
+    qact_unit_load(v, f);
+    qact_unit_encode(f, x);
 }
 
 // Store an encoded block into a unit (16-byte aligned) through pointers of

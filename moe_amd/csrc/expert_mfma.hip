@@ -280,7 +280,9 @@ __device__ inline bool tile_of(const MfmaArgs &a, int mode, int gx, TileInfo &ti
     const int lin = blockIdx.x + gx * blockIdx.y;
     ti.ksplit = gz > 1 ? (int)blockIdx.z : 0;
     const int mt_sh = (a.T + BM - 1) / BM;
-    const int valid = mode == 1 ? mt_sh * gy : a.ntiles[0] * gy;  // <= total
+    // Routed tiles come first in the tile list, the shared expert's last; a
+    // launch walks only its own (at most gx of them, so valid <= total).
+    const int valid = mode == 1 ? mt_sh * gy : (a.ntiles[0] - a.shared_tiles) * gy;
     // XCD x (= lin mod 8) takes t in [x * per, (x + 1) * per) in order.
     int t = lin;
     if ((total & 7) == 0) {

@@ -677,7 +677,10 @@ int moe_layer_forward(moe_layer *L, const float *x, int32_t t, float *out, float
         m.I = L->I;
         m.I_s = L->I_s;
         m.E = L->E;
+        // Routed tiles: sum over experts of ceil(n_e / bm) <= t k / bm +
+        // (experts with tokens); the shared expert's tiles follow them.
         m.max_tiles = t * k / bm + std::min(L->E, t * k) + 1;
+        m.shared_tiles = L->has_shared ? (t + bm - 1) / bm : 0;
         m.ypart = (size_t)t * k * L->H;
         m.yspart = (size_t)t * L->H;
         m.ksplit = mfma_down_ksplit((t * k + bm - 1) / bm + std::min(L->E, t * k) / 2, L->H, L->I,

@@ -51,6 +51,7 @@ class Shape:
     shared_gate: bool = False
     weight_std: float = 0.02
     router_std: float = 0.02
+    zipf: float = 0.0          # > 0: router rows rescaled so expert popularity follows Zipf(zipf)
 
     def spec(self) -> MoeSpec:
         return MoeSpec(hidden=self.hidden, n_experts=self.n_experts, top_k=self.top_k, sigmoid=self.sigmoid,
@@ -77,6 +78,11 @@ SHAPES = {
     # top-8, scale 2.5, Q4_0 routed experts, one Q5_0 shared expert.
     "deepseek_v3": Shape("deepseek_v3", 7168, 2048, 256, 8, L.DT_Q4_0, sigmoid=True, routed_scale=2.5,
                          n_group=8, topk_group=4, shared_inter=2048, shared_dt=L.DT_Q5_0, e_bias_std=0.1),
+    # configs[3] as benchmarked: router rows skewed so expert popularity is
+    # Zipf(s = 1.1) (see zipf_router_scales).
+    "deepseek_v3_zipf": Shape("deepseek_v3_zipf", 7168, 2048, 256, 8, L.DT_Q4_0, sigmoid=True, routed_scale=2.5,
+                              n_group=8, topk_group=4, shared_inter=2048, shared_dt=L.DT_Q5_0, e_bias_std=0.1,
+                              zipf=1.1),
     # DeepSeek-V2-Lite MoE layer: 64 experts top-6 plus two shared
     # experts loaded as one 2816-wide MLP (src/model.rs:431-439), Q8_0.  The
     # model's own config sets norm_topk_prob false, which the reference reads.
@@ -112,6 +118,79 @@ class HostLayer:
 def _fill(dst: np.ndarray, seed: int, stream: int, dt: int, rows: int, cols: int, mean: float, std: float) -> None:
     rc = L.lib().moe_synth_quantized(seed, stream, dt, rows, cols, mean, std, dst.ctypes.data_as(C.c_void_p))
     L.check(rc, "moe_synth_quantized")
+
+
+STREAM_ZIPF_CAL = 0xB000  # calibration activations of the Zipf skew
+
+
+def zipf_targets(n_experts: int, s: float, total: float, cap: float) -> np.ndarray:
+    """Selections per popularity rank r = 1..E proportional to r^-s, summing to
+    `total`, with no rank above `cap` (the excess spread over the others in
+    proportion, repeatedly)."""
+    w = np.arange(1, n_experts + 1, dtype=np.float64) ** -s
+    t = w / w.sum() * total
+    fixed = np.zeros(n_experts, dtype=bool)
+    for _ in range(n_experts):
+        over = (t > cap) & ~fixed
+        if not over.any():
+            break
+        fixed |= over
+        t[fixed] = cap
+        free = ~fixed
+        t[free] = w[free] / w[free].sum() * (total - cap * fixed.sum())
+    return t
+
+
+def _route_counts(logits: np.ndarray, bias: np.ndarray, shape: Shape) -> np.ndarray:
+    """Selections per expert under the layer's rule (src/model.rs:855-888):
+    sigmoid or softmax scores, + bias, group-limited, top-k; float64, for
+    calibration only."""
+    T, E = logits.shape
+    sc = 1.0 / (1.0 + np.exp(-logits)) if shape.sigmoid else np.exp(logits - logits.max(1, keepdims=True))
+    rank = sc + bias[None, :]
+    if shape.n_group > 1 and shape.topk_group < shape.n_group:
+        per = E // shape.n_group
+        g = rank.reshape(T, shape.n_group, per)
+        gs = np.sort(g, axis=2)[:, :, -2:].sum(axis=2)
+        keep = np.argsort(-gs, axis=1, kind="stable")[:, :shape.topk_group]
+        mask = np.full((T, shape.n_group), -np.inf)
+        np.put_along_axis(mask, keep, 0.0, axis=1)
+        rank = (g + mask[:, :, None]).reshape(T, E)
+    sel = np.argsort(-rank, axis=1, kind="stable")[:, :shape.top_k]
+    return np.bincount(sel.ravel(), minlength=E)
+
+
+def zipf_router_scales(router: np.ndarray, bias: np.ndarray, shape: Shape, seed: int,
+                       n_cal: int = 512) -> np.ndarray:
+    """Per-expert scales for the router rows, so that on a calibration batch
+    of N(0, 1) tokens the selection histogram comes as close as this family
+    allows to Zipf(shape.zipf) over the experts.
+
+    x has zero mean, so scaling a row changes only the spread of its logits;
+    under sigmoid scores an expert clears the top-k threshold for at most
+    about half of the tokens, so the target is capped at 0.45 of the tokens
+    (zipf_targets).  The scales follow a power law of a seeded popularity rank
+    r, exp(a - b ln r); (a, b) is the point of a fixed grid whose histogram,
+    sorted, is nearest the target in L1 — deterministic, so every build of
+    the layer has the same bytes.  With the DeepSeek-V3 rule the correction
+    bias (N(0, 0.1)) dominates which experts are popular; the scales set how
+    concentrated the histogram is."""
+    E = shape.n_experts
+    x = activations(seed, n_cal, shape.hidden).astype(np.float64)
+    base = x @ router.astype(np.float64).T
+    order = np.random.default_rng(seed).permutation(E)  # order[r] = expert of popularity rank r + 1
+    log_rank = np.empty(E)
+    log_rank[order] = np.log(np.arange(1, E + 1, dtype=np.float64))
+    target = zipf_targets(E, shape.zipf, float(n_cal * shape.top_k), 0.45 * n_cal)
+    bias64 = bias.astype(np.float64)
+    best, best_ab = None, (0.0, 0.0)
+    for a in np.linspace(-2.0, 4.0, 13):
+        for b in np.linspace(0.0, 3.0, 13):
+            counts = _route_counts(base * np.exp(a - b * log_rank)[None, :], bias64, shape)
+            err = np.abs(np.sort(counts)[::-1] - target).sum()
+            if best is None or err < best:
+                best, best_ab = err, (a, b)
+    return np.exp(best_ab[0] - best_ab[1] * log_rank)
 
 
 def build_host_layer(shape: Shape, seed: int) -> HostLayer:
@@ -152,6 +231,12 @@ def build_host_layer(shape: Shape, seed: int) -> HostLayer:
         else:
             which = ("shared.gate", "shared.up", "shared.down").index(name)
             _fill(dst, seed, STREAM_SHARED[which], dt, rows, cols, 0.0, shape.weight_std)
+    if shape.zipf > 0:
+        r = index["router"]
+        router = buf[r.offset:r.offset + r.nbytes].view(np.float32).reshape(E, H)
+        bias = (buf[index["e_bias"].offset:index["e_bias"].offset + 4 * E].view(np.float32)
+                if "e_bias" in index else np.zeros(E, np.float32))
+        router *= zipf_router_scales(router, bias, shape, seed).astype(np.float32)[:, None]
     return HostLayer(shape, buf, index)
 
 

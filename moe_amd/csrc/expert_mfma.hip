@@ -635,11 +635,13 @@ bool mfma_fits(size_t t, size_t k, size_t H, size_t I, size_t I_s) {
 }
 
 // Split K of the down projection (2 or 4 parts) when its grid would leave
-// CUs idle: the fewest parts that give about two blocks per CU.
+// CUs idle: the fewest parts that give every CU a block (one block fits per
+// CU: the ring takes most of the LDS).  Each part is written separately and
+// summed by the combine, so fewer parts also mean less traffic there.
 int mfma_down_ksplit(int m_tiles, int n_rows, int K, int K_shared) {
     const long long blocks = (long long)m_tiles * ((n_rows + BW - 1) / BW);
     int ks = 1;
-    while (ks < kMaxKSplit && blocks * ks < 512) ks *= 2;
+    while (ks < kMaxKSplit && blocks * ks < 256) ks *= 2;
     while (ks > 1 && (K % (ks * BK) != 0 || (K_shared > 0 && K_shared % (ks * BK) != 0))) ks /= 2;
     return ks;
 }

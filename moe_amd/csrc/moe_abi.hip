@@ -211,6 +211,7 @@ int reserve(moe_layer *L, int max_t, int k) {
         {(void **)&w.dtasks, (size_t)(k + 1) * sizeof(DecodeTask)},
         {(void **)&w.route_count, 4},
         {(void **)&w.ntiles, 4},
+        {(void **)&w.chunks, (size_t)dispatch_chunks((int)T) * E * 4},
         {(void **)&w.xh, T * H * 2},
         {(void **)&w.h, T * k * I * 4},
         {(void **)&w.hs, T * Is * 4},
@@ -583,7 +584,7 @@ static int route_and_dispatch(moe_layer *L, const float *x, int t, int k, int bm
     if (rc) return rc;
     if ((rc = copy_logits())) return rc;
     return stage(L, 2, s, [&] {
-        e = launch_dispatch(a, s);
+        e = launch_dispatch(a, w.chunks, s);
         return e == hipSuccess ? MOE_OK : hip_fail(e, "dispatch kernel");
     });
 }

@@ -86,6 +86,7 @@ struct Workspace {
     DecodeTask *dtasks = nullptr; // [k + 1] one-token task table
     unsigned *route_count = nullptr;  // [1] finished router blocks (one-token route), zero between calls
     int32_t *ntiles = nullptr;    // [1]
+    int32_t *chunks = nullptr;    // [dispatch_chunks(T) * E] per-chunk expert counts / first rows
     uint16_t *xh = nullptr;       // [T, H] f16 activations (MFMA path)
     float *h = nullptr;           // [T*k, I] routed SwiGLU activations (f32, or f16 on the MFMA path)
     float *hs = nullptr;          // [T, I_s] shared-expert activations
@@ -133,7 +134,11 @@ struct DispatchArgs {
     const float *shgate;          // [1] or null
     int I, dk_bound;
 };
-hipError_t launch_dispatch(const DispatchArgs &a, hipStream_t s);
+// More than one chunk of tokens (T > 512): three launches (count per
+// chunk, scan, place per chunk) using chunk_scratch [dispatch_chunks(T) * E]
+// ints; otherwise one block.  The permuted rows are the same either way.
+int dispatch_chunks(int T);
+hipError_t launch_dispatch(const DispatchArgs &a, int32_t *chunk_scratch, hipStream_t s);
 
 // Router + gating + dispatch of one token in one launch (n_rows blocks; the
 // last to finish gates and dispatches).  `counter` is zero between calls.

@@ -575,36 +575,18 @@ __device__ inline int block_scan_excl(int v, int *wave_sums, int *total) {
 // per-expert token order (src/model.rs:902-924).  Positions come from
 // per-wave 64-bit ballots, so tokens keep ascending order within an expert
 // without relying on atomic ordering.
-__device__ void dispatch_block(const DispatchArgs &a) {
-    __shared__ int cnt[kMaxExperts];
-    __shared__ int off[kMaxExperts];
-    __shared__ int run[kMaxExperts];
-    __shared__ unsigned long long bm[kDispatchWaves][kMaxExperts];
-    __shared__ int wb[kDispatchWaves][kMaxExperts];
-    __shared__ int wave_sums[kDispatchWaves];
-    __shared__ unsigned long long s_reused, s_bytes;
-    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+// Offsets, hit list, counters, one-token task table and MFMA tile list from
+// the per-expert counts (one expert per thread, E <= kMaxExperts); returns
+// this thread's expert's first permuted row.  Every thread of the block
+// calls it.
+__device__ int dispatch_tables(const DispatchArgs &a, int c, int *wave_sums, unsigned long long *s_reused,
+                               unsigned long long *s_bytes) {
+    const int tid = threadIdx.x;
     const int E = a.E, T = a.T, k = a.k;
-    const int n = T * k;
-    for (int e = tid; e < E; e += kDispatchThreads) {
-        cnt[e] = 0;
-        run[e] = 0;
-    }
-    if (tid == 0) s_reused = 0, s_bytes = 0;
-    __syncthreads();
-    for (int i = tid; i < n; i += kDispatchThreads) {
-        const int e = a.sel[i];
-        if (e >= 0 && e < E) atomicAdd(&cnt[e], 1);
-    }
-    __syncthreads();
-
-    // Offsets, hit list and tile list: one expert per thread (E <= 512).
     const int e = tid;
-    const int c = e < E ? cnt[e] : 0;
     int total;
     const int o = block_scan_excl(c, wave_sums, &total);
     if (e < E) {
-        off[e] = o;
         a.counts[e] = c;
         a.offsets[e] = o;
     }
@@ -618,12 +600,12 @@ __device__ void dispatch_block(const DispatchArgs &a) {
     if (c > 0) {
         a.hits[1 + hp] = e;
         if (a.hits_out) a.hits_out[1 + hp] = (uint32_t)e;
-        atomicAdd(&s_bytes, a.expert_bytes[e]);
+        atomicAdd(s_bytes, a.expert_bytes[e]);
         if (a.prev) {
             const uint32_t np = a.prev[0];
             bool in_prev = false;
             for (uint32_t j = 0; j < np; j++) in_prev |= a.prev[1 + j] == (uint32_t)e;
-            if (in_prev) atomicAdd(&s_reused, (unsigned long long)c);
+            if (in_prev) atomicAdd(s_reused, (unsigned long long)c);
         }
     }
     if (tid == 0) {
@@ -683,50 +665,139 @@ __device__ void dispatch_block(const DispatchArgs &a) {
             a.ntiles[0] = ntot;
         }
     }
-    __syncthreads();
-    if (tid == 0) {
-        a.stats[0] += (unsigned long long)n;
-        a.stats[1] += s_reused;
-        a.stats[2] += s_bytes;
-    }
+    return o;
+}
 
-    // Stable positions, kDispatchThreads tokens per pass.
-    for (int t0 = 0; t0 < T; t0 += kDispatchThreads) {
-        const int t = t0 + tid;
-        for (int x = lane; x < E; x += 64) bm[wv][x] = 0ull;
-        __syncthreads();
-        if (t < T)
-            for (int s = 0; s < k; s++) atomicOr(&bm[wv][a.sel[(size_t)t * k + s]], 1ull << lane);
-        __syncthreads();
-        for (int x = tid; x < E; x += kDispatchThreads) {
-            int r = run[x];
-            for (int w2 = 0; w2 < kDispatchWaves; w2++) {
-                wb[w2][x] = r;
-                r += __popcll(bm[w2][x]);
-            }
-            run[x] = r;
+// Stable permuted rows of tokens t0 .. t0 + kDispatchThreads - 1 (one per
+// thread): within an expert, lower token first.  run[e] enters as the
+// expert's next free row and leaves advanced past these tokens.  bm and wb
+// are LDS scratch.
+__device__ void dispatch_place(const DispatchArgs &a, int t0, int *run, unsigned long long (*bm)[kMaxExperts],
+                               int (*wb)[kMaxExperts]) {
+    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    const int E = a.E, T = a.T, k = a.k;
+    const int t = t0 + tid;
+    for (int x = lane; x < E; x += 64) bm[wv][x] = 0ull;
+    __syncthreads();
+    if (t < T)
+        for (int s = 0; s < k; s++) atomicOr(&bm[wv][a.sel[(size_t)t * k + s]], 1ull << lane);
+    __syncthreads();
+    for (int x = tid; x < E; x += kDispatchThreads) {
+        int r = run[x];
+        for (int w2 = 0; w2 < kDispatchWaves; w2++) {
+            wb[w2][x] = r;
+            r += __popcll(bm[w2][x]);
         }
-        __syncthreads();
-        if (t < T) {
-            const unsigned long long below = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
-            for (int s = 0; s < k; s++) {
-                const int ex = a.sel[(size_t)t * k + s];
-                const float wt = a.wsel[(size_t)t * k + s];
-                const int pp = off[ex] + wb[wv][ex] + __popcll(bm[wv][ex] & below);
-                a.perm_tok[pp] = t;
-                a.perm_w[pp] = wt;
-                a.pos[(size_t)t * k + s] = pp;
-                if (a.routes) {
-                    a.routes[(size_t)t * k + s].expert = (uint32_t)ex;
-                    a.routes[(size_t)t * k + s].weight = wt;
-                }
+        run[x] = r;
+    }
+    __syncthreads();
+    if (t < T) {
+        const unsigned long long below = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
+        for (int s = 0; s < k; s++) {
+            const int ex = a.sel[(size_t)t * k + s];
+            const float wt = a.wsel[(size_t)t * k + s];
+            const int pp = wb[wv][ex] + __popcll(bm[wv][ex] & below);
+            a.perm_tok[pp] = t;
+            a.perm_w[pp] = wt;
+            a.pos[(size_t)t * k + s] = pp;
+            if (a.routes) {
+                a.routes[(size_t)t * k + s].expert = (uint32_t)ex;
+                a.routes[(size_t)t * k + s].weight = wt;
             }
         }
-        __syncthreads();
+    }
+    __syncthreads();
+}
+
+// Counts of the selections of tokens t0 .. t0 + len - 1 into cnt (LDS,
+// zeroed by the caller).
+__device__ inline void dispatch_count(const DispatchArgs &a, int t0, int len, int *cnt) {
+    const int E = a.E, k = a.k;
+    const int n = len * k;
+    for (int i = threadIdx.x; i < n; i += kDispatchThreads) {
+        const int e = a.sel[(size_t)t0 * k + i];
+        if (e >= 0 && e < E) atomicAdd(&cnt[e], 1);
     }
 }
 
+__device__ void dispatch_block(const DispatchArgs &a) {
+    __shared__ int cnt[kMaxExperts];
+    __shared__ int run[kMaxExperts];
+    __shared__ unsigned long long bm[kDispatchWaves][kMaxExperts];
+    __shared__ int wb[kDispatchWaves][kMaxExperts];
+    __shared__ int wave_sums[kDispatchWaves];
+    __shared__ unsigned long long s_reused, s_bytes;
+    const int tid = threadIdx.x;
+    const int E = a.E, T = a.T;
+    for (int e = tid; e < E; e += kDispatchThreads) cnt[e] = 0;
+    if (tid == 0) s_reused = 0, s_bytes = 0;
+    __syncthreads();
+    dispatch_count(a, 0, T, cnt);
+    __syncthreads();
+    const int c = tid < E ? cnt[tid] : 0;
+    const int o = dispatch_tables(a, c, wave_sums, &s_reused, &s_bytes);
+    if (tid < E) run[tid] = o;
+    __syncthreads();
+    if (tid == 0) {
+        a.stats[0] += (unsigned long long)T * a.k;
+        a.stats[1] += s_reused;
+        a.stats[2] += s_bytes;
+    }
+    // Stable positions, kDispatchThreads tokens per pass.
+    for (int t0 = 0; t0 < T; t0 += kDispatchThreads) dispatch_place(a, t0, run, bm, wb);
+}
+
 __global__ __launch_bounds__(kDispatchThreads) void dispatch_kernel(DispatchArgs a) { dispatch_block(a); }
+
+// Many tokens: chunks of kDispatchThreads tokens.  Pass 1 counts each
+// chunk's selections per expert; pass 2 (one block) sums them into the
+// tables and gives every (chunk, expert) its first row; pass 3 places each
+// chunk's tokens from there.  The rows are the same as dispatch_block's.
+__global__ __launch_bounds__(kDispatchThreads) void dispatch_count_kernel(DispatchArgs a, int32_t *chunk_cnt) {
+    __shared__ int cnt[kMaxExperts];
+    const int t0 = blockIdx.x * kDispatchThreads;
+    for (int e = threadIdx.x; e < a.E; e += kDispatchThreads) cnt[e] = 0;
+    __syncthreads();
+    dispatch_count(a, t0, min(kDispatchThreads, a.T - t0), cnt);
+    __syncthreads();
+    for (int e = threadIdx.x; e < a.E; e += kDispatchThreads) chunk_cnt[(size_t)blockIdx.x * a.E + e] = cnt[e];
+}
+
+__global__ __launch_bounds__(kDispatchThreads) void dispatch_scan_kernel(DispatchArgs a, int32_t *chunk_cnt,
+                                                                         int n_chunks) {
+    __shared__ int wave_sums[kDispatchWaves];
+    __shared__ unsigned long long s_reused, s_bytes;
+    const int tid = threadIdx.x;
+    if (tid == 0) s_reused = 0, s_bytes = 0;
+    __syncthreads();
+    int c = 0;
+    if (tid < a.E)
+        for (int ch = 0; ch < n_chunks; ch++) c += chunk_cnt[(size_t)ch * a.E + tid];
+    int o = dispatch_tables(a, c, wave_sums, &s_reused, &s_bytes);
+    // Each chunk's first row per expert, in place of its count.
+    if (tid < a.E)
+        for (int ch = 0; ch < n_chunks; ch++) {
+            int32_t *p = chunk_cnt + (size_t)ch * a.E + tid;
+            const int v = *p;
+            *p = o;
+            o += v;
+        }
+    __syncthreads();
+    if (tid == 0) {
+        a.stats[0] += (unsigned long long)a.T * a.k;
+        a.stats[1] += s_reused;
+        a.stats[2] += s_bytes;
+    }
+}
+
+__global__ __launch_bounds__(kDispatchThreads) void dispatch_place_kernel(DispatchArgs a, const int32_t *chunk_base) {
+    __shared__ int run[kMaxExperts];
+    __shared__ unsigned long long bm[kDispatchWaves][kMaxExperts];
+    __shared__ int wb[kDispatchWaves][kMaxExperts];
+    for (int e = threadIdx.x; e < a.E; e += kDispatchThreads) run[e] = chunk_base[(size_t)blockIdx.x * a.E + e];
+    __syncthreads();
+    dispatch_place(a, blockIdx.x * kDispatchThreads, run, bm, wb);
+}
 
 // The dispatch of a single token by one wavefront: the same outputs as
 // dispatch_block for T = 1.  idx/w are the token's k selections (distinct
@@ -998,8 +1069,17 @@ hipError_t launch_route_one(const float *W, const float *x, int n_rows, int E, i
     return go(route_one_kernel<8>);
 }
 
-hipError_t launch_dispatch(const DispatchArgs &a, hipStream_t s) {
-    hipLaunchKernelGGL(dispatch_kernel, dim3(1), dim3(kDispatchThreads), 0, s, a);
+int dispatch_chunks(int T) { return T > kDispatchThreads ? (T + kDispatchThreads - 1) / kDispatchThreads : 0; }
+
+hipError_t launch_dispatch(const DispatchArgs &a, int32_t *chunk_scratch, hipStream_t s) {
+    const int nc = dispatch_chunks(a.T);
+    if (nc == 0 || !chunk_scratch) {
+        hipLaunchKernelGGL(dispatch_kernel, dim3(1), dim3(kDispatchThreads), 0, s, a);
+        return hipGetLastError();
+    }
+    hipLaunchKernelGGL(dispatch_count_kernel, dim3(nc), dim3(kDispatchThreads), 0, s, a, chunk_scratch);
+    hipLaunchKernelGGL(dispatch_scan_kernel, dim3(1), dim3(kDispatchThreads), 0, s, a, chunk_scratch, nc);
+    hipLaunchKernelGGL(dispatch_place_kernel, dim3(nc), dim3(kDispatchThreads), 0, s, a, chunk_scratch);
     return hipGetLastError();
 }
 

@@ -45,6 +45,9 @@ extern "C" {
 #define MOE_DT_Q5_0 6
 #define MOE_DT_Q8_0 8
 #define MOE_DT_BF16 30
+/* The reference's own 6-bit format (Dt::Q6, 26 bytes per 32 values), which
+ * a .moe file may hold; listed by the container reader, read by no kernel. */
+#define MOE_DT_Q6_REF (-2)
 
 /* Gate kinds (Spec::sigmoid, src/spec.rs:305-306). */
 #define MOE_GATE_SOFTMAX 0
@@ -186,6 +189,56 @@ const char *moe_last_error(void);
  * port of glibc's expf), for checking it against the host libm.  x and y are
  * device f32 [n].  No counterpart in the reference. */
 int moe_debug_expf(const float *x, float *y, uint64_t n, void *stream);
+
+/* --------------------------------------------------- checkpoint containers */
+
+/* One tensor of a single-file checkpoint: Store's Rec (src/store.rs:25-47).
+ * `offset` is the byte offset of the first row from the start of the file;
+ * a 3-D expert stack is `slabs` x `rows` rows of width `cols`, rows
+ * Dt::row_bytes(cols) apart (src/quant.rs:68-83).  `dt` is MOE_DT_* (GGUF's
+ * numbering, so other GGUF types keep their ggml number), `bytes` the size
+ * (0 for a type whose row size this library does not know). */
+typedef struct moe_rec {
+    const char *name;      /* owned by the container */
+    int32_t dt;
+    int32_t _reserved;
+    uint64_t slabs, rows, cols;
+    uint64_t offset;
+    uint64_t bytes;
+} moe_rec;
+
+typedef struct moe_container moe_container;
+
+/* Parse a packed `.moe` file (src/store.rs:228-279) or a GGUF v2/v3 file
+ * (src/gguf.rs:206-276) held in caller-owned memory (typically an mmap that
+ * outlives the container).  Every length in the header is checked against
+ * `len`: a corrupt or truncated file is MOE_EINVAL, never an out-of-bounds
+ * read.  Replaces Store::open for single-file checkpoints. */
+int moe_container_open(const void *bytes, uint64_t len, moe_container **out);
+void moe_container_close(moe_container *c);
+/* 1 = .moe, 2 = GGUF. */
+int moe_container_kind(const moe_container *c);
+int64_t moe_container_count(const moe_container *c);
+int moe_container_rec(const moe_container *c, int64_t i, moe_rec *out);
+/* Store::shape / Store::has by name (src/store.rs:293-301, 317-319). */
+int moe_container_find(const moe_container *c, const char *name, moe_rec *out);
+/* A .moe header's "config" object as JSON text (Store::config), or NULL. */
+const char *moe_container_config(const moe_container *c);
+
+/* The Hugging Face name of a GGUF tensor (gguf::rename, src/gguf.rs:435-487)
+ * into out[cap]; returns 1 (and leaves out alone) for tensors with no
+ * counterpart, such as rope frequency tables. */
+int moe_gguf_rename(const char *name, char *out, uint64_t cap);
+
+/* Upload n tensors of a host buffer (byte ranges [offsets[i], offsets[i] +
+ * lengths[i]) of host[host_len]) into one new device region, each starting
+ * on a 256-byte boundary; dev_offsets_out[i] receives tensor i's offset in
+ * the region.  Rows keep their offsets relative to their tensor, so a view
+ * of a tensor addresses the region as Store::view addresses the file; the
+ * kernels' wide loads get aligned rows even where the file packs tensors
+ * back to back (.moe payloads are unpadded, src/store.rs:439-441). */
+int moe_upload_tensors(moe_ctx *ctx, const void *host, uint64_t host_len, const uint64_t *offsets,
+                       const uint64_t *lengths, int64_t n, uint64_t *dev_offsets_out, uint64_t *region_out);
 
 /* ------------------------------------------------------- host utilities */
 

@@ -52,6 +52,14 @@ class RouteC(C.Structure):
     _fields_ = [("expert", C.c_uint32), ("weight", C.c_float)]
 
 
+class RecC(C.Structure):
+    _fields_ = [("name", C.c_char_p), ("dt", C.c_int32), ("_reserved", C.c_int32), ("slabs", C.c_uint64),
+                ("rows", C.c_uint64), ("cols", C.c_uint64), ("offset", C.c_uint64), ("bytes", C.c_uint64)]
+
+
+DT_Q6_REF = -2
+
+
 # name -> (restype, argtypes); every function include/moe_hip.h declares.
 PROTOTYPES = {
     "moe_ctx_create": (C.c_int, [C.c_int, C.POINTER(C.c_void_p)]),
@@ -76,6 +84,17 @@ PROTOTYPES = {
                                       C.c_double, C.c_void_p]),
     "moe_debug_expf": (C.c_int, [C.c_void_p, C.c_void_p, C.c_uint64, C.c_void_p]),
     "moe_layer_profile": (C.c_int, [C.c_void_p, C.c_int]),
+    "moe_container_open": (C.c_int, [C.c_void_p, C.c_uint64, C.POINTER(C.c_void_p)]),
+    "moe_container_close": (None, [C.c_void_p]),
+    "moe_container_kind": (C.c_int, [C.c_void_p]),
+    "moe_container_count": (C.c_int64, [C.c_void_p]),
+    "moe_container_rec": (C.c_int, [C.c_void_p, C.c_int64, C.POINTER(RecC)]),
+    "moe_container_find": (C.c_int, [C.c_void_p, C.c_char_p, C.POINTER(RecC)]),
+    "moe_container_config": (C.c_char_p, [C.c_void_p]),
+    "moe_gguf_rename": (C.c_int, [C.c_char_p, C.c_char_p, C.c_uint64]),
+    "moe_upload_tensors": (C.c_int, [C.c_void_p, C.c_void_p, C.c_uint64, C.POINTER(C.c_uint64),
+                                     C.POINTER(C.c_uint64), C.c_int64, C.POINTER(C.c_uint64),
+                                     C.POINTER(C.c_uint64)]),
     "moe_layer_stage_times": (C.c_int, [C.c_void_p, C.POINTER(C.c_double), C.POINTER(C.c_uint64)]),
 }
 

@@ -37,7 +37,7 @@ HIP_FLAGS = [
 EXACT = {"route.hip", "combine.hip", "expert_gemv.hip", "expert_decode.hip"}
 
 SOURCES = ["route.hip", "expert_gemv.hip", "expert_decode.hip", "expert_mfma.hip", "combine.hip", "moe_abi.hip"]
-HOST_SOURCES = ["host_util.cpp"]
+HOST_SOURCES = ["host_util.cpp", "container.cpp"]
 
 
 def _run(cmd: list[str]) -> None:

@@ -18,10 +18,12 @@
 using namespace moe;
 
 
-namespace {
+namespace moe {
 
 thread_local std::string g_err;
 
+// Records the message moe_last_error returns (the host-only sources report
+// through it too) and passes the status code through.
 int fail(int code, const char *fmt, ...) {
     char buf[512];
     va_list ap;
@@ -31,6 +33,11 @@ int fail(int code, const char *fmt, ...) {
     g_err = buf;
     return code;
 }
+
+}  // namespace moe
+
+namespace {
+
 int hip_fail(hipError_t e, const char *what) { return fail(MOE_EHIP, "%s: %s", what, hipGetErrorString(e)); }
 
 struct DeviceGuard {
@@ -292,6 +299,39 @@ int moe_upload(moe_ctx *ctx, const void *host, uint64_t bytes, uint64_t *region_
     }
     std::lock_guard<std::mutex> lk(ctx->mu);
     ctx->regions.push_back(Region{p, bytes});
+    *region_out = ctx->regions.size() - 1;
+    return MOE_OK;
+}
+
+int moe_upload_tensors(moe_ctx *ctx, const void *host, uint64_t host_len, const uint64_t *offsets,
+                       const uint64_t *lengths, int64_t n, uint64_t *dev_offsets_out, uint64_t *region_out) {
+    if (!ctx || !region_out || n < 0 || (n > 0 && (!host || !offsets || !lengths || !dev_offsets_out)))
+        return fail(MOE_EINVAL, "moe_upload_tensors: bad argument");
+    uint64_t total = 0;
+    for (int64_t i = 0; i < n; i++) {
+        if (offsets[i] > host_len || lengths[i] > host_len - offsets[i])
+            return fail(MOE_EINVAL, "moe_upload_tensors: tensor %lld (%llu bytes at %llu) is outside the %llu-byte buffer",
+                        (long long)i, (unsigned long long)lengths[i], (unsigned long long)offsets[i],
+                        (unsigned long long)host_len);
+        dev_offsets_out[i] = total;
+        total = align_up(total + lengths[i], 256);
+    }
+    DeviceGuard g(ctx->device);
+    void *p = nullptr;
+    hipError_t e = hipMalloc(&p, std::max<uint64_t>(total, 256));
+    if (e != hipSuccess)
+        return fail(MOE_ENOMEM, "moe_upload_tensors: %llu bytes: %s", (unsigned long long)total, hipGetErrorString(e));
+    for (int64_t i = 0; i < n; i++) {
+        if (!lengths[i]) continue;
+        e = hipMemcpy(static_cast<char *>(p) + dev_offsets_out[i], static_cast<const char *>(host) + offsets[i],
+                      lengths[i], hipMemcpyHostToDevice);
+        if (e != hipSuccess) {
+            hipFree(p);
+            return hip_fail(e, "moe_upload_tensors: hipMemcpy");
+        }
+    }
+    std::lock_guard<std::mutex> lk(ctx->mu);
+    ctx->regions.push_back(Region{p, total});
     *region_out = ctx->regions.size() - 1;
     return MOE_OK;
 }

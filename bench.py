@@ -209,6 +209,7 @@ def main() -> int:
     ap.add_argument("--copies", type=int, default=4, help="distinct weight copies cycled through")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--mode", type=int, default=0, help="kernel path (moe_layer_set_mode): 0 automatic")
     ap.add_argument("--summarize-pmc", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
                     help="write the HBM traffic summary from two rocprofv3 counter passes and exit")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
@@ -236,6 +237,9 @@ def main() -> int:
     log(f"generated {host.buf.nbytes / 1e6:.0f} MB in {time.time() - t0:.1f}s; uploading {args.copies} copies")
     ctx = Context(0)
     layers = [synth.make_layer(ctx, host, layer_index=0) for _ in range(args.copies)]
+    if args.mode:
+        for layer in layers:
+            layer.set_mode(args.mode)
     dev = torch.device("cuda:0")
     k = layers[0].k
 

@@ -136,8 +136,8 @@ int moe_layer_set_routing(moe_layer *layer, const moe_routing *routing);
 int moe_layer_reserve(moe_layer *layer, int32_t max_t);
 
 /* Kernel path: 0 = automatic (one-token integer-dot kernels at t = 1, MFMA
- * grouped GEMM once experts average three or more tokens, register GEMV in
- * between, exact kernels for shapes none fits), 1 = exact kernels
+ * grouped GEMM for t >= 2, register GEMV for shapes the MFMA kernel does not
+ * take, exact kernels for shapes none fits), 1 = exact kernels
  * (bit-identical to the CPU path, slow), 2 = GEMV, 3 = MFMA, 4 = one-token
  * kernels at t = 1 and GEMV otherwise.  No counterpart in the reference,
  * which has one CPU path. */

@@ -135,11 +135,14 @@ int moe_layer_set_routing(moe_layer *layer, const moe_routing *routing);
  * forward calls with t <= max_t allocate nothing. */
 int moe_layer_reserve(moe_layer *layer, int32_t max_t);
 
-/* Kernel path: 0 = automatic (one-token integer-dot kernels at t = 1, MFMA
- * grouped GEMM for t >= 2, register GEMV for shapes the MFMA kernel does not
- * take, exact kernels for shapes none fits), 1 = exact kernels
+/* Kernel path: 0 = automatic (one-token integer-dot kernels at t = 1,
+ * few-tokens integer-dot kernels while the hit experts average at most 3
+ * tokens (1.5 for rows wider than 4096), MFMA grouped GEMM beyond, register
+ * GEMV for shapes the MFMA kernel does not take, exact kernels for shapes
+ * none fits), 1 = exact kernels
  * (bit-identical to the CPU path, slow), 2 = GEMV, 3 = MFMA, 4 = one-token
- * kernels at t = 1 and GEMV otherwise.  No counterpart in the reference,
+ * kernels at t = 1 and GEMV otherwise, 5 = few-tokens integer-dot kernels
+ * (up to 256 tokens).  No counterpart in the reference,
  * which has one CPU path. */
 int moe_layer_set_mode(moe_layer *layer, int mode);
 

@@ -37,153 +37,12 @@
 #include "gmem.h"
 #include "moe_internal.h"
 #include "qact.h"
+#include "qdot.h"
 
 namespace moe {
 namespace {
 
-typedef uint32_t u32x4a4 __attribute__((ext_vector_type(4), aligned(4)));
-typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
-
-__device__ inline float h2f(uint32_t bits) { return __half2float(__ushort_as_half((unsigned short)(bits & 0xffff))); }
-__device__ inline uint32_t alignb(uint32_t hi, uint32_t lo, uint32_t s) { return __builtin_amdgcn_alignbyte(hi, lo, s); }
-__device__ inline int sdot4(uint32_t a, uint32_t b, int c) { return __builtin_amdgcn_sdot4((int)a, (int)b, c, false); }
-// Bits 0..3 of h moved to bit 4 of bytes 0..3.
-__device__ inline uint32_t spread4(uint32_t h) { return ((h * 0x00204081u) & 0x01010101u) << 4; }
-
-// A 64-value unit of a weight row: two quantisation blocks, 4-byte aligned.
-template <int DT>
-struct WUnit;
-template <>
-struct WUnit<MOE_DT_Q4_0> {
-    static constexpr int dw = 9, bytes = 36;
-};
-template <>
-struct WUnit<MOE_DT_Q5_0> {
-    static constexpr int dw = 11, bytes = 44;
-};
-template <>
-struct WUnit<MOE_DT_Q8_0> {
-    static constexpr int dw = 17, bytes = 68;
-};
-
-// Loads the first WUnit<DT>::dw entries of d (a buffer sized for the widest
-// format in use).
-template <int DT, int DN>
-__device__ inline void load_wunit(const uint8_t *p, uint32_t (&d)[DN]) {
-    static_assert(DN >= WUnit<DT>::dw, "unit buffer too small");
-    const uint32_t *q = reinterpret_cast<const uint32_t *>(__builtin_assume_aligned(p, 4));
-    constexpr int N = WUnit<DT>::dw;
-#pragma unroll
-    for (int i = 0; i + 4 <= N; i += 4) {
-        const u32x4_dw v = gload_x4(q + i);
-        d[i] = v.x, d[i + 1] = v.y, d[i + 2] = v.z, d[i + 3] = v.w;
-    }
-#pragma unroll
-    for (int i = N & ~3; i < N; i++) d[i] = gload(q + i);
-}
-
-// The activation unit (144 bytes, 16-byte aligned) into 36 registers, from
-// address space AS (1: global, 3: LDS).
-template <int AS>
-__device__ inline void load_qunit(const uint8_t *p, uint32_t (&x)[kQUnitDw]) {
-    typedef const __attribute__((address_space(AS))) u32x4 *v4p;
-    const v4p q = (v4p)p;
-#pragma unroll
-    for (int i = 0; i < kQUnitDw / 4; i++) {
-        const u32x4 v = q[i];
-        x[4 * i] = v.x, x[4 * i + 1] = v.y, x[4 * i + 2] = v.z, x[4 * i + 3] = v.w;
-    }
-}
-
-// Dot of a weight unit with an activation unit.
-//   Q4_0 [dA qA0..15][dB qB0..15]: byte j holds value j (low nibble) and
-//        value j + 16 (high nibble), stored unsigned with offset 8.
-//   Q5_0 [dA hA(4) qA][dB hB qB]: bit j of h is bit 4 of value j, offset 16.
-//   Q8_0 [dA qA0..31][dB qB0..31]: signed bytes.
-// For a block: sum_i d (q_i - o) x_i = d s2 (254 A + B - o sq) with
-// A = sum q hi, B = sum q lo; B starts at -o sq.
-template <int DT, int DN>
-__device__ inline float qdot(const uint32_t (&d)[DN], const uint32_t (&x)[kQUnitDw]) {
-    static_assert(DN >= WUnit<DT>::dw, "unit buffer too small");
-    const float s2a = __uint_as_float(x[32]), s2b = __uint_as_float(x[33]);
-    const int sqa = (int)x[34], sqb = (int)x[35];
-    int Aa = 0, Ab = 0, Ba, Bb;
-    float sa, sb;
-    if constexpr (DT == MOE_DT_Q4_0) {
-        sa = h2f(d[0]), sb = h2f(d[4] >> 16);
-        Ba = -8 * sqa, Bb = -8 * sqb;
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const uint32_t qa = alignb(d[i + 1], d[i], 2), qb = d[5 + i];
-            const uint32_t la = qa & 0x0f0f0f0fu, ha = (qa >> 4) & 0x0f0f0f0fu;
-            const uint32_t lb = qb & 0x0f0f0f0fu, hb = (qb >> 4) & 0x0f0f0f0fu;
-            Aa = sdot4(la, x[i], Aa), Aa = sdot4(ha, x[4 + i], Aa);
-            Ba = sdot4(la, x[16 + i], Ba), Ba = sdot4(ha, x[20 + i], Ba);
-            Ab = sdot4(lb, x[8 + i], Ab), Ab = sdot4(hb, x[12 + i], Ab);
-            Bb = sdot4(lb, x[24 + i], Bb), Bb = sdot4(hb, x[28 + i], Bb);
-        }
-    } else if constexpr (DT == MOE_DT_Q5_0) {
-        sa = h2f(d[0]), sb = h2f(d[5] >> 16);
-        Ba = -16 * sqa, Bb = -16 * sqb;
-        const uint32_t hA = alignb(d[1], d[0], 2), hB = d[6];
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const uint32_t qa = alignb(d[i + 2], d[i + 1], 2), qb = d[7 + i];
-            const uint32_t la = (qa & 0x0f0f0f0fu) | spread4((hA >> (4 * i)) & 0xfu);
-            const uint32_t ha = ((qa >> 4) & 0x0f0f0f0fu) | spread4((hA >> (16 + 4 * i)) & 0xfu);
-            const uint32_t lb = (qb & 0x0f0f0f0fu) | spread4((hB >> (4 * i)) & 0xfu);
-            const uint32_t hb = ((qb >> 4) & 0x0f0f0f0fu) | spread4((hB >> (16 + 4 * i)) & 0xfu);
-            Aa = sdot4(la, x[i], Aa), Aa = sdot4(ha, x[4 + i], Aa);
-            Ba = sdot4(la, x[16 + i], Ba), Ba = sdot4(ha, x[20 + i], Ba);
-            Ab = sdot4(lb, x[8 + i], Ab), Ab = sdot4(hb, x[12 + i], Ab);
-            Bb = sdot4(lb, x[24 + i], Bb), Bb = sdot4(hb, x[28 + i], Bb);
-        }
-    } else {
-        sa = h2f(d[0]), sb = h2f(d[8] >> 16);
-        Ba = 0, Bb = 0;
-#pragma unroll
-        for (int i = 0; i < 8; i++) {
-            const uint32_t qa = alignb(d[i + 1], d[i], 2), qb = d[9 + i];
-            Aa = sdot4(qa, x[i], Aa), Ba = sdot4(qa, x[16 + i], Ba);
-            Ab = sdot4(qb, x[8 + i], Ab), Bb = sdot4(qb, x[24 + i], Bb);
-        }
-    }
-    const float fa = (float)(254 * Aa + Ba), fb = (float)(254 * Ab + Bb);
-    return fmaf(sb * s2b, fb, (sa * s2a) * fa);
-}
-
-// Sum over groups of CG consecutive lanes (CG = 16, 32, 64); every lane of
-// a group receives the same sum.  The first four steps are DPP moves inside
-// a row of 16 lanes.
-__device__ inline float dpp_add(float v, int ctrl) {
-    int r;
-    switch (ctrl) {
-    case 0: r = __builtin_amdgcn_update_dpp(0, __float_as_int(v), 0xb1, 0xf, 0xf, false); break;   // quad [1,0,3,2]
-    case 1: r = __builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x4e, 0xf, 0xf, false); break;   // quad [2,3,0,1]
-    case 2: r = __builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x141, 0xf, 0xf, false); break;  // half-row mirror
-    default: r = __builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x140, 0xf, 0xf, false); break; // row mirror
-    }
-    return v + __int_as_float(r);
-}
-// Sums over slices of CG consecutive lanes (CG = 16, 32, 64): afterwards
-// the last lane of each slice holds its slice's sum (every lane of it for
-// CG = 16).  Rows of 16 lanes reduce through quad permutes and mirrors; rows
-// join through row broadcasts, which leave the total in the last lane.
-__device__ inline float slice_sum(float v, int cg) {
-    v = dpp_add(v, 0);
-    v = dpp_add(v, 1);
-    v = dpp_add(v, 2);
-    v = dpp_add(v, 3);
-    if (cg >= 32) v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x142, 0xa, 0xf, false));
-    if (cg >= 64) v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x143, 0xc, 0xf, false));
-    return v;
-}
-
-__device__ inline float silu_mul(float g, float u) { return (g / (1.0f + __expf(-g))) * u; }
-
-// Lanes of a row slice: CG lanes (16, 32, 64) own UPL units each (1, or 2
-// for rows of 65..128 units: units c and c + 64 of lane c).
-__device__ inline int lanes_for(int units) { return units <= 16 ? 16 : units <= 32 ? 32 : 64; }
+using namespace qd;
 
 // Loads the 32 floats at src into registers (16-byte aligned).
 typedef float f32x4 __attribute__((ext_vector_type(4)));
@@ -217,32 +76,37 @@ struct UpStep {
     bool ok;
 };
 
+// Every step yields loadable pointers, so that every step issues the same
+// loads: the compiler then counts them exactly and waits for one step at a
+// time (loads under a condition make it wait for all of them).  A step past
+// the end, or of a task without an expert, reads task 0's first rows (task 0
+// always has an expert) and is not computed; lanes past the row's units
+// (c >= units) read its last unit.
 __device__ inline UpStep up_step(const DecodeTask *tasks, int k_bound, int s, int n_steps, int spr, int slices,
-                                 int slot, int c, int UB) {
+                                 int slot, int c, int units, int UB) {
     UpStep st;
-    st.ok = false;
-    if (s >= n_steps) return st;
-    const int t = s < k_bound * spr ? s / spr : k_bound;
+    const int sc = s < n_steps ? s : n_steps - 1;
+    const int t = sc < k_bound * spr ? sc / spr : k_bound;
     const DecodeTask &T = tasks[t];
-    if (!T.live) return st;
-    const int r = (t < k_bound ? s - t * spr : s - k_bound * spr) * slices + slot;
-    st.g = T.g + (size_t)r * T.gs + (size_t)c * UB;
-    st.u = T.u + (size_t)r * T.us + (size_t)c * UB;
+    st.ok = s < n_steps && T.live;
+    const int r = T.live ? (t < k_bound ? sc - t * spr : sc - k_bound * spr) * slices + slot : slot;
+    const DecodeTask &L = T.live ? T : tasks[0];
+    const int cl = c < units ? c : units - 1;
+    st.g = L.g + (size_t)r * L.gs + (size_t)cl * UB;
+    st.u = L.u + (size_t)r * L.us + (size_t)cl * UB;
     st.h = T.h + r;
-    st.ok = true;
     return st;
 }
 
 template <int DT, int UPL, int DW>
 __device__ inline void up_load(const UpStep &st, const bool (&live)[UPL], uint32_t (&w)[2][UPL][DW]) {
-    if (!st.ok) return;
     constexpr int UB = WUnit<DT>::bytes;
 #pragma unroll
-    for (int j = 0; j < UPL; j++)
-        if (live[j]) {
-            load_wunit<DT, DW>(st.g + (size_t)j * 64 * UB, w[0][j]);
-            load_wunit<DT, DW>(st.u + (size_t)j * 64 * UB, w[1][j]);
-        }
+    for (int j = 0; j < UPL; j++) {
+        const size_t off = live[j] ? (size_t)j * 64 * UB : 0;
+        load_wunit<DT, DW>(st.g + off, w[0][j]);
+        load_wunit<DT, DW>(st.u + off, w[1][j]);
+    }
 }
 
 template <int DT, int UPL, int DW>
@@ -288,7 +152,7 @@ __global__ __launch_bounds__(256) void decode_up_kernel(DecodeArgs a, const floa
     UpStep st[NBUF];
 #pragma unroll
     for (int b = 0; b + 1 < NBUF; b++) {
-        st[b] = up_step(tasks, a.k_bound, s0 + b * nw, n_steps, spr, slices, slot, c, UB);
+        st[b] = up_step(tasks, a.k_bound, s0 + b * nw, n_steps, spr, slices, slot, c, units, UB);
         up_load<DT, UPL, DW>(st[b], live, w[b]);
     }
     if ((int)threadIdx.x < n_xb)
@@ -303,7 +167,7 @@ __global__ __launch_bounds__(256) void decode_up_kernel(DecodeArgs a, const floa
 #pragma unroll
         for (int b = 0; b < NBUF; b++) {
             const int nb = (b + NBUF - 1) % NBUF;
-            st[nb] = up_step(tasks, a.k_bound, s + (NBUF - 1) * nw, n_steps, spr, slices, slot, c, UB);
+            st[nb] = up_step(tasks, a.k_bound, s + (NBUF - 1) * nw, n_steps, spr, slices, slot, c, units, UB);
             up_load<DT, UPL, DW>(st[nb], live, w[nb]);
             if (s >= n_steps) break;
             up_compute<DT, UPL, DW>(st[b], live, w[b], xa, cg, tail);
@@ -332,16 +196,23 @@ struct DownLane {
     uint32_t stride;
 };
 
+// Unconditional, like up_load: ranges past the end re-read the last one,
+// rows past the slot's rs its last row, units past the row its last unit,
+// and lanes of a task without an expert read task 0's rows (down_lane).
 template <int DT, int UPL, int RS, int DW>
 __device__ inline void down_load(const DownLane &L, int range, int n_ranges, int rb, uint32_t (&w)[RS][UPL][DW]) {
-    if (!L.active || range >= n_ranges) return;
     constexpr int UB = WUnit<DT>::bytes;
-    const uint8_t *p = L.w + (size_t)(range * rb + L.slot * L.rs) * L.stride;
+    const int rg = range < n_ranges ? range : n_ranges - 1;
+    const uint8_t *p = L.w + (size_t)(rg * rb + L.slot * L.rs) * L.stride;
 #pragma unroll
-    for (int i = 0; i < RS; i++)
+    for (int i = 0; i < RS; i++) {
+        const int ii = i < L.rs ? i : L.rs - 1;
 #pragma unroll
-        for (int j = 0; j < UPL; j++)
-            if (i < L.rs && L.live[j]) load_wunit<DT, DW>(p + (size_t)i * L.stride + (size_t)j * 64 * UB, w[i][j]);
+        for (int j = 0; j < UPL; j++) {
+            const size_t off = L.live[j] ? (size_t)j * 64 * UB : 0;
+            load_wunit<DT, DW>(p + (size_t)ii * L.stride + off, w[i][j]);
+        }
+    }
 }
 
 template <int DT, int UPL, int RS, int DW>
@@ -369,9 +240,11 @@ __device__ inline void down_lane(const DecodeTask *tasks, int k_bound, int wv, i
     L.active = T.live != 0;
     L.tail = false;
     L.live[0] = L.live[1] = false;
-    L.rs = 0;
+    L.rs = 1;
     L.cg = 64;
     L.kw = L.slot = 0;
+    L.w = tasks[0].d;  // loaded, not computed (down_load)
+    L.stride = tasks[0].ds;
     if (!L.active) return;
     const int units = T.dcols / 64, lane = threadIdx.x & 63;
     const int ks = shared ? ks_s : ks_r;
@@ -383,7 +256,7 @@ __device__ inline void down_lane(const DecodeTask *tasks, int k_bound, int wv, i
     const int u0 = L.kw * 64 + lane % L.cg;
     L.live[0] = u0 < units;
     L.live[1] = u0 + 64 < units;
-    L.w = T.d + (size_t)u0 * WUnit<DT>::bytes;
+    L.w = T.d + (size_t)(u0 < units ? u0 : units - 1) * WUnit<DT>::bytes;
     L.stride = T.ds;
 }
 

@@ -14,6 +14,7 @@
 
 #include "moe_internal.h"
 #include "qact.h"
+#include "qact.h"
 
 using namespace moe;
 
@@ -59,7 +60,7 @@ struct Region {
 };
 
 // Forward path for a call.
-enum Path { kExact = 1, kGemv = 2, kMfma = 3, kDecode = 4 };
+enum Path { kExact = 1, kGemv = 2, kMfma = 3, kDecode = 4, kBatch = 5 };
 
 }  // namespace
 
@@ -76,7 +77,7 @@ struct moe_layer {
     int gate = 0, norm_topk = 1, n_group = 1, topk_group = 1;
     float routed_scale = 1.0f;
     bool has_shared = false, has_shared_gate = false;
-    bool fast_ok = false, mfma_ok = false, decode_ok = false;
+    bool fast_ok = false, mfma_ok = false, decode_ok = false, batch_ok = false;
     int mode = 0;  // 0 auto, else a Path
     // routing override
     float temp = 0.0f;
@@ -180,6 +181,16 @@ int effective_k(const moe_layer *L) {
 
 size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
 
+// Whether the few-tokens kernels beat MFMA tiles.  Their cost is the
+// weight bytes of every tile (an expert's weights are read once per tile of
+// nt tokens, at about twice the MFMA kernels' rate); measured on MI355X they
+// win while the hit experts average at most 1.5 tiles' worth of tokens.
+bool batch_pays(int t, int k, int E, int nt) {
+    if (t < 2 || t > kBatchMaxT) return false;
+    const long long rows = (long long)t * k, hit = std::min<long long>(E, rows);
+    return 2 * rows <= 3LL * nt * hit;
+}
+
 void free_ws(Workspace &w) {
     if (w.base) hipFree(w.base);
     w = Workspace();
@@ -191,16 +202,20 @@ int reserve(moe_layer *L, int max_t, int k) {
     k = std::max(k, L->ws_k);
     const size_t T = (size_t)max_t, E = (size_t)L->E, H = (size_t)L->H;
     const size_t I = (size_t)std::max(L->I, 1), Is = (size_t)std::max(L->I_s, 1);
-    const size_t max_tiles = T * k / 16 + E + 2 + (T + 15) / 16;
+    // Tiles of one token or more (the few-tokens path), or 160 (MFMA).
+    const size_t max_tiles = T * k + E + 2 + T;
+    // Activation units for the few-tokens path, which runs up to kBatchMaxT tokens.
+    const size_t Tb = L->batch_ok ? std::min<size_t>(T, kBatchMaxT) : 0;
     struct Item {
         void **dst;
         size_t bytes;
     };
     Workspace w;
     w.max_t = max_t;
+    w.batch_t = (int)Tb;
     // Room for the K parts of a split MFMA down projection.  Splitting only
     // pays for small grids, so parts after the first are bounded in rows.
-    const size_t extra = L->mfma_ok ? (kMaxKSplit - 1) * std::min<size_t>(T * k, 8192) : 0;
+    const size_t extra = (L->mfma_ok || L->batch_ok) ? (kMaxKSplit - 1) * std::min<size_t>(T * k, 8192) : 0;
     w.y_rows = T * k + extra;
     w.ys_rows = T + extra;
     Item items[] = {
@@ -220,6 +235,9 @@ int reserve(moe_layer *L, int max_t, int k) {
         {(void **)&w.ntiles, 4},
         {(void **)&w.chunks, (size_t)dispatch_chunks((int)T) * E * 4},
         {(void **)&w.xh, T * H * 2},
+        {(void **)&w.xq, Tb * (H / 64) * kQUnitBytes},
+        {(void **)&w.hq, Tb * k * (I / 64) * kQUnitBytes},
+        {(void **)&w.hsq, Tb * (Is / 64) * kQUnitBytes},
         {(void **)&w.h, T * k * I * 4},
         {(void **)&w.hs, T * Is * 4},
         {(void **)&w.y, w.y_rows * H * 4},
@@ -447,6 +465,9 @@ int moe_layer_create(moe_ctx *ctx, const moe_layer_desc *d, moe_layer **out) {
         L->decode_ok &= s.m[0].dt == s.m[2].dt;
     }
     L->decode_ok &= e0.m[0].dt == e0.m[2].dt;
+    L->batch_ok = fast && batch_supported(H, I, L->has_shared ? L->I_s : 0, e0.m[0].dt,
+                                          L->has_shared ? L->experts_host[E].m[0].dt : e0.m[0].dt);
+    for (int e = 0; e < E + (L->has_shared ? 1 : 0); e++) L->batch_ok &= batch_supported(H, I, 0, L->experts_host[e].m[2].dt, 0);
 
     // Device-side tables.
     hipError_t he;
@@ -522,7 +543,8 @@ int moe_layer_set_routing(moe_layer *L, const moe_routing *r) {
 }
 
 int moe_layer_set_mode(moe_layer *L, int mode) {
-    if (!L || mode < 0 || mode > kDecode) return fail(MOE_EINVAL, "moe_layer_set_mode: mode %d", mode);
+    if (!L || mode < 0 || mode > kBatch) return fail(MOE_EINVAL, "moe_layer_set_mode: mode %d", mode);
+    if (mode == kBatch && !L->batch_ok) return fail(MOE_EUNSUP, "this layer's shapes do not fit the few-tokens kernels");
     if (mode == kDecode && !L->decode_ok) return fail(MOE_EUNSUP, "this layer's shapes do not fit the one-token kernels");
     if (mode == kGemv && !L->fast_ok) return fail(MOE_EUNSUP, "this layer's shapes do not fit the GEMV kernels");
     if (mode == kMfma && !L->mfma_ok) return fail(MOE_EUNSUP, "this layer's shapes do not fit the MFMA kernels");
@@ -649,24 +671,29 @@ int moe_layer_forward(moe_layer *L, const float *x, int32_t t, float *out, float
     if (rc) return rc;
     Workspace &w = L->ws;
 
-    // Path: the one-token kernels for one token, MFMA from two tokens on (it
-    // beats the register GEMV at every size measured on MI355X, down to two
-    // tokens over eight experts), GEMV where the MFMA kernel does not take
-    // the shapes, the exact kernels when neither fits (or when asked).
+    // Path: the one-token kernels for one token, the few-tokens kernels
+    // while experts hold few tokens each, MFMA beyond (it beats the register
+    // GEMV at every size measured on MI355X), GEMV where the MFMA kernel does
+    // not take the shapes, the exact kernels when neither fits (or when
+    // asked).
     Path path = kExact;
     if (L->mode) {
         path = (Path)L->mode;
     } else if (L->fast_ok) {
         path = L->mfma_ok ? kMfma : kGemv;
-        if (t == 1 && L->decode_ok) path = kDecode;
+        if (t == 1 && L->decode_ok)
+            path = kDecode;
+        else if (L->batch_ok && batch_pays(t, k, L->E, batch_tile_tokens(L->H)))
+            path = kBatch;
     }
+    if (path == kBatch && (!L->batch_ok || t > w.batch_t)) path = L->mfma_ok ? kMfma : kGemv;
     if (path == kDecode) {
         const int dt_r = L->experts_host[0].m[0].dt;
         const int dt_s = L->has_shared ? L->experts_host[L->E].m[0].dt : dt_r;
         if (t != 1 || !decode_fits(L->I, L->I_s, k, L->has_shared, dt_r, dt_s)) path = kGemv;
     }
     if (path == kMfma && !mfma_fits(t, k, L->H, L->I, L->has_shared ? L->I_s : 0)) path = kGemv;
-    const int bm = path == kMfma ? mfma_tile_m() : 0;
+    const int bm = path == kMfma ? mfma_tile_m() : path == kBatch ? batch_tile_tokens(L->H) : 0;
     if ((rc = route_and_dispatch(L, x, t, k, bm, path == kDecode, routes, hits, prev, stats, nullptr,
                                  path == kMfma ? w.xh : nullptr, s)))
         return rc;
@@ -701,7 +728,48 @@ int moe_layer_forward(moe_layer *L, const float *x, int32_t t, float *out, float
             return e == hipSuccess ? MOE_OK : hip_fail(e, "one-token down kernel");
         });
     }
-    if (path == kMfma) {
+    if (path == kBatch) {
+        BatchArgs b{};
+        b.experts = L->experts_dev;
+        b.tiles = w.tiles;
+        b.ntiles = w.ntiles;
+        b.counts = w.counts;
+        b.offsets = w.offsets;
+        b.perm_tok = w.perm_tok;
+        b.xq = w.xq;
+        b.h = w.h;
+        b.hs = w.hs;
+        b.hq = w.hq;
+        b.hsq = w.hsq;
+        b.y = w.y;
+        b.ys = w.ys;
+        b.T = t;
+        b.H = L->H;
+        b.I = L->I;
+        b.I_s = L->I_s;
+        b.E = L->E;
+        b.max_tiles = t * k / bm + std::min(L->E, t * k) + 1;
+        b.shared_tiles = L->has_shared ? (t + bm - 1) / bm : 0;
+        b.ypart = (size_t)t * k * L->H;
+        b.yspart = (size_t)t * L->H;
+        b.ksplit = batch_ksplit(L->I, L->has_shared ? L->I_s : 0);
+        if ((size_t)b.ksplit * t * k > w.y_rows || (size_t)b.ksplit * t > w.ys_rows)
+            return fail(MOE_EUNSUP, "few-tokens path: %d K parts do not fit the workspace", b.ksplit);
+        ksplit = b.ksplit;
+        rc = stage(L, 3, s, [&] {
+            e = launch_qenc(x, t, L->H, w.xq, s);
+            if (e == hipSuccess) e = launch_batch_up(b, e0, sh, s);
+            return e == hipSuccess ? MOE_OK : hip_fail(e, "few-tokens gate/up kernel");
+        });
+        if (rc) return rc;
+        rc = stage(L, 4, s, [&] {
+            e = launch_qenc(w.h, t * k, L->I, w.hq, s);
+            if (e == hipSuccess && sh) e = launch_qenc(w.hs, t, L->I_s, w.hsq, s);
+            if (e == hipSuccess) e = launch_batch_down(b, e0, sh, s);
+            return e == hipSuccess ? MOE_OK : hip_fail(e, "few-tokens down kernel");
+        });
+        if (rc) return rc;
+    } else if (path == kMfma) {
         MfmaArgs m{};
         m.experts = L->experts_dev;
         m.tiles = w.tiles;

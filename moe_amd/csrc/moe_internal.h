@@ -88,6 +88,10 @@ struct Workspace {
     int32_t *ntiles = nullptr;    // [1]
     int32_t *chunks = nullptr;    // [dispatch_chunks(T) * E] per-chunk expert counts / first rows
     uint16_t *xh = nullptr;       // [T, H] f16 activations (MFMA path)
+    uint8_t *xq = nullptr;        // [batch_t, H/64] activation units (few-tokens path)
+    uint8_t *hq = nullptr;        // [batch_t * k, I/64] units of h
+    uint8_t *hsq = nullptr;       // [batch_t, I_s/64] units of hs
+    int batch_t = 0;              // tokens the unit buffers have room for
     float *h = nullptr;           // [T*k, I] routed SwiGLU activations (f32, or f16 on the MFMA path)
     float *hs = nullptr;          // [T, I_s] shared-expert activations
     float *y = nullptr;           // [parts][T*k, H] routed expert outputs (parts: split K of the down projection)
@@ -224,6 +228,35 @@ hipError_t launch_mfma(bool up, const MfmaArgs &a, int bm, const ExpertDev &e0, 
 
 // Weighted combine in ascending expert order + shared expert + residual
 // (src/model.rs:936-942, 956-970, 680-683).
+// Few tokens per expert: the experts' rows dotted with int8-encoded
+// activations (qact.h), NT tokens per tile, every weight unit loaded once
+// per tile.  Tiles come from the dispatch tile list built with bm = NT.
+struct BatchArgs {
+    const ExpertDev *experts;
+    const int32_t *tiles, *ntiles;
+    const int32_t *counts, *offsets, *perm_tok;
+    const uint8_t *xq;            // [T, H/64] activation units
+    float *h, *hs;                // f32 [T*k, I], [T, I_s]
+    const uint8_t *hq, *hsq;      // [T*k, I/64], [T, I_s/64] units of h, hs
+    float *y, *ys;                // f32 [parts][T*k, H], [parts][T, H]
+    size_t ypart, yspart;         // elements between the K parts of y, ys
+    int T, H, I, I_s, E;
+    int max_tiles;                // grid height of the routed launch: >= the routed tiles
+    int shared_tiles;             // tiles of the shared expert at the end of the tile list (0 if none)
+    int ksplit;                   // down projection: K parts, part p written at y + p * ypart
+};
+constexpr int kBatchMaxT = 256;   // largest t the few-tokens path is sized for
+// Formats and widths the few-tokens kernels take.
+bool batch_supported(int H, int I, int I_s, int dt_routed, int dt_shared);
+// Tokens per tile (the dispatch's bm) for hidden width H.
+int batch_tile_tokens(int H);
+// K parts of the down projection (each part at most 64 units per row).
+int batch_ksplit(int I, int I_s);
+// Rows [rows, cols] of f32 (cols a multiple of 64) to activation units.
+hipError_t launch_qenc(const float *src, int rows, int cols, uint8_t *dst, hipStream_t s);
+hipError_t launch_batch_up(const BatchArgs &a, const ExpertDev &e0, const ExpertDev *sh, hipStream_t s);
+hipError_t launch_batch_down(const BatchArgs &a, const ExpertDev &e0, const ExpertDev *sh, hipStream_t s);
+
 struct CombineArgs {
     const float *y, *ys;
     int parts;                    // K parts of y and ys, summed in order before weighting

@@ -110,6 +110,12 @@ LAYER_CASES = [
     ("deepseek_v3", 1, None), ("deepseek_v3", 64, None),
     # one-token kernels forced (4) and the register GEMV at T = 1 (2)
     ("tiny_mixtral", 1, 4), ("tiny_mixtral", 1, 2), ("mixtral", 1, 2), ("qwen3", 1, 2), ("deepseek_v3", 1, 2),
+    # few-tokens kernels forced (5): odd tiles, one token per expert, wide rows (one token per tile),
+    # Q5_0 shared expert, two shared experts, K split in four (Mixtral's down rows)
+    ("tiny_mixtral", 7, 5), ("mixtral", 2, 5), ("mixtral", 9, 5), ("qwen3", 3, 5), ("qwen3", 256, 5),
+    ("v2_lite", 5, 5), ("deepseek_v3", 8, 5), ("deepseek_v3", 37, 5),
+    # MFMA at few tokens per expert, where the automatic choice is the few-tokens path
+    ("mixtral", 32, 3), ("v2_lite", 32, 3), ("deepseek_v3", 64, 3),
 ]
 
 

@@ -315,7 +315,9 @@ __global__ __launch_bounds__(NTHR) void decode_down_kernel(DecodeArgs a, int rb,
     const int u0 = L.kw * 64 + (threadIdx.x & 63) % L.cg;
     float hraw[64];
     if constexpr (UPL == 1) {
-        if (L.active && L.live[0]) qact_unit_load(hv + (size_t)u0 * 64, hraw);
+        // Unconditional (lanes without a unit read task 0's first), so that
+        // the encoding below waits for these loads only.
+        qact_unit_load((L.active && L.live[0]) ? hv + (size_t)u0 * 64 : tasks[0].h, hraw);
     } else if (L.active) {
 #pragma unroll
         for (int j = 0; j < UPL; j++)
@@ -331,6 +333,9 @@ __global__ __launch_bounds__(NTHR) void decode_down_kernel(DecodeArgs a, int rb,
     };
 #pragma unroll
     for (int b = 0; b + 1 < NBUF; b++) load(b, w[b]);
+    // Keep every prologue load ahead of the encoding (the scheduler would
+    // otherwise sink some of them below it, where they wait for it).
+    __builtin_amdgcn_sched_barrier(0);
     if constexpr (UPL == 1)
         if (L.active && L.live[0]) qact_unit_encode(hraw, xa[0]);
 

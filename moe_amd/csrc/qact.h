@@ -70,7 +70,9 @@ __device__ inline QBlock qact_block(const float (&v)[32]) {
 // are separate so a caller can issue other loads in between.
 typedef float qa_f32x4 __attribute__((ext_vector_type(4)));
 __device__ inline void qact_unit_load(const float *v, float (&f)[64]) {
-    const qa_f32x4 *s4 = reinterpret_cast<const qa_f32x4 *>(v);
+    // Global loads (not flat ones, which LDS waits would also wait for).
+    typedef const __attribute__((address_space(1))) qa_f32x4 *g4p;
+    const g4p s4 = (g4p)v;
 #pragma unroll
     for (int i = 0; i < 16; i++) {
         const qa_f32x4 t = s4[i];

@@ -289,25 +289,30 @@ __global__ __launch_bounds__(256) void router_tiled_kernel(const float *__restri
 
 // ------------------------------------------------------------------ gating
 
-// Wave-wide argmax of a packed (key << 32 | ~index) value.
-__device__ inline long long wave_max64(long long v) {
-#pragma unroll
-    for (int m = 32; m >= 1; m >>= 1) {
-        long long o = __shfl_xor(v, m, 64);
-        v = o > v ? o : v;
-    }
-    return v;
-}
 __device__ inline float wave_max_rs(float v) {
 #pragma unroll
     for (int m = 32; m >= 1; m >>= 1) v = fmax_rs(v, __shfl_xor(v, m, 64));
     return v;
 }
-__device__ inline long long pack_key(int32_t key, int e) {
-    const unsigned long long hi = (unsigned long long)(uint32_t)key << 32;
-    return (long long)(hi | (0xffffffffu - (uint32_t)e));
+// Wave-wide max of an int32, every lane receiving it: DPP steps within rows
+// of 16 lanes, row broadcasts to lane 63, then a read of lane 63.
+__device__ inline int32_t dpp_max_step(int32_t v, int ctrl) {
+    int o;
+    switch (ctrl) {
+    case 0: o = __builtin_amdgcn_update_dpp(INT32_MIN, v, 0xb1, 0xf, 0xf, false); break;   // quad [1,0,3,2]
+    case 1: o = __builtin_amdgcn_update_dpp(INT32_MIN, v, 0x4e, 0xf, 0xf, false); break;   // quad [2,3,0,1]
+    case 2: o = __builtin_amdgcn_update_dpp(INT32_MIN, v, 0x141, 0xf, 0xf, false); break;  // half-row mirror
+    case 3: o = __builtin_amdgcn_update_dpp(INT32_MIN, v, 0x140, 0xf, 0xf, false); break;  // row mirror
+    case 4: o = __builtin_amdgcn_update_dpp(INT32_MIN, v, 0x142, 0xa, 0xf, false); break;  // row bcast 15
+    default: o = __builtin_amdgcn_update_dpp(INT32_MIN, v, 0x143, 0xc, 0xf, false); break; // row bcast 31
+    }
+    return o > v ? o : v;
 }
-constexpr long long kTaken = (long long)0x8000000000000000ull;
+__device__ inline int32_t wave_max_i32(int32_t v) {
+#pragma unroll
+    for (int c = 0; c < 6; c++) v = dpp_max_step(v, c);
+    return __builtin_amdgcn_readlane(v, 63);
+}
 
 // LDS scratch of one gating wavefront.
 template <int EPL>
@@ -342,11 +347,12 @@ __device__ void gate_token(const float *__restrict__ lg, int t, const GateParams
                            unsigned long long *__restrict__ stats) {
     const int lane = threadIdx.x & 63;
     const int E = p.n_experts;
-    float sc[EPL], rank[EPL];
+    float sc[EPL], rank[EPL], bias[EPL];
 #pragma unroll
-    for (int i = 0; i < EPL; i++) {
+    for (int i = 0; i < EPL; i++) {  // logits and biases requested together
         const int e = lane * EPL + i;
         sc[i] = e < E ? lg[e] : 0.0f;
+        bias[i] = (p.e_bias && e < E) ? p.e_bias[e] : 0.0f;
     }
     if (p.sigmoid) {
 #pragma unroll
@@ -368,8 +374,17 @@ __device__ void gate_token(const float *__restrict__ lg, int t, const GateParams
         }
         wave_sync();
         if (lane == 0) {
+            // Sequential sum (e ascending); reads issued 16 at a time.
             float s = 0.0f;
-            for (int e = 0; e < E; e++) s += S.sc[e];
+            int e = 0;
+            for (; e + 16 <= E; e += 16) {
+                float v[16];
+#pragma unroll
+                for (int u = 0; u < 16; u++) v[u] = S.sc[e + u];
+#pragma unroll
+                for (int u = 0; u < 16; u++) s += v[u];
+            }
+            for (; e < E; e++) s += S.sc[e];
             S.bcast = s;
         }
         wave_sync();
@@ -380,9 +395,63 @@ __device__ void gate_token(const float *__restrict__ lg, int t, const GateParams
 #pragma unroll
     for (int i = 0; i < EPL; i++) {
         const int e = lane * EPL + i;
-        rank[i] = (p.e_bias && e < E) ? sc[i] + p.e_bias[e] : sc[i];
+        rank[i] = (p.e_bias && e < E) ? sc[i] + bias[i] : sc[i];
     }
-    if (p.n_group > 1 && p.topk_group < p.n_group) {
+    const int per_g = p.n_group > 0 ? E / p.n_group : 0, lpg = per_g / EPL;
+    if (p.n_group > 1 && p.topk_group < p.n_group && per_g * p.n_group == E && per_g % EPL == 0 &&
+        (lpg & (lpg - 1)) == 0 && lpg <= 64) {
+        // Groups of lpg whole lanes: each lane takes the top two keys of its
+        // EPL experts, the group's lanes merge theirs by shuffles (the two
+        // largest keys, hence values, do not depend on the merge order), and
+        // the group sum is formed as below: -0.0 + first + second.
+        // Same insertion as the sequential form below: keys equal to
+        // INT32_MIN never enter and leave their slot's value at 0.
+        int32_t k1 = INT32_MIN, k2 = INT32_MIN;
+        auto put = [&](int32_t k) {
+            if (k > k1) {
+                k2 = k1;
+                k1 = k;
+            } else if (k > k2) {
+                k2 = k;
+            }
+        };
+#pragma unroll
+        for (int i = 0; i < EPL; i++) put(tkey(rank[i]));
+        for (int m = 1; m < lpg; m <<= 1) {
+            const int32_t o1 = __shfl_xor(k1, m, 64), o2 = __shfl_xor(k2, m, 64);
+            put(o1);
+            put(o2);
+        }
+        auto val = [](int32_t k) {
+            return k == INT32_MIN ? 0.0f : __int_as_float(k ^ (int32_t)(((uint32_t)(k >> 31)) >> 1));
+        };
+        float gsum = -0.0f;
+        if (per_g >= 1) gsum = gsum + val(k1);
+        if (per_g >= 2) gsum = gsum + val(k2);
+        const int g = lane / lpg;
+        if (lane % lpg == 0) S.gs[g] = gsum;
+        wave_sync();
+        const int32_t kg = tkey(gsum);
+        int position = 0;
+        int g2 = 0;
+        for (; g2 + 8 <= p.n_group; g2 += 8) {  // reads issued 8 at a time
+            float v[8];
+#pragma unroll
+            for (int u = 0; u < 8; u++) v[u] = S.gs[g2 + u];
+#pragma unroll
+            for (int u = 0; u < 8; u++) {
+                const int32_t kk = tkey(v[u]);
+                position += (kk > kg) || (kk == kg && g2 + u < g);
+            }
+        }
+        for (; g2 < p.n_group; g2++) {
+            const int32_t kk = tkey(S.gs[g2]);
+            position += (kk > kg) || (kk == kg && g2 < g);
+        }
+        if (position >= p.topk_group)
+#pragma unroll
+            for (int i = 0; i < EPL; i++) rank[i] = -INFINITY;
+    } else if (p.n_group > 1 && p.topk_group < p.n_group) {
 #pragma unroll
         for (int i = 0; i < EPL; i++)
             if (lane * EPL + i < E) S.rank[lane * EPL + i] = rank[i];
@@ -391,16 +460,24 @@ __device__ void gate_token(const float *__restrict__ lg, int t, const GateParams
         if (lane < p.n_group) {
             int32_t k1 = INT32_MIN, k2 = INT32_MIN;
             float v1 = 0.0f, v2 = 0.0f;
-            for (int i = 0; i < per; i++) {
-                float v = S.rank[lane * per + i];
-                int32_t k = tkey(v);
+            auto take = [&](float v) {
+                const int32_t k = tkey(v);
                 if (k > k1) {
                     k2 = k1, v2 = v1;
                     k1 = k, v1 = v;
                 } else if (k > k2) {
                     k2 = k, v2 = v;
                 }
+            };
+            int i = 0;
+            for (; i + 8 <= per; i += 8) {  // reads issued 8 at a time, taken in order
+                float v[8];
+#pragma unroll
+                for (int u = 0; u < 8; u++) v[u] = S.rank[lane * per + i + u];
+#pragma unroll
+                for (int u = 0; u < 8; u++) take(v[u]);
             }
+            for (; i < per; i++) take(S.rank[lane * per + i]);
             float gsum = -0.0f;
             if (per >= 1) gsum = gsum + v1;
             if (per >= 2) gsum = gsum + v2;
@@ -449,11 +526,20 @@ __device__ void gate_token(const float *__restrict__ lg, int t, const GateParams
         if (lane < E) S.key[lane] = my;
         wave_sync();
         int pos = 0;
-        if (lane < E)
-            for (int e2 = 0; e2 < E; e2++) {
+        if (lane < E) {
+            int e2 = 0;
+            for (; e2 + 8 <= E; e2 += 8) {
+                int32_t kv[8];
+#pragma unroll
+                for (int u = 0; u < 8; u++) kv[u] = S.key[e2 + u];
+#pragma unroll
+                for (int u = 0; u < 8; u++) pos += (kv[u] > my) || (kv[u] == my && e2 + u < lane);
+            }
+            for (; e2 < E; e2++) {
                 const int32_t k2 = S.key[e2];
                 pos += (k2 > my) || (k2 == my && e2 < lane);
             }
+        }
         if (lane < E && pos < k) S.idx[pos] = lane;
         if (lane < E && pos <= k) S.bypos[pos] = my;
         wave_sync();
@@ -462,29 +548,36 @@ __device__ void gate_token(const float *__restrict__ lg, int t, const GateParams
         tie = __any(tie) ? 1 : 0;
     } else {
         // k + 1 rounds of argmax; the extra round finds the best unselected
-        // rank for the tie check.
-        long long cand[EPL];
+        // rank for the tie check.  A round takes the wave's largest key, then
+        // the lowest expert holding it: experts ascend with the lane and,
+        // within a lane, with i, so that is the lowest lane whose best
+        // (lowest i among its largest keys) has the key.
+        int32_t ckey[EPL];
+        bool cfree[EPL];
 #pragma unroll
         for (int i = 0; i < EPL; i++) {
-            const int e = lane * EPL + i;
-            cand[i] = e < E ? pack_key(tkey(rank[i]), e) : kTaken;
+            ckey[i] = tkey(rank[i]);
+            cfree[i] = lane * EPL + i < E;
         }
         int32_t prev_key = 0;
         const int rounds = k < E ? k + 1 : k;
         for (int r = 0; r < rounds; r++) {
-            long long best = kTaken;
+            int bi = -1;
+            int32_t bk = INT32_MIN;
 #pragma unroll
-            for (int i = 0; i < EPL; i++) best = cand[i] > best ? cand[i] : best;
-            best = wave_max64(best);
-            const int e = (int)(0xffffffffu - (uint32_t)(best & 0xffffffffll));
-            const int32_t key = (int32_t)(best >> 32);
+            for (int i = 0; i < EPL; i++)
+                if (cfree[i] && (bi < 0 || ckey[i] > bk)) bk = ckey[i], bi = i;
+            const int32_t key = wave_max_i32(bi >= 0 ? bk : INT32_MIN);
+            const unsigned long long at = __ballot(bi >= 0 && bk == key);
+            const int wl = __builtin_ctzll(at);
+            const int e = wl * EPL + __builtin_amdgcn_readlane(bi, wl);
             if (r > 0 && key == prev_key) tie = 1;
             prev_key = key;
             if (r < k) {
                 if (lane == 0) S.idx[r] = e;
 #pragma unroll
                 for (int i = 0; i < EPL; i++)
-                    if (lane * EPL + i == e) cand[i] = kTaken;
+                    if (lane * EPL + i == e) cfree[i] = false;
             }
         }
     }
@@ -511,17 +604,29 @@ __device__ void gate_token(const float *__restrict__ lg, int t, const GateParams
                 idx[b] = v;
             }
         }
-        float z = -0.0f;
-        for (int j = 0; j < k; j++) z += fmax_rs(S.sc[idx[j]], 0.0f);
-        if (p.norm_topk) z = fmax_rs(z, 1e-20f);
-        for (int j = 0; j < k; j++) {
-            float wv = fmax_rs(S.sc[idx[j]], 0.0f);
-            if (p.norm_topk) wv = wv / z;
-            wv = wv * p.routed_scale;
-            sel[(size_t)t * k + j] = idx[j];
-            wsel[(size_t)t * k + j] = wv;
-            S.w[j] = wv;
-        }
+    }
+    wave_sync();
+    // Weights: lane j < k holds pick j's max(score, 0); the normaliser sums
+    // them in pick order from -0.0 (read lane by lane), then each lane
+    // finishes its own weight.
+    int ij = 0;
+    float vj = 0.0f;
+    if (lane < k) {
+        ij = S.idx[lane];
+        vj = fmax_rs(S.sc[ij], 0.0f);
+    }
+    float z = -0.0f;
+    for (int j = 0; j < k; j++) z += __int_as_float(__builtin_amdgcn_readlane(__float_as_int(vj), j));
+    if (p.norm_topk) z = fmax_rs(z, 1e-20f);
+    if (lane < k) {
+        float wv = vj;
+        if (p.norm_topk) wv = wv / z;
+        wv = wv * p.routed_scale;
+        sel[(size_t)t * k + lane] = ij;
+        wsel[(size_t)t * k + lane] = wv;
+        S.w[lane] = wv;
+    }
+    if (lane == 0) {
         if (p.has_shared_gate) {
             float nv = -lg[E];
             float den = 1.0f + expf_exact(nv);

@@ -206,6 +206,8 @@ def main() -> int:
     ap.add_argument("--shape", default="mixtral")
     ap.add_argument("--tokens", type=int, default=512)
     ap.add_argument("--decode-tokens", type=int, default=1)
+    ap.add_argument("--batch-tokens", type=int, default=32,
+                    help="a few-tokens batch also measured (BASELINE's HBM-bound T=32 row); 0 to skip")
     ap.add_argument("--copies", type=int, default=4, help="distinct weight copies cycled through")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu", action="store_true")
@@ -244,7 +246,7 @@ def main() -> int:
     k = layers[0].k
 
     results = {}
-    for t in (args.decode_tokens, args.tokens):
+    for t in [args.decode_tokens] + ([args.batch_tokens] if args.batch_tokens else []) + [args.tokens]:
         for layer in layers:
             layer.reserve(t)
         x = torch.from_numpy(synth.activations(1, t, shape.hidden)).to(dev)
@@ -270,6 +272,19 @@ def main() -> int:
     layer_bytes = td["up_bytes"] + td["down_bytes"] + shape.n_experts * shape.hidden * 4 + \
         2 * args.decode_tokens * shape.hidden * 4
     layer_gbs = layer_bytes / (td["ms"] * 1e-3) / 1e9
+
+    batch = None
+    if args.batch_tokens:
+        tb = results[args.batch_tokens]
+        b_bytes = tb["up_bytes"] + tb["down_bytes"] + shape.n_experts * shape.hidden * 4 + \
+            2 * args.batch_tokens * shape.hidden * 4
+        b_gbs = b_bytes / (tb["ms"] * 1e-3) / 1e9
+        batch = {"tokens": args.batch_tokens, "value": round(args.batch_tokens / (tb["ms"] * 1e-3), 1),
+                 "unit": "tokens/s", "ms_per_step": round(tb["ms"], 5),
+                 "roofline": {"bound": "hbm", "kernel": "whole layer (hit experts' bytes once)",
+                              "achieved": round(b_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                              "frac": round(b_gbs / HBM_PEAK_GBS, 4)},
+                 "stages_us": {k_: round(v * 1e3, 2) for k_, v in tb["stages"].items()}}
 
     cpu = None
     if not args.no_cpu:
@@ -308,6 +323,7 @@ def main() -> int:
                                 "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(dec_gbs / HBM_PEAK_GBS, 4),
                                 "traffic": traffic_of("decode_up_kernel"), "layer_frac": round(layer_gbs / HBM_PEAK_GBS, 4)},
                    "stages_us": {k_: round(v * 1e3, 2) for k_, v in td["stages"].items()}},
+        "batch": batch,
         "stages_us": {k_: round(v * 1e3, 2) for k_, v in tp["stages"].items()},
     }
     print(json.dumps(line), flush=True)

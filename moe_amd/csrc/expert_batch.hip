@@ -50,22 +50,36 @@ __device__ inline MatDev mat_of(const MatDev *m) {
 
 // ------------------------------------------------------------- encoding
 
-// One thread per 32-value block: rows [rows, cols] of src to units.
+// One wavefront per 64-value unit, one value per lane: lanes 0..31 form
+// block 0, 32..63 block 1.  The block's largest magnitude and the sum of
+// its codes come from shuffles inside each half; every lane then writes its
+// own hi and lo bytes (the unit's bytes i and 64 + i), and lanes 0 and 32
+// their block's s2 and sq.  Same values as qact_block.
 __global__ __launch_bounds__(256) void qenc_kernel(const float *__restrict__ src, int rows, int cols,
                                                    uint8_t *__restrict__ dst) {
     const int units = cols / 64;
-    const long long nb = (long long)rows * units * 2;
-    for (long long i = (long long)blockIdx.x * 256 + threadIdx.x; i < nb; i += (long long)gridDim.x * 256) {
-        const long long r = i / (2 * units);
-        const int rem = (int)(i - r * 2 * units), u = rem >> 1, half = rem & 1;
-        const qa_f32x4 *s4 = reinterpret_cast<const qa_f32x4 *>(src + r * cols + 64 * u + 32 * half);
-        float v[32];
+    const long long n = (long long)rows * units;
+    const int lane = threadIdx.x & 63;
+    const long long w0 = (long long)blockIdx.x * 4 + (threadIdx.x >> 6), nw = (long long)gridDim.x * 4;
+    for (long long w = w0; w < n; w += nw) {
+        const long long r = w / units;
+        const int u = (int)(w - r * units);
+        const float v = gload(src + r * cols + 64 * u + lane);
+        float amax = fmaxf(0.0f, fabsf(v));  // as the sequential fold from 0
 #pragma unroll
-        for (int q = 0; q < 8; q++) {
-            const qa_f32x4 f = gload(s4 + q);
-            v[4 * q] = f.x, v[4 * q + 1] = f.y, v[4 * q + 2] = f.z, v[4 * q + 3] = f.w;
+        for (int m = 16; m >= 1; m >>= 1) amax = fmaxf(amax, __shfl_xor(amax, m, 64));
+        int hi, lo;
+        qact_encode(v, qact_inv(amax), hi, lo);
+        int sq = 254 * hi + lo;
+#pragma unroll
+        for (int m = 16; m >= 1; m >>= 1) sq += __shfl_xor(sq, m, 64);
+        uint8_t *unit = dst + (size_t)w * kQUnitBytes;
+        gstore(unit + lane, (uint8_t)(hi & 0xff));
+        gstore(unit + 64 + lane, (uint8_t)(lo & 0xff));
+        if ((lane & 31) == 0) {
+            gstore(reinterpret_cast<float *>(unit + 128) + (lane >> 5), qact_s2(amax));
+            gstore(reinterpret_cast<int32_t *>(unit + 136) + (lane >> 5), sq);
         }
-        qact_block_put<1>(qact_block(v), dst + ((size_t)r * units + u) * kQUnitBytes, half);
     }
 }
 
@@ -394,8 +408,8 @@ int batch_ksplit(int I, int I_s) {
 hipError_t launch_qenc(const float *src, int rows, int cols, uint8_t *dst, hipStream_t s) {
     if (rows <= 0) return hipSuccess;
     if (cols % 64 != 0) return hipErrorInvalidValue;
-    const long long threads = (long long)rows * (cols / 32);
-    const int grid = (int)std::min<long long>((threads + 255) / 256, 4LL * cus());
+    const long long waves = (long long)rows * (cols / 64);  // one per unit
+    const int grid = (int)std::min<long long>((waves + 3) / 4, 8LL * cus());
     hipLaunchKernelGGL(qenc_kernel, dim3(grid), dim3(256), 0, s, src, rows, cols, dst);
     return hipGetLastError();
 }

@@ -194,28 +194,26 @@ __global__ __launch_bounds__(256) void batch_up_kernel(BatchArgs a, int rpb, int
             load_wunit<DT, DW>(U.ptr + (size_t)r * U.stride + (size_t)u * UB, wb[1][j]);
         }
     };
+    // Branch-free but for the stores: rows past the block re-read valid
+    // rows (load), tokens past the tile have all-zero units, and lanes past
+    // the row's units add nothing.
     auto compute = [&](int s, const uint32_t (&wb)[2][UPL][DW]) {
         const int r = row_of(s);
         float g[NT], u[NT];
 #pragma unroll
         for (int t = 0; t < NT; t++) g[t] = 0.0f, u[t] = 0.0f;
-        if (r < r1) {
 #pragma unroll
-            for (int j = 0; j < UPL; j++)
-                if (live[j]) {
-                    float pg[NT], pu[NT];
-                    qdot_multi<DT, DW, NT>(wb[0][j], xa[j], n, pg);
-                    qdot_multi<DT, DW, NT>(wb[1][j], xa[j], n, pu);
+        for (int j = 0; j < UPL; j++) {
+            float pg[NT], pu[NT];
+            qdot_multi<DT, DW, NT>(wb[0][j], xa[j], pg);
+            qdot_multi<DT, DW, NT>(wb[1][j], xa[j], pu);
 #pragma unroll
-                    for (int t = 0; t < NT; t++) g[t] += pg[t], u[t] += pu[t];
-                }
+            for (int t = 0; t < NT; t++) g[t] += live[j] ? pg[t] : 0.0f, u[t] += live[j] ? pu[t] : 0.0f;
         }
 #pragma unroll
         for (int t = 0; t < NT; t++) {
-            if (t < n) {
-                const float gs = slice_sum(g[t], cg), us = slice_sum(u[t], cg);
-                if (tail && r < r1) gstore(hrow[t] + r, silu_mul(gs, us));
-            }
+            const float gs = slice_sum(g[t], cg), us = slice_sum(u[t], cg);
+            if (tail && r < r1 && t < n) gstore(hrow[t] + r, silu_mul(gs, us));
         }
     };
 #pragma unroll
@@ -279,18 +277,14 @@ __global__ __launch_bounds__(256) void batch_down_kernel(BatchArgs a, int rpb, i
         const int r = min(row_of(min(s, nsteps - 1)), r1 - 1);
         load_wunit<DT, DW>(D.ptr + (size_t)r * D.stride + (size_t)uload * UB, wb);
     };
-    auto compute = [&](int s, const uint32_t (&wb)[DW]) {
+    auto compute = [&](int s, const uint32_t (&wb)[DW]) {  // branch-free as in the gate/up kernel
         const int r = row_of(s);
         float yv[NT];
-#pragma unroll
-        for (int t = 0; t < NT; t++) yv[t] = 0.0f;
-        if (r < r1 && live) qdot_multi<DT, DW, NT>(wb, xa, n, yv);
+        qdot_multi<DT, DW, NT>(wb, xa, yv);
 #pragma unroll
         for (int t = 0; t < NT; t++) {
-            if (t < n) {
-                const float v = slice_sum(yv[t], cg);
-                if (tail && r < r1) gstore(yrow[t] + r, v);
-            }
+            const float v = slice_sum(live ? yv[t] : 0.0f, cg);
+            if (tail && r < r1 && t < n) gstore(yrow[t] + r, v);
         }
     };
 #pragma unroll
@@ -370,17 +364,24 @@ hipError_t down_go(const BatchArgs &a, int K, int tiles, int mode, hipStream_t s
 }
 
 hipError_t up_dt(int dt, const BatchArgs &a, int rows, int tiles, int mode, hipStream_t s) {
-    const bool two = a.H / 64 > 64;  // two units per lane, one token per tile
-    switch (dt) {
-    case MOE_DT_Q4_0: return two ? up_go<MOE_DT_Q4_0, 1, 2>(a, rows, tiles, mode, s) : up_go<MOE_DT_Q4_0, 2, 1>(a, rows, tiles, mode, s);
-    case MOE_DT_Q5_0: return two ? up_go<MOE_DT_Q5_0, 1, 2>(a, rows, tiles, mode, s) : up_go<MOE_DT_Q5_0, 2, 1>(a, rows, tiles, mode, s);
-    case MOE_DT_Q8_0: return two ? up_go<MOE_DT_Q8_0, 1, 2>(a, rows, tiles, mode, s) : up_go<MOE_DT_Q8_0, 2, 1>(a, rows, tiles, mode, s);
+    // Two units per lane (rows wider than 4096) take one token per tile.
+    const int v = a.H / 64 > 64 ? 0 : a.nt == 1 ? 1 : 2;
+    switch (dt * 3 + v) {
+    case MOE_DT_Q4_0 * 3 + 0: return up_go<MOE_DT_Q4_0, 1, 2>(a, rows, tiles, mode, s);
+    case MOE_DT_Q4_0 * 3 + 1: return up_go<MOE_DT_Q4_0, 1, 1>(a, rows, tiles, mode, s);
+    case MOE_DT_Q4_0 * 3 + 2: return up_go<MOE_DT_Q4_0, 2, 1>(a, rows, tiles, mode, s);
+    case MOE_DT_Q5_0 * 3 + 0: return up_go<MOE_DT_Q5_0, 1, 2>(a, rows, tiles, mode, s);
+    case MOE_DT_Q5_0 * 3 + 1: return up_go<MOE_DT_Q5_0, 1, 1>(a, rows, tiles, mode, s);
+    case MOE_DT_Q5_0 * 3 + 2: return up_go<MOE_DT_Q5_0, 2, 1>(a, rows, tiles, mode, s);
+    case MOE_DT_Q8_0 * 3 + 0: return up_go<MOE_DT_Q8_0, 1, 2>(a, rows, tiles, mode, s);
+    case MOE_DT_Q8_0 * 3 + 1: return up_go<MOE_DT_Q8_0, 1, 1>(a, rows, tiles, mode, s);
+    case MOE_DT_Q8_0 * 3 + 2: return up_go<MOE_DT_Q8_0, 2, 1>(a, rows, tiles, mode, s);
     default: return hipErrorInvalidValue;
     }
 }
 
 hipError_t down_dt(int dt, const BatchArgs &a, int K, int tiles, int mode, hipStream_t s) {
-    const bool one = batch_tile_tokens(a.H) == 1;
+    const bool one = a.nt == 1;
     switch (dt) {
     case MOE_DT_Q4_0: return one ? down_go<MOE_DT_Q4_0, 1>(a, K, tiles, mode, s) : down_go<MOE_DT_Q4_0, 2>(a, K, tiles, mode, s);
     case MOE_DT_Q5_0: return one ? down_go<MOE_DT_Q5_0, 1>(a, K, tiles, mode, s) : down_go<MOE_DT_Q5_0, 2>(a, K, tiles, mode, s);
@@ -398,7 +399,7 @@ bool batch_supported(int H, int I, int I_s, int dt_routed, int dt_shared) {
     return true;
 }
 
-int batch_tile_tokens(int H) { return H / 64 > 64 ? 1 : 2; }
+int batch_tile_tokens(int H, int t, int k, int E) { return (H / 64 > 64 || (long long)t * k <= E) ? 1 : 2; }
 
 int batch_ksplit(int I, int I_s) {
     const int units = std::max(I, I_s) / 64;

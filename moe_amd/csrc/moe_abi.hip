@@ -683,7 +683,7 @@ int moe_layer_forward(moe_layer *L, const float *x, int32_t t, float *out, float
         path = L->mfma_ok ? kMfma : kGemv;
         if (t == 1 && L->decode_ok)
             path = kDecode;
-        else if (L->batch_ok && batch_pays(t, k, L->E, batch_tile_tokens(L->H)))
+        else if (L->batch_ok && batch_pays(t, k, L->E, batch_tile_tokens(L->H, t, k, L->E)))
             path = kBatch;
     }
     if (path == kBatch && (!L->batch_ok || t > w.batch_t)) path = L->mfma_ok ? kMfma : kGemv;
@@ -693,7 +693,7 @@ int moe_layer_forward(moe_layer *L, const float *x, int32_t t, float *out, float
         if (t != 1 || !decode_fits(L->I, L->I_s, k, L->has_shared, dt_r, dt_s)) path = kGemv;
     }
     if (path == kMfma && !mfma_fits(t, k, L->H, L->I, L->has_shared ? L->I_s : 0)) path = kGemv;
-    const int bm = path == kMfma ? mfma_tile_m() : path == kBatch ? batch_tile_tokens(L->H) : 0;
+    const int bm = path == kMfma ? mfma_tile_m() : path == kBatch ? batch_tile_tokens(L->H, t, k, L->E) : 0;
     if ((rc = route_and_dispatch(L, x, t, k, bm, path == kDecode, routes, hits, prev, stats, nullptr,
                                  path == kMfma ? w.xh : nullptr, s)))
         return rc;
@@ -753,6 +753,7 @@ int moe_layer_forward(moe_layer *L, const float *x, int32_t t, float *out, float
         b.ypart = (size_t)t * k * L->H;
         b.yspart = (size_t)t * L->H;
         b.ksplit = batch_ksplit(L->I, L->has_shared ? L->I_s : 0);
+        b.nt = bm;
         if ((size_t)b.ksplit * t * k > w.y_rows || (size_t)b.ksplit * t > w.ys_rows)
             return fail(MOE_EUNSUP, "few-tokens path: %d K parts do not fit the workspace", b.ksplit);
         ksplit = b.ksplit;

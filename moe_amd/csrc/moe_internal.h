@@ -244,12 +244,15 @@ struct BatchArgs {
     int max_tiles;                // grid height of the routed launch: >= the routed tiles
     int shared_tiles;             // tiles of the shared expert at the end of the tile list (0 if none)
     int ksplit;                   // down projection: K parts, part p written at y + p * ypart
+    int nt;                       // tokens per tile (the dispatch's bm): 1 or 2
 };
 constexpr int kBatchMaxT = 256;   // largest t the few-tokens path is sized for
 // Formats and widths the few-tokens kernels take.
 bool batch_supported(int H, int I, int I_s, int dt_routed, int dt_shared);
-// Tokens per tile (the dispatch's bm) for hidden width H.
-int batch_tile_tokens(int H);
+// Tokens per tile (the dispatch's bm) for hidden width H and t tokens with
+// k experts each over E experts: 1 for rows wider than 4096 or at most one
+// token per expert on average, else 2.
+int batch_tile_tokens(int H, int t, int k, int E);
 // K parts of the down projection (each part at most 64 units per row).
 int batch_ksplit(int I, int I_s);
 // Rows [rows, cols] of f32 (cols a multiple of 64) to activation units.

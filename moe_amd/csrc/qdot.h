@@ -161,11 +161,10 @@ __device__ inline float silu_mul(float g, float u) { return (g / (1.0f + __expf(
 __device__ inline int lanes_for(int units) { return units <= 16 ? 16 : units <= 32 ? 32 : 64; }
 
 // A weight unit dotted with the activation units of NT tokens: out[t] for
-// t < n (the weights are unpacked once for all of them).  Same arithmetic
-// as qdot per token.
+// every t (the weights are unpacked once for all of them; callers pad with
+// all-zero units, whose dots are zero).  Same arithmetic as qdot per token.
 template <int DT, int DN, int NT>
-__device__ inline void qdot_multi(const uint32_t (&d)[DN], const uint32_t (&x)[NT][kQUnitDw], int n,
-                                  float (&out)[NT]) {
+__device__ inline void qdot_multi(const uint32_t (&d)[DN], const uint32_t (&x)[NT][kQUnitDw], float (&out)[NT]) {
     static_assert(DN >= WUnit<DT>::dw, "unit buffer too small");
     int Aa[NT], Ab[NT], Ba[NT], Bb[NT];
     float sa, sb;
@@ -191,12 +190,10 @@ __device__ inline void qdot_multi(const uint32_t (&d)[DN], const uint32_t (&x)[N
             }
 #pragma unroll
             for (int t = 0; t < NT; t++) {
-                if (t < n) {
-                    Aa[t] = sdot4(la, x[t][i], Aa[t]), Aa[t] = sdot4(ha, x[t][4 + i], Aa[t]);
-                    Ba[t] = sdot4(la, x[t][16 + i], Ba[t]), Ba[t] = sdot4(ha, x[t][20 + i], Ba[t]);
-                    Ab[t] = sdot4(lb, x[t][8 + i], Ab[t]), Ab[t] = sdot4(hb, x[t][12 + i], Ab[t]);
-                    Bb[t] = sdot4(lb, x[t][24 + i], Bb[t]), Bb[t] = sdot4(hb, x[t][28 + i], Bb[t]);
-                }
+                Aa[t] = sdot4(la, x[t][i], Aa[t]), Aa[t] = sdot4(ha, x[t][4 + i], Aa[t]);
+                Ba[t] = sdot4(la, x[t][16 + i], Ba[t]), Ba[t] = sdot4(ha, x[t][20 + i], Ba[t]);
+                Ab[t] = sdot4(lb, x[t][8 + i], Ab[t]), Ab[t] = sdot4(hb, x[t][12 + i], Ab[t]);
+                Bb[t] = sdot4(lb, x[t][24 + i], Bb[t]), Bb[t] = sdot4(hb, x[t][28 + i], Bb[t]);
             }
         }
     } else {
@@ -206,10 +203,8 @@ __device__ inline void qdot_multi(const uint32_t (&d)[DN], const uint32_t (&x)[N
             const uint32_t qa = alignb(d[i + 1], d[i], 2), qb = d[9 + i];
 #pragma unroll
             for (int t = 0; t < NT; t++) {
-                if (t < n) {
-                    Aa[t] = sdot4(qa, x[t][i], Aa[t]), Ba[t] = sdot4(qa, x[t][16 + i], Ba[t]);
-                    Ab[t] = sdot4(qb, x[t][8 + i], Ab[t]), Bb[t] = sdot4(qb, x[t][24 + i], Bb[t]);
-                }
+                Aa[t] = sdot4(qa, x[t][i], Aa[t]), Ba[t] = sdot4(qa, x[t][16 + i], Ba[t]);
+                Ab[t] = sdot4(qb, x[t][8 + i], Ab[t]), Bb[t] = sdot4(qb, x[t][24 + i], Bb[t]);
             }
         }
     }

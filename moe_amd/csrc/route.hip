@@ -193,25 +193,31 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 2))) voi
 // fma(0, 0, acc) == acc for every acc a chain can hold (chains start at +0
 // and never reach -0), so padding does not change a single bit.
 constexpr int kRT = 32;   // rows per tile
-constexpr int kTT = 32;   // tokens per tile
 constexpr int kKC = 64;   // K chunk
+template <int TPT>
 __global__ __launch_bounds__(256) void router_tiled_kernel(const float *__restrict__ W, const float *__restrict__ x,
                                                            int T, int n_rows, int E, int H, float temp,
                                                            float *__restrict__ logits, __half *__restrict__ xh) {
-    __shared__ __attribute__((aligned(16))) float wt[kRT][kKC + 4];
-    __shared__ __attribute__((aligned(16))) float xt[kTT][kKC + 4];
+    // Rows 80 floats apart (16 banks mod 32), and router row rg * 8 + i kept
+    // at i * 4 + rg: the four row groups a wavefront reads at once then fall
+    // in different bank halves (token rows are read as broadcasts).
+    constexpr int kLS = kKC + 16;
+    __shared__ __attribute__((aligned(16))) float wt[kRT][kLS];
+    constexpr int kTTv = 4 * TPT;  // tokens per tile: TPT per thread
+    __shared__ __attribute__((aligned(16))) float xt[kTTv][kLS];
     const int tid = threadIdx.x, j = tid & 15, g = tid >> 4;
     const int rg = g & 3, tg = g >> 2;
-    const int r0 = blockIdx.x * kRT, t0 = blockIdx.y * kTT;
+    const int r0 = blockIdx.x * kRT, t0 = blockIdx.y * kTTv;
     const int n16 = H / 16;
     const int kfull = n16 * 16;  // elements covered by full 16-chunks
-    float acc[8][8];
+    float acc[8][TPT];
 #pragma unroll
     for (int i = 0; i < 8; i++)
 #pragma unroll
-        for (int u = 0; u < 8; u++) acc[i][u] = 0.0f;
-    // Each thread moves 2 float4 of W and 2 of x per chunk (32 rows x 16
-    // float4); the next chunk's loads are issued before this chunk's FMAs.
+        for (int u = 0; u < TPT; u++) acc[i][u] = 0.0f;
+    // Each thread moves 2 float4 of W (32 rows x 16 float4) and up to 2 of x
+    // (kTTv tokens) per chunk; the next chunk's loads are issued before this
+    // chunk's FMAs.
     const bool vec = (H & 3) == 0;
     float4 pw[2], px[2];
     auto load_chunk = [&](int k0) {
@@ -222,12 +228,12 @@ __global__ __launch_bounds__(256) void router_tiled_kernel(const float *__restri
             float4 w4 = make_float4(0.f, 0.f, 0.f, 0.f), x4 = w4;
             if (vec) {
                 if (gr < n_rows && gk < kfull) w4 = *reinterpret_cast<const float4 *>(W + (size_t)gr * H + gk);
-                if (gt < T && gk < kfull) x4 = *reinterpret_cast<const float4 *>(x + (size_t)gt * H + gk);
+                if (rr < kTTv && gt < T && gk < kfull) x4 = *reinterpret_cast<const float4 *>(x + (size_t)gt * H + gk);
             } else {
                 float *wp = &w4.x, *xp = &x4.x;
                 for (int e = 0; e < 4; e++) {
                     if (gr < n_rows && gk + e < kfull) wp[e] = W[(size_t)gr * H + gk + e];
-                    if (gt < T && gk + e < kfull) xp[e] = x[(size_t)gt * H + gk + e];
+                    if (rr < kTTv && gt < T && gk + e < kfull) xp[e] = x[(size_t)gt * H + gk + e];
                 }
             }
             pw[u] = w4, px[u] = x4;
@@ -238,11 +244,11 @@ __global__ __launch_bounds__(256) void router_tiled_kernel(const float *__restri
 #pragma unroll
         for (int u = 0; u < 2; u++) {
             const int q = tid + 256 * u, rr = q >> 4, kk = (q & 15) * 4;
-            *reinterpret_cast<float4 *>(&wt[rr][kk]) = pw[u];
-            *reinterpret_cast<float4 *>(&xt[rr][kk]) = px[u];
+            *reinterpret_cast<float4 *>(&wt[(rr & 7) * 4 + (rr >> 3)][kk]) = pw[u];
+            if (rr < kTTv) *reinterpret_cast<float4 *>(&xt[rr][kk]) = px[u];
             // The first row range writes the f16 copy (launched only when
             // the chunks cover all of H, i.e. H % 16 == 0).
-            if (xh && blockIdx.x == 0 && t0 + rr < T && k0 + kk < kfull) {
+            if (xh && blockIdx.x == 0 && rr < kTTv && t0 + rr < T && k0 + kk < kfull) {
                 __half *o = xh + (size_t)(t0 + rr) * H + k0 + kk;
                 o[0] = __float2half_rn(px[u].x);
                 o[1] = __float2half_rn(px[u].y);
@@ -254,15 +260,15 @@ __global__ __launch_bounds__(256) void router_tiled_kernel(const float *__restri
         if (k0 + kKC < kfull) load_chunk(k0 + kKC);
 #pragma unroll
         for (int s = 0; s < kKC / 16; s++) {
-            float wv[8], xv[8];
+            float wv[8], xv[TPT];
 #pragma unroll
-            for (int i = 0; i < 8; i++) wv[i] = wt[rg * 8 + i][16 * s + j];
+            for (int i = 0; i < 8; i++) wv[i] = wt[i * 4 + rg][16 * s + j];
 #pragma unroll
-            for (int u = 0; u < 8; u++) xv[u] = xt[tg * 8 + u][16 * s + j];
+            for (int u = 0; u < TPT; u++) xv[u] = xt[tg * TPT + u][16 * s + j];
 #pragma unroll
             for (int i = 0; i < 8; i++)
 #pragma unroll
-                for (int u = 0; u < 8; u++) acc[i][u] = fmaf(wv[i], xv[u], acc[i][u]);
+                for (int u = 0; u < TPT; u++) acc[i][u] = fmaf(wv[i], xv[u], acc[i][u]);
         }
         __syncthreads();
     }
@@ -272,8 +278,8 @@ __global__ __launch_bounds__(256) void router_tiled_kernel(const float *__restri
     for (int i = 0; i < 8; i++) {
         const int r = r0 + rg * 8 + i;
 #pragma unroll
-        for (int u = 0; u < 8; u++) {
-            const int t = t0 + tg * 8 + u;
+        for (int u = 0; u < TPT; u++) {
+            const int t = t0 + tg * TPT + u;
             float a = acc[i][u];
             const bool valid = r < n_rows && t < T;
             if (has8 && j < 8 && valid) a = fmaf(W[(size_t)r * H + kfull + j], x[(size_t)t * H + kfull + j], a);
@@ -1114,10 +1120,13 @@ hipError_t launch_router(const float *W, const float *x, int T, int n_rows, int 
             const double t = rounds * (trips + per_cu * lds / 64.0 / clk_us + (H / 16) * 10.0 / clk_us);
             if (t < best) best = t, best_rb = RB, best_tb = TB;
         }
-    // The tiled kernel: 32 x 32 tiles, about three blocks per CU, ~1150
-    // cycles per 64-value K chunk.
-    const double tiled_blocks = (double)((n_rows + kRT - 1) / kRT) * ((T + kTT - 1) / kTT);
-    const double tiled = std::ceil(tiled_blocks / (256.0 * 3)) * (H / 64.0) * 1150.0 / clk_us;
+    // The tiled kernel: 32 rows x 4 TPT tokens, TPT = 8 unless that leaves
+    // fewer than three blocks per CU (latency then shows: 32 x 32 tiles at
+    // one block per CU ran 4.5x slower than their FMA count); ~1150 cycles
+    // per 64-value K chunk at TPT = 8.
+    auto tiles_of = [&](int tpt) { return (double)((n_rows + kRT - 1) / kRT) * ((T + 4 * tpt - 1) / (4 * tpt)); };
+    const int tpt = tiles_of(8) >= 3 * 256 ? 8 : tiles_of(4) >= 3 * 256 ? 4 : 2;
+    const double tiled = std::ceil(tiles_of(8) / (256.0 * 3)) * (H / 64.0) * 1150.0 / clk_us;
     if (best_rb > 0 && best <= tiled) {
         const int RB = best_rb, TB = best_tb;
         dim3 grid((n_rows + RB - 1) / RB, (T + TB - 1) / TB);
@@ -1131,9 +1140,14 @@ hipError_t launch_router(const float *W, const float *x, int T, int n_rows, int 
         hipLaunchKernelGGL(router_lds_kernel, grid, dim3(256), lds, s, W, x, T, n_rows, E, H, RB, TB, temp, logits,
                            xh);
     } else {
-        dim3 grid((n_rows + kRT - 1) / kRT, (T + kTT - 1) / kTT);
-        hipLaunchKernelGGL(router_tiled_kernel, grid, dim3(256), 0, s, W, x, T, n_rows, E, H, temp, logits,
-                           (H % 16 == 0) ? xh : nullptr);
+        dim3 grid((n_rows + kRT - 1) / kRT, (T + 4 * tpt - 1) / (4 * tpt));
+        __half *xo = (H % 16 == 0) ? xh : nullptr;
+        if (tpt == 8)
+            hipLaunchKernelGGL(router_tiled_kernel<8>, grid, dim3(256), 0, s, W, x, T, n_rows, E, H, temp, logits, xo);
+        else if (tpt == 4)
+            hipLaunchKernelGGL(router_tiled_kernel<4>, grid, dim3(256), 0, s, W, x, T, n_rows, E, H, temp, logits, xo);
+        else
+            hipLaunchKernelGGL(router_tiled_kernel<2>, grid, dim3(256), 0, s, W, x, T, n_rows, E, H, temp, logits, xo);
         if (xh && H % 16 != 0) {
             hipError_t e = hipGetLastError();
             if (e != hipSuccess) return e;

@@ -198,10 +198,10 @@ template <int TPT>
 __global__ __launch_bounds__(256) void router_tiled_kernel(const float *__restrict__ W, const float *__restrict__ x,
                                                            int T, int n_rows, int E, int H, float temp,
                                                            float *__restrict__ logits, __half *__restrict__ xh) {
-    // Rows 80 floats apart (16 banks mod 32), and router row rg * 8 + i kept
-    // at i * 4 + rg: the four row groups a wavefront reads at once then fall
-    // in different bank halves (token rows are read as broadcasts).
-    constexpr int kLS = kKC + 16;
+    // A chunk row holds its 64 values transposed, value 16 s + j at 4 j + s,
+    // so that chain lane j reads its four values of the chunk (s = 0..3) with
+    // one 16-byte read; eight lanes then read 128 contiguous bytes.
+    constexpr int kLS = kKC;
     __shared__ __attribute__((aligned(16))) float wt[kRT][kLS];
     constexpr int kTTv = 4 * TPT;  // tokens per tile: TPT per thread
     __shared__ __attribute__((aligned(16))) float xt[kTTv][kLS];
@@ -244,8 +244,16 @@ __global__ __launch_bounds__(256) void router_tiled_kernel(const float *__restri
 #pragma unroll
         for (int u = 0; u < 2; u++) {
             const int q = tid + 256 * u, rr = q >> 4, kk = (q & 15) * 4;
-            *reinterpret_cast<float4 *>(&wt[(rr & 7) * 4 + (rr >> 3)][kk]) = pw[u];
-            if (rr < kTTv) *reinterpret_cast<float4 *>(&xt[rr][kk]) = px[u];
+            // Values kk..kk+3 are (s, j) = (kk / 16, kk % 16 + e).
+            const int s0 = kk >> 4, j0 = kk & 15;
+            float *wr = &wt[rr][0];
+            wr[4 * (j0 + 0) + s0] = pw[u].x, wr[4 * (j0 + 1) + s0] = pw[u].y;
+            wr[4 * (j0 + 2) + s0] = pw[u].z, wr[4 * (j0 + 3) + s0] = pw[u].w;
+            if (rr < kTTv) {
+                float *xr = &xt[rr][0];
+                xr[4 * (j0 + 0) + s0] = px[u].x, xr[4 * (j0 + 1) + s0] = px[u].y;
+                xr[4 * (j0 + 2) + s0] = px[u].z, xr[4 * (j0 + 3) + s0] = px[u].w;
+            }
             // The first row range writes the f16 copy (launched only when
             // the chunks cover all of H, i.e. H % 16 == 0).
             if (xh && blockIdx.x == 0 && rr < kTTv && t0 + rr < T && k0 + kk < kfull) {
@@ -258,17 +266,23 @@ __global__ __launch_bounds__(256) void router_tiled_kernel(const float *__restri
         }
         __syncthreads();
         if (k0 + kKC < kfull) load_chunk(k0 + kKC);
+        static_assert(kKC == 64, "four 16-value steps per chunk");
+        float4 wq[8], xq[TPT];
 #pragma unroll
-        for (int s = 0; s < kKC / 16; s++) {
-            float wv[8], xv[TPT];
+        for (int i = 0; i < 8; i++) wq[i] = *reinterpret_cast<const float4 *>(&wt[rg * 8 + i][4 * j]);
 #pragma unroll
-            for (int i = 0; i < 8; i++) wv[i] = wt[i * 4 + rg][16 * s + j];
+        for (int u = 0; u < TPT; u++) xq[u] = *reinterpret_cast<const float4 *>(&xt[tg * TPT + u][4 * j]);
 #pragma unroll
-            for (int u = 0; u < TPT; u++) xv[u] = xt[tg * TPT + u][16 * s + j];
+        for (int s = 0; s < 4; s++) {
 #pragma unroll
-            for (int i = 0; i < 8; i++)
+            for (int i = 0; i < 8; i++) {
+                const float wv = s == 0 ? wq[i].x : s == 1 ? wq[i].y : s == 2 ? wq[i].z : wq[i].w;
 #pragma unroll
-                for (int u = 0; u < TPT; u++) acc[i][u] = fmaf(wv[i], xv[u], acc[i][u]);
+                for (int u = 0; u < TPT; u++) {
+                    const float xv = s == 0 ? xq[u].x : s == 1 ? xq[u].y : s == 2 ? xq[u].z : xq[u].w;
+                    acc[i][u] = fmaf(wv, xv, acc[i][u]);
+                }
+            }
         }
         __syncthreads();
     }

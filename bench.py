@@ -186,16 +186,16 @@ def summarize_pmc(fetch_dir: str, write_dir: str, out_json: str) -> int:
 
 
 def traffic_of(kernel_prefix: str):
-    """HBM bytes per launch of the first kernel whose name starts with
-    kernel_prefix, from the committed counter summary (None if absent)."""
+    """HBM bytes per launch of the kernel whose name starts with
+    kernel_prefix, from the committed counter summary (None if absent).  The
+    bench launches some kernels at two sizes (T=32 and T=512); the launch
+    with the largest grid is the one the headline roofline describes."""
     try:
         doc = json.load(open(TRAFFIC_FILE))
     except (OSError, ValueError):
         return None
-    for k in doc["kernels"]:
-        if k["kernel"].startswith(kernel_prefix):
-            return k["hbm_bytes"]
-    return None
+    hits = [k for k in doc["kernels"] if k["kernel"].startswith(kernel_prefix)]
+    return max(hits, key=lambda k: k.get("grid", 0))["hbm_bytes"] if hits else None
 
 
 def main() -> int:

@@ -296,3 +296,45 @@ def test_interventions(ctx, oracle, kind):
         assert victim not in set(g["sel"].ravel().tolist())
     if kind == "forced":
         assert all(target in row for row in g["sel"].tolist())
+
+
+def test_trace_file_from_gpu_routes(ctx, oracle, tmp_path):
+    """A traced prefill then a decode step, written as the reference's JSONL
+    trace (src/main.rs:771-799) and read back (src/route.rs:58-90): every
+    route line holds the CPU path's experts and weights, and the counts
+    match its selections."""
+    import json
+
+    import torch
+
+    from moe_amd import synth
+    from moe_amd.layer import State
+    from moe_amd.trace import Counts, write_trace
+
+    host, gl, ol = layer_pair(ctx, oracle, "tiny_mixtral")
+    st = State(1, trace=True)
+    dev = torch.device("cuda:0")
+    want = []
+    for i, t in enumerate([12, 1]):
+        x = synth.activations(SEED + 40 + i, t, 512)
+        _, sel, w, _, _ = ol.forward(x)
+        want += [(st.pos + j, sel[j].tolist(), w[j].tolist()) for j in range(t)]
+        xd = torch.from_numpy(x).to(dev)
+        out = torch.empty_like(xd)
+        gl.feed_forward(xd, out, state=st)
+        st.pos += t
+    torch.cuda.synchronize()
+    path = tmp_path / "routes.jsonl"
+    assert write_trace(str(path), st.trace, "mixtral", 1, 8, 2) == 13
+    lines = [json.loads(s) for s in path.read_text().splitlines()]
+    assert lines[0] == {"experts": 8, "layers": 1, "model": "mixtral", "top_k": 2}
+    for rec, (pos, sel, w) in zip(lines[1:], want):
+        assert rec["pos"] == pos and rec["layer"] == 0 and rec["token"] is None
+        assert [e for e, _ in rec["experts"]] == sel
+        # The weights read back as the exact f32 the CPU path computed.
+        assert np.array_equal(np.float32([v for _, v in rec["experts"]]).view(np.uint32),
+                              np.float32(w).view(np.uint32))
+    c = Counts.read(str(path))
+    assert c.tokens == 13 and c.experts == 8 and c.top_k == 2
+    for e in range(8):
+        assert c.count(0, e) == sum(sel.count(e) for _, sel, _ in want)

@@ -235,6 +235,40 @@ class MoeSpec:
     topk_group: int = 1
 
 
+class Mlp:
+    """A dense SwiGLU MLP, Mlp::forward (src/model.rs:20-40), as Ffn::Dense
+    runs it (src/model.rs:840), on the expert kernels.
+
+    It is a routed layer with one expert and a router row of zeros: the
+    softmax over one logit gives the expert weight exp(0) / exp(0) = 1, the
+    renormalisation divides by 1, and the combine writes 0 + 1 * y = y, so
+    the output is the expert's output unchanged; the routing stages add a
+    few microseconds per call."""
+
+    def __init__(self, ctx: "Context", gate: View, up: View, down: View):
+        if not (gate.rows == up.rows == down.cols and gate.cols == up.cols == down.rows):
+            raise ValueError(f"gate {gate.rows}x{gate.cols}, up {up.rows}x{up.cols}, down {down.rows}x{down.cols}"
+                             " do not form an MLP")
+        self.hidden, self.inter = gate.cols, gate.rows
+        self._router_region = ctx.upload(np.zeros(self.hidden, dtype=np.float32))
+        router = View(L.DT_F32, 1, self.hidden, self._router_region.id, 0)
+        self.layer = MoeLayer(ctx, MoeSpec(hidden=self.hidden, n_experts=1, top_k=1), router, [(gate, up, down)])
+
+    def set_mode(self, mode: int) -> None:
+        self.layer.set_mode(mode)
+
+    def reserve(self, max_t: int) -> None:
+        self.layer.reserve(max_t)
+
+    def forward(self, x, out, residual=None, stream=None) -> None:
+        """out = down(silu(gate x) * up x) for x [t, hidden] f32 (CUDA);
+        residual += out when given."""
+        self.layer.feed_forward(x, out, residual=residual, stream=stream)
+
+    def close(self) -> None:
+        self.layer.close()
+
+
 class MoeLayer:
     """Ffn::Moe on the GPU (src/model.rs:68-71, 841-971)."""
 

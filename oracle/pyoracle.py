@@ -132,6 +132,15 @@ def matmul(w: QT, x: np.ndarray) -> np.ndarray:
     return out
 
 
+def mlp_forward(gate: QT, up: QT, down: QT, x: np.ndarray) -> np.ndarray:
+    """Mlp::forward (src/model.rs:26-35): down(silu(gate x) * up x)."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    t = x.shape[0]
+    out = np.empty((t, down.rows), dtype=np.float32)
+    lib().orc_mlp_forward(C.byref(gate), C.byref(up), C.byref(down), _p(x), t, _p(out))
+    return out
+
+
 def expf(x: float) -> np.float32:
     return np.float32(lib().orc_expf(float(x)))
 

@@ -199,3 +199,30 @@ def test_forward_single_expert_matches_mlp(oracle):
     ref = ((gx / (1 + np.exp(-gx))) * ux) @ d.T
     assert np.abs(out - ref).max() < 1e-5 * np.abs(ref).max() + 1e-6
     assert stats.tolist() == [5, 0, 3 * 4 * H * I, 0]
+
+
+def test_mlp_is_swiglu_of_the_matmuls(oracle):
+    """Mlp::forward (src/model.rs:26-35) is down(silu(g) * u) with
+    g = matmul(gate, x), u = matmul(up, x) and silu(g) = g / (1 + exp(-g)):
+    divide, then multiply, each rounded to f32, exp from glibc.  The
+    composition from the pinned matmul and expf equals the oracle's MLP bit
+    for bit; dropping the divide's order (g * sigmoid(g)) or fusing breaks
+    it somewhere on these inputs."""
+    from moe_amd import synth
+
+    H, I, t = 128, 96, 5
+    rng = np.random.default_rng(11)
+    w = {n: (rng.standard_normal((r, c)) * 0.2).astype(np.float32)
+         for n, r, c in [("gate", I, H), ("up", I, H), ("down", H, I)]}
+    qts = {n: oracle.qt(F32, a.shape[0], a.shape[1], a.view(np.uint8).reshape(-1)) for n, a in w.items()}
+    x = synth.normal(5, 1, t * H).reshape(t, H)
+    got = oracle.mlp_forward(qts["gate"], qts["up"], qts["down"], x)
+    g = oracle.matmul(qts["gate"], x)
+    u = oracle.matmul(qts["up"], x)
+    e = oracle.expf_array(-g)
+    h = (g / (np.float32(1.0) + e)).astype(np.float32) * u
+    want = oracle.matmul(qts["down"], h.astype(np.float32))
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+    # A plausible mistake, g * (1 / (1 + e)), rounds differently.
+    h2 = (g * (np.float32(1.0) / (np.float32(1.0) + e))).astype(np.float32) * u
+    assert not np.array_equal(oracle.matmul(qts["down"], h2).view(np.uint32), got.view(np.uint32))

@@ -442,7 +442,7 @@ __global__ __launch_bounds__(256, 1) __attribute__((amdgpu_waves_per_eu(1, 1))) 
         // broadcasts); each lane then picks its dwords (Slots: base, or
         // base + 2 for the upper lane half).
         half8 bq[2][2][2];  // [kb][j][m]
-        half8 af[2][MT];
+        half8 af[4][MT];    // one per group, read two groups ahead
         uint32_t rowv[2][BL::rd];
         auto read_rows = [&](lds_p stage_b) {
 #pragma unroll
@@ -512,6 +512,7 @@ __global__ __launch_bounds__(256, 1) __attribute__((amdgpu_waves_per_eu(1, 1))) 
         for (int p = 0; p < NS - 1; p++) dma_range(I0{}, std::integral_constant<int, ND>{}, p, p);
         wait_vm_barrier<(NS - 2) * ND>();
         read_a(sm, 0, af[0]);
+        read_a(sm, 1, af[1]);
         read_rows(smB);
         dequant_raw(I0{}, bq[0]);
         int st = 0;
@@ -527,30 +528,30 @@ __global__ __launch_bounds__(256, 1) __attribute__((amdgpu_waves_per_eu(1, 1))) 
             const lds_p sa = sm + st * A_STAGE;
             const int st1 = st + 1 == NS ? 0 : st + 1, stn = st == 0 ? NS - 1 : st - 1;
             const int sn = s + NS - 1;
-            // g = 0 (kb 0, m 0): group 1's activations first.
-            read_a(sa, 1, af[1]);
+            // g = 0 (kb 0, m 0): group 2's activations first.
+            read_a(sa, 2, af[2]);
             __builtin_amdgcn_sched_barrier(0);
             mfmas_dma(af[0], bq[0], 0, I0{}, std::integral_constant<int, MA>{}, sn, stn);
-            // g = 1 (kb 0, m 1): dequantise block 1, read group 2.
+            // g = 1 (kb 0, m 1): dequantise block 1, read group 3.
             dequant_raw(I1{}, bq[1]);
-            read_a(sa, 2, af[0]);
+            read_a(sa, 3, af[3]);
             mfmas_dma(af[1], bq[0], 1, std::integral_constant<int, MA>{}, std::integral_constant<int, MT>{}, sn, stn);
             __builtin_amdgcn_sched_barrier(0);
-            // g = 2 (kb 1, m 0): read group 3; then wait for this wave's
-            // loads of step s + 1 and meet the other waves, after which step
-            // s + 1's stage is complete and nobody reads stage s any more.
-            read_a(sa, 3, af[1]);
-            mfmas(af[0], bq[1], 0);
+            // g = 2 (kb 1, m 0); then wait for this wave's loads of step
+            // s + 1 and meet the other waves, after which step s + 1's stage
+            // is complete and nobody reads stage s any more.
+            mfmas(af[2], bq[1], 0);
             __builtin_amdgcn_sched_barrier(0);
             wait_vm_barrier<WAIT>();
             __builtin_amdgcn_sched_barrier(0);
-            // g = 3 (kb 1, m 1): step s + 1's group 0 and weight rows; step
-            // s + NS - 1's weight DMAs.
+            // g = 3 (kb 1, m 1): step s + 1's groups 0 and 1 and weight
+            // rows; step s + NS - 1's weight DMAs.
             const lds_p sa1 = sm + st1 * A_STAGE;
             read_a(sa1, 0, af[0]);
+            read_a(sa1, 1, af[1]);
             read_rows(smB + st1 * BL::stage);
             __builtin_amdgcn_sched_barrier(0);
-            mfmas_dma(af[1], bq[1], 1, std::integral_constant<int, MT>{}, std::integral_constant<int, ND>{}, sn, stn);
+            mfmas_dma(af[3], bq[1], 1, std::integral_constant<int, MT>{}, std::integral_constant<int, ND>{}, sn, stn);
             dequant_raw(I0{}, bq[0]);
             __builtin_amdgcn_sched_barrier(0);
             st = st1;

@@ -75,12 +75,15 @@ def stage_times(layers, x, out, steps: int):
     for i in range(steps):
         layers[i % len(layers)].feed_forward(x, out)
     torch.cuda.synchronize()
-    ms = (C.c_double * 6)()
-    n = (C.c_uint64 * 6)()
+    ns = len(L.STAGES)
+    ms = (C.c_double * ns)()
+    n = (C.c_uint64 * ns)()
     for layer in layers:
         L.check(L.lib().moe_layer_stage_times(layer.handle, ms, n))
         L.check(L.lib().moe_layer_profile(layer.handle, 0))
-    return {L.STAGES[i]: (ms[i] / n[i] if n[i] else 0.0) for i in range(6)}
+    # Per step: a stage launched twice per forward (the activation encoding
+    # runs before gate/up and before down) counts both launches.
+    return {L.STAGES[i]: (ms[i] / steps if n[i] else 0.0) for i in range(ns)}
 
 
 def selected_bytes(layer, host, x) -> tuple[int, int]:
@@ -101,8 +104,20 @@ def selected_bytes(layer, host, x) -> tuple[int, int]:
     return up, down
 
 
-def cpu_baseline(host, t_decode: int, t_prefill: int, seconds: float):
-    """The CPU restatement of the reference path on this host's cores."""
+def cpu_model() -> str:
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def cpu_baseline(host, t_decode: int, t_prefill: int, runs: int = 5):
+    """The CPU restatement of the reference path on this host's cores: per
+    T, one warm-up forward (it also pages in the weights), then the median
+    of `runs` timed forwards (SURVEY's protocol for the CPU baseline)."""
     sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
     from moe_amd import synth
     from oracle import pyoracle
@@ -110,20 +125,17 @@ def cpu_baseline(host, t_decode: int, t_prefill: int, seconds: float):
     pyoracle.build()
     ol = pyoracle.from_host_layer(host)
     cores = int(pyoracle.lib().orc_max_threads())
-    xd = synth.activations(1, t_decode, host.shape.hidden)
-    ol.forward(xd)  # warm: pages in the weights
-    n, t0 = 0, time.perf_counter()
-    while time.perf_counter() - t0 < seconds * 0.5:
-        ol.forward(xd)
-        n += 1
-    dec = n * t_decode / (time.perf_counter() - t0)
-    xp = synth.activations(1, t_prefill, host.shape.hidden)
-    n, t0 = 0, time.perf_counter()
-    while n < 1 or time.perf_counter() - t0 < seconds * 0.5:
-        ol.forward(xp)
-        n += 1
-    pre = n * t_prefill / (time.perf_counter() - t0)
-    return dec, pre, cores, n
+    res = {}
+    for t in (t_decode, t_prefill):
+        x = synth.activations(1, t, host.shape.hidden)
+        ol.forward(x)
+        times = []
+        for _ in range(runs):
+            t0 = time.perf_counter()
+            ol.forward(x)
+            times.append(time.perf_counter() - t0)
+        res[t] = t / float(np.median(times))
+    return res[t_decode], res[t_prefill], cores
 
 
 def copy_calibration(mib: int) -> int:
@@ -209,7 +221,7 @@ def main() -> int:
     ap.add_argument("--batch-tokens", type=int, default=32,
                     help="a few-tokens batch also measured (BASELINE's HBM-bound T=32 row); 0 to skip")
     ap.add_argument("--copies", type=int, default=4, help="distinct weight copies cycled through")
-    ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    ap.add_argument("--cpu-runs", type=int, default=5, help="timed CPU forwards per T (median)")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--mode", type=int, default=0, help="kernel path (moe_layer_set_mode): 0 automatic")
     ap.add_argument("--summarize-pmc", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
@@ -289,11 +301,13 @@ def main() -> int:
     cpu = None
     if not args.no_cpu:
         log("timing the CPU restatement (oracle/) on the host cores")
-        dec, pre, cores, n = cpu_baseline(host, args.decode_tokens, args.tokens, args.cpu_seconds)
-        cpu = dict(value=round(pre, 2), unit="tokens/s", cores=cores, kind="port",
-                   sample=f"{n} forward(s) of the same layer at T={args.tokens} plus repeated T={args.decode_tokens}"
-                          f" decode for ~{args.cpu_seconds / 2:.0f}s each, same weights and inputs",
-                   decode_value=round(dec, 2))
+        dec, pre, cores = cpu_baseline(host, args.decode_tokens, args.tokens, args.cpu_runs)
+        cpu = dict(value=round(pre, 2), unit="tokens/s", cores=cores, kind="port", cpu_model=cpu_model(),
+                   median_of=args.cpu_runs,
+                   sample=f"the same layer, weights and inputs: per T one warm-up forward, then the median of "
+                          f"{args.cpu_runs} timed forwards, at T={args.tokens} (value) and T={args.decode_tokens} "
+                          f"(decode_value)",
+                   tokens=args.tokens, decode_tokens=args.decode_tokens, decode_value=round(dec, 2))
 
     line = {
         "metric": METRIC,
@@ -306,20 +320,29 @@ def main() -> int:
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "f16",
+        "dtype": "f32",
+        "arithmetic": "f32 precision on the matrix cores: weights d*q split exactly into two f16 pieces, "
+                      "activations into two f16 pieces (22 significant bits, per-row power-of-two scale), "
+                      "hi*hi + hi*lo + lo*hi accumulated in f32 by V_MFMA_F32_32X32X16_F16 (3 MFMAs per "
+                      "product; roofline flops count each product once)",
         "data": "synthetic",
         "config": {"workload": f"{shape.name}_moe_layer_T{args.tokens}", "hidden": shape.hidden,
                    "inter": shape.inter, "experts": shape.n_experts, "top_k": shape.top_k,
                    "weights": "Q4_0" if shape.expert_dt == 2 else str(shape.expert_dt), "tokens": args.tokens,
                    "weight_copies": args.copies},
-        "roofline": {"bound": "mfma", "kernel": "expert gate/up (MFMA grouped GEMM)",
+        "roofline": {"bound": "mfma", "kernel": "mfma_kernel<Q4_0, up> (expert gate/up, MFMA grouped GEMM)",
                      "achieved": round(achieved, 2), "peak": MFMA_F16_PEAK_TFLOPS, "unit": "TFLOP/s",
-                     "frac": round(achieved / MFMA_F16_PEAK_TFLOPS, 4), "traffic": traffic_of("mfma_kernel<2, true>"),
+                     "frac": round(achieved / MFMA_F16_PEAK_TFLOPS, 4), "traffic": traffic_of("mfma_kernel<2, true"),
+                     "mfma_pipe_frac": round(3 * achieved / MFMA_F16_PEAK_TFLOPS, 4),
                      "layer_frac": round(layer_tflops / MFMA_F16_PEAK_TFLOPS, 4)},
         "cpu_baseline": cpu,
         "decode": {"tokens": args.decode_tokens, "value": round(args.decode_tokens / (td["ms"] * 1e-3), 1),
                    "unit": "tokens/s", "ms_per_step": round(td["ms"], 5), "dtype": "f32",
-                   "roofline": {"bound": "hbm", "kernel": "expert gate/up (GEMV)", "achieved": round(dec_gbs, 1),
+                   "arithmetic": "f32 precision: quantised codes dotted exactly (v_dot4_i32_i8) with activations "
+                                 "held as three int8 levels (error 2^-24 of each 32-value block's range), f32 "
+                                 "scales and sums",
+                   "roofline": {"bound": "hbm", "kernel": "decode_up_kernel (one-token gate/up, integer-dot "
+                                                          "GEMV)", "achieved": round(dec_gbs, 1),
                                 "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(dec_gbs / HBM_PEAK_GBS, 4),
                                 "traffic": traffic_of("decode_up_kernel"), "layer_frac": round(layer_gbs / HBM_PEAK_GBS, 4)},
                    "stages_us": {k_: round(v * 1e3, 2) for k_, v in td["stages"].items()}},

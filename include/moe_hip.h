@@ -16,8 +16,14 @@
  *     moe_last_error().
  *   - Device pointers are HIP device addresses on the context's device.
  *     `stream` is a hipStream_t passed as void* (NULL = the null stream).
- *   - A forward call is asynchronous on `stream`; concurrent calls on one
- *     layer must use one stream (the layer's workspace is shared).
+ *   - A forward call is asynchronous on `stream` and never waits for the
+ *     device.  Calls are reentrant per stream, as the reference's
+ *     Model::feed_forward(&self, ..., st: &mut State, ...) is per sequence
+ *     (src/model.rs:836): moe_layer_forward keeps one workspace per stream it
+ *     is called on, and moe_layer_forward_ws runs on a workspace the caller
+ *     owns, so calls on different streams (or workspaces) share no scratch.
+ *     Host threads may call concurrently; moe_layer_set_routing and
+ *     moe_layer_set_mode apply to calls made after they return.
  */
 #ifndef MOE_HIP_H
 #define MOE_HIP_H
@@ -128,12 +134,28 @@ int moe_layer_create(moe_ctx *ctx, const moe_layer_desc *desc, moe_layer **out);
 void moe_layer_destroy(moe_layer *layer);
 
 /* Install router interventions (NULL clears them).  Replaces setting
- * Model::routing for one layer (src/model.rs:238-280). */
+ * Model::routing for one layer (src/model.rs:238-280).  The interventions
+ * travel by value in each call's kernel arguments: calls already queued keep
+ * the routing they were made with. */
 int moe_layer_set_routing(moe_layer *layer, const moe_routing *routing);
 
-/* Pre-size the per-call workspace for up to `max_t` tokens so that later
- * forward calls with t <= max_t allocate nothing. */
+/* Allocate the workspace moe_layer_forward uses on `stream` for up to
+ * `max_t` tokens (at the current top_k or the layer's own, whichever is
+ * larger).  After a reservation no forward call allocates on that stream,
+ * and a call with more tokens (or, after set_routing, more experts per token)
+ * than reserved fails with MOE_EINVAL.  Without one, moe_layer_forward
+ * allocates a stream's workspace on its first call there and grows it when
+ * t grows; an outgrown workspace is released by moe_layer_destroy (queued
+ * work may still use it), so growth never waits for the device.  No
+ * counterpart in the reference, which allocates scratch per call
+ * (src/model.rs:900-935). */
+int moe_layer_reserve_stream(moe_layer *layer, int32_t max_t, void *stream);
+/* moe_layer_reserve_stream on the null stream. */
 int moe_layer_reserve(moe_layer *layer, int32_t max_t);
+
+/* Bytes of a caller-owned workspace for moe_layer_forward_ws over up to
+ * `max_t` tokens at the layer's current top_k. */
+int moe_layer_workspace_size(const moe_layer *layer, int32_t max_t, uint64_t *bytes);
 
 /* Kernel path: 0 = automatic (one-token integer-dot kernels at t = 1,
  * few-tokens integer-dot kernels while the hit experts average at most 3
@@ -142,8 +164,12 @@ int moe_layer_reserve(moe_layer *layer, int32_t max_t);
  * none fits), 1 = exact kernels
  * (bit-identical to the CPU path, slow), 2 = GEMV, 3 = MFMA, 4 = one-token
  * kernels at t = 1 and GEMV otherwise, 5 = few-tokens integer-dot kernels
- * (up to 256 tokens).  No counterpart in the reference,
- * which has one CPU path. */
+ * (up to 256 tokens).  Every path computes in f32 precision: the GEMV and
+ * exact kernels in f32 arithmetic, the integer-dot kernels on activations
+ * held as three int8 levels (2^-24 of each 32-value block's range), the
+ * MFMA kernels on two-piece f16 operands (exact weights, 22-bit
+ * activations) accumulated in f32.  No counterpart in the reference, which
+ * has one CPU path. */
 int moe_layer_set_mode(moe_layer *layer, int mode);
 
 /* Experts each token is routed to (min(top_k, E)) under the current routing. */
@@ -171,6 +197,18 @@ int moe_layer_k(const moe_layer *layer);
 int moe_layer_forward(moe_layer *layer, const float *x, int32_t t, float *out, float *residual, moe_route *routes,
                       uint32_t *hits, const uint32_t *prev, uint64_t *stats, void *stream);
 
+/* moe_layer_forward on a caller-owned workspace: `workspace` is device
+ * memory of `workspace_bytes` (>= moe_layer_workspace_size for t tokens),
+ * 256-byte aligned, zero-filled before its first use (every call leaves the
+ * counters it keeps there at zero again).  Allocates nothing.  Calls on
+ * different workspaces may run concurrently on any streams; calls that
+ * share a workspace must be ordered (one stream).  Replaces the same
+ * feed_forward arm as moe_layer_forward (src/model.rs:836-971), whose
+ * State is per sequence. */
+int moe_layer_forward_ws(moe_layer *layer, const float *x, int32_t t, float *out, float *residual,
+                         moe_route *routes, uint32_t *hits, const uint32_t *prev, uint64_t *stats, void *workspace,
+                         uint64_t workspace_bytes, void *stream);
+
 /* Router logits and gating only: routes [t, k] for x [t, H], as
  * src/model.rs:844-898 computes them.  `logits` (device f32 [t, E]) may be
  * NULL; if given it receives the router logits after the temperature. */
@@ -179,10 +217,11 @@ int moe_layer_route(moe_layer *layer, const float *x, int32_t t, moe_route *rout
 /* Stage timing (no counterpart in the reference).  While enabled, forward
  * records HIP events around each of its stages on the call's stream:
  * 0 router, 1 gating, 2 dispatch, 3 expert gate/up, 4 expert down,
- * 5 combine.  moe_layer_stage_times synchronises on the last event and adds
- * each stage's accumulated milliseconds and launch count into ms[6], n[6],
- * then resets the accumulators. */
-#define MOE_STAGES 6
+ * 5 combine, 6 activation encoding (f16 pieces or int8 levels of x and h).
+ * moe_layer_stage_times synchronises on the recorded events and adds each
+ * stage's accumulated milliseconds and launch count into ms[7], n[7], then
+ * resets the accumulators. */
+#define MOE_STAGES 7
 int moe_layer_profile(moe_layer *layer, int enable);
 int moe_layer_stage_times(moe_layer *layer, double *ms, uint64_t *n);
 

@@ -70,6 +70,10 @@ PROTOTYPES = {
     "moe_layer_destroy": (None, [C.c_void_p]),
     "moe_layer_set_routing": (C.c_int, [C.c_void_p, C.POINTER(RoutingC)]),
     "moe_layer_reserve": (C.c_int, [C.c_void_p, C.c_int32]),
+    "moe_layer_reserve_stream": (C.c_int, [C.c_void_p, C.c_int32, C.c_void_p]),
+    "moe_layer_workspace_size": (C.c_int, [C.c_void_p, C.c_int32, C.POINTER(C.c_uint64)]),
+    "moe_layer_forward_ws": (C.c_int, [C.c_void_p, C.c_void_p, C.c_int32, C.c_void_p, C.c_void_p, C.c_void_p,
+                                       C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_uint64, C.c_void_p]),
     "moe_layer_set_mode": (C.c_int, [C.c_void_p, C.c_int]),
     "moe_layer_k": (C.c_int, [C.c_void_p]),
     "moe_layer_forward": (C.c_int, [C.c_void_p, C.c_void_p, C.c_int32, C.c_void_p, C.c_void_p, C.c_void_p,
@@ -98,7 +102,7 @@ PROTOTYPES = {
     "moe_layer_stage_times": (C.c_int, [C.c_void_p, C.POINTER(C.c_double), C.POINTER(C.c_uint64)]),
 }
 
-STAGES = ("router", "gating", "dispatch", "expert_up", "expert_down", "combine")
+STAGES = ("router", "gating", "dispatch", "expert_up", "expert_down", "combine", "encode")
 
 _lib = None
 

@@ -4,7 +4,7 @@
 // weight of the hit experts once and do little arithmetic per weight, so
 // they are HBM-bound if the arithmetic per weight byte stays small.  The
 // one-token kernels' scheme carries over: weights are dotted, still
-// quantised, with two-level int8 activations (qact.h) by v_dot4_i32_i8, and
+// quantised, with three-level int8 activations (qact.h) by v_dot4_i32_i8, and
 // a lane keeps the activation units of NT tokens in registers so that each
 // weight unit it loads serves all of them (the unpacking of a unit is shared
 // by the tokens; the dots are four values per operation per token).
@@ -51,10 +51,10 @@ __device__ inline MatDev mat_of(const MatDev *m) {
 // ------------------------------------------------------------- encoding
 
 // One wavefront per 64-value unit, one value per lane: lanes 0..31 form
-// block 0, 32..63 block 1.  The block's largest magnitude and the sum of
+// block 0, 32..63 block 1.  The block's largest magnitude and the sums of
 // its codes come from shuffles inside each half; every lane then writes its
-// own hi and lo bytes (the unit's bytes i and 64 + i), and lanes 0 and 32
-// their block's s2 and sq.  Same values as qact_block.
+// own three level bytes (the unit's bytes i, 64 + i and 128 + i), and lanes
+// 0 and 32 their block's s3, q01 and q2.  Same values as qact_block.
 __global__ __launch_bounds__(256) void qenc_kernel(const float *__restrict__ src, int rows, int cols,
                                                    uint8_t *__restrict__ dst) {
     const int units = cols / 64;
@@ -68,17 +68,19 @@ __global__ __launch_bounds__(256) void qenc_kernel(const float *__restrict__ src
         float amax = fmaxf(0.0f, fabsf(v));  // as the sequential fold from 0
 #pragma unroll
         for (int m = 16; m >= 1; m >>= 1) amax = fmaxf(amax, __shfl_xor(amax, m, 64));
-        int hi, lo;
-        qact_encode(v, qact_inv(amax), hi, lo);
-        int sq = 254 * hi + lo;
+        int a0, a1, a2;
+        qact_encode(v, qact_inv(amax), a0, a1, a2);
+        int q01 = 254 * a0 + a1, q2 = a2;
 #pragma unroll
-        for (int m = 16; m >= 1; m >>= 1) sq += __shfl_xor(sq, m, 64);
+        for (int m = 16; m >= 1; m >>= 1) q01 += __shfl_xor(q01, m, 64), q2 += __shfl_xor(q2, m, 64);
         uint8_t *unit = dst + (size_t)w * kQUnitBytes;
-        gstore(unit + lane, (uint8_t)(hi & 0xff));
-        gstore(unit + 64 + lane, (uint8_t)(lo & 0xff));
+        gstore(unit + lane, (uint8_t)(a0 & 0xff));
+        gstore(unit + 64 + lane, (uint8_t)(a1 & 0xff));
+        gstore(unit + 128 + lane, (uint8_t)(a2 & 0xff));
         if ((lane & 31) == 0) {
-            gstore(reinterpret_cast<float *>(unit + 128) + (lane >> 5), qact_s2(amax));
-            gstore(reinterpret_cast<int32_t *>(unit + 136) + (lane >> 5), sq);
+            gstore(reinterpret_cast<float *>(unit + 4 * kQS) + (lane >> 5), qact_s3(amax));
+            gstore(reinterpret_cast<int32_t *>(unit + 4 * kQ01) + (lane >> 5), q01);
+            gstore(reinterpret_cast<int32_t *>(unit + 4 * kQ2) + (lane >> 5), q2);
         }
     }
 }

@@ -3,11 +3,12 @@
 // Decoding one token reads every weight of the k selected experts once and
 // does two multiply-adds per weight, so the kernels are HBM-bound only if the
 // arithmetic per weight byte stays small.  They dot the quantised weights
-// directly against two-level int8 activations (qact.h) with v_dot4_i32_i8:
-// a Q4_0 block of 32 values costs 3 unpack operations and 4 integer dots per
-// 8 values plus 5 float operations per block, about 2.4 times fewer
+// directly against three-level int8 activations (qact.h) with
+// v_dot4_i32_i8: a Q4_0 block of 32 values costs 3 unpack operations and 6
+// integer dots per 8 values plus 7 float operations per block, fewer
 // operations than dequantising to fp32.  The integer sums are exact; the
-// activation error is at most 2^-16 of each 32-value block's range.
+// activation error is at most 2^-24 of each 32-value block's range, so the
+// products carry f32 precision.
 //
 //  * decode_up_kernel: h = silu(gate . x) * (up . x) for every row of the
 //    selected experts (and the shared expert): src/model.rs:31-33 and the

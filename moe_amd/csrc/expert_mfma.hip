@@ -1,40 +1,53 @@
-// expert_mfma.hip — grouped SwiGLU expert GEMMs on gfx950 matrix cores.
+// expert_mfma.hip — grouped SwiGLU expert GEMMs on gfx950 matrix cores, in
+// f32 precision.
 //
-// One block computes a tile of up to 160 tokens x 256 weight rows of one
-// expert:
+// One block computes a tile of up to BM tokens (160, or 128 when a Q8_0
+// matrix needs the LDS) x 256 weight rows of one expert:
 //   up   : 128 gate rows and the same 128 up rows of the expert, K = H; the
-//          epilogue forms h = silu(G) * U and stores it as f16.
+//          epilogue forms h = silu(G) * U in f32 (src/model.rs:31-33).
 //   down : 256 rows of W_down, K = I (optionally split into 2 or 4 K parts,
 //          each written to its own part of y); output y in f32.
 // Four waves, one per SIMD.  Wave w owns every token row of the tile and 64
 // weight rows, so each weight value is dequantised exactly once per tile, in
-// the registers of the wave that multiplies it (f16, d * q rounded once), and
-// the 160 x 64 f32 accumulators live in the wave's AGPRs
-// (V_MFMA_F32_32X32X16_F16).  An expert's tokens normally fit one tile, so a
-// weight row is dequantised once per expert.  160 tokens (not more) leaves
-// LDS room for a deep ring: a step multiplies in ~0.4 us while a weight load
-// from HBM takes ~2 us under load, so loads run several steps ahead.
+// the registers of the wave that multiplies it, and the BM x 64 f32
+// accumulators live in the wave's AGPRs (V_MFMA_F32_32X32X16_F16).
+//
+// Precision.  The reference multiplies f32 activations by exactly
+// dequantised f32 weights d q (src/quant.rs:482-506).  Here both operands
+// are carried as two f16 pieces and three MFMAs accumulate
+// hi.hi + hi.lo + lo.hi in f32:
+//   weights      d q has at most 18 significant bits (11 of d, 7 of q), so
+//                hi = f16(d q) and lo = d q - hi (one fma, exact) hold it
+//                exactly; d is first multiplied by 2^wexp (exact), the
+//                matrix's power of two that puts its largest |d q| in
+//                [2^14, 2^15), so lo stays in f16's normal range;
+//   activations  split_rows_kernel writes hi + lo of v 2^ex, ex per row
+//                putting the row's largest |v| in [2^14, 2^15): 22
+//                significant bits (the dropped lo.lo term and the rounding
+//                of lo are ~2^-22 of a product);
+// the epilogue multiplies by 2^-(ex + wexp), which is exact.
 //
 // Operands reach LDS by DMA (global_load_lds), never through VGPRs:
-//   activations  16-byte chunks of each token row; the chunk index is XORed
-//                with the row's low three bits, so the 16-byte fragment reads
-//                of eight consecutive rows hit eight different bank groups;
+//   activations  16-byte chunks of each token row, for hi and lo alike; the
+//                chunk index is XORed with the row's low three bits, so the
+//                16-byte fragment reads of eight consecutive rows hit eight
+//                different bank groups;
 //   weights      the raw bytes of two quantised blocks per row per K step, in
 //                per-wave regions (32 rows each) that only the owning wave
 //                reads.
-// An NS-stage ring (5 stages for Q4_0, 4 for Q5_0/Q8_0: as many as LDS
-// holds) keeps the loads of NS - 1 K steps in flight behind the step being
-// multiplied.  The DMAs are issued from inline assembly, because the
-// compiler makes every LDS read that follows an LDS DMA wait for all
-// outstanding loads; the kernel instead waits with exact vmcnt counts: in the
-// middle of step s a wave waits for its own loads of step s + 1 and
-// dequantises that step's first block ahead of time, and one barrier per step
+// A three-stage ring holds K steps s, s + 1 and s + 2; the loads of step
+// s + 3 go out during step s, as soon as every wave is past its last read of
+// step s's stage, so each load has about two steps (~2.5 us) to arrive.  The
+// DMAs are issued from inline assembly, because the compiler makes every
+// LDS read that follows an LDS DMA wait for all outstanding loads; the
+// kernel instead waits with exact vmcnt counts, and one barrier per step
 // publishes the other waves' activation chunks.
 #include <hip/hip_fp16.h>
 #include <hip/hip_runtime.h>
 
 #include <type_traits>
 
+#include "exact_math.h"
 #include "gmem.h"
 #include "moe_internal.h"
 
@@ -44,11 +57,13 @@ namespace {
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 typedef float floatx16 __attribute__((ext_vector_type(16)));
 
-constexpr int BM = 160;              // tokens per tile
-constexpr int MTMAX = BM / 32;       // 32-token MFMA tiles per block tile
-constexpr int BW = 256;              // weight rows per tile (up: 128 gate + 128 up rows)
-constexpr int BK = 64;               // K values per step (two 32-value blocks)
-constexpr int A_STAGE = BM * BK * 2;  // bytes of activations per stage
+constexpr int BW = 256;  // weight rows per tile (up: 128 gate + 128 up rows)
+constexpr int BK = 64;   // K values per step (two 32-value blocks)
+// Bytes of one activation piece (hi or lo) of one ring stage.
+template <int BM>
+constexpr int a_stage() {
+    return BM * BK * 2;
+}
 
 __device__ inline uint32_t alignb(uint32_t hi, uint32_t lo, uint32_t s) { return __builtin_amdgcn_alignbyte(hi, lo, s); }
 __device__ inline uint32_t perm(uint32_t hi, uint32_t lo, uint32_t sel) { return __builtin_amdgcn_perm(hi, lo, sel); }
@@ -64,12 +79,19 @@ __device__ inline uint32_t h2_bits(__half2 h) {
 }
 __device__ inline uint32_t spread4(uint32_t h) { return ((h * 0x00204081u) & 0x01010101u) << 4; }
 
-// Codes b0..b3 (bytes of v, each < 256), minus `off2`, times `d2`, as f16
-// pairs (b0, b1) and (b2, b3).  0x64 in the high byte makes each f16 exactly
-// 1024 + b, so the subtraction is exact and the product rounds once.
-__device__ inline void codes4(uint32_t v, __half2 off2, __half2 d2, uint32_t &w01, uint32_t &w23) {
-    w01 = h2_bits(__hmul2(__hsub2(as_h2(perm(0x64646464u, v, 0x04010400u)), off2), d2));
-    w23 = h2_bits(__hmul2(__hsub2(as_h2(perm(0x64646464u, v, 0x04030402u)), off2), d2));
+// Codes b0..b3 (bytes of v, each < 256) minus `off2`, times `d2`: the
+// products as exact f16 pieces, hi (pairs (b0, b1), (b2, b3)) and lo.  0x64
+// in the high byte makes each f16 exactly 1024 + b, so q = b - off is exact;
+// hi = f16(q d) and lo = fma(q, d, -hi), which is exact because q d - hi fits
+// in f16's 11 bits.
+__device__ inline void codes4(uint32_t v, __half2 off2, __half2 d2, uint32_t &h01, uint32_t &h23, uint32_t &l01,
+                              uint32_t &l23) {
+    const __half2 q01 = __hsub2(as_h2(perm(0x64646464u, v, 0x04010400u)), off2);
+    const __half2 q23 = __hsub2(as_h2(perm(0x64646464u, v, 0x04030402u)), off2);
+    const __half2 p01 = __hmul2(q01, d2), p23 = __hmul2(q23, d2);
+    h01 = h2_bits(p01), h23 = h2_bits(p23);
+    l01 = h2_bits(__hfma2(q01, d2, __hneg2(p01)));
+    l23 = h2_bits(__hfma2(q23, d2, __hneg2(p23)));
 }
 __device__ inline half8 pack8(const uint32_t (&o)[4]) {
     half8 r;
@@ -118,21 +140,21 @@ struct BLay {
                            : (uint32_t)(xbytes + 128 * (d - 4 * nx4) + 4 * r);
     }
 };
-// Ring stages per format: as many as fit in the 160 KiB of LDS.
-template <int DT>
+// Ring stages per format and token tile: as many as fit in the 160 KiB of
+// LDS beside three per-row arrays.
+template <int DT, int BM>
 constexpr int ring_stages() {
-    return (160 * 1024 - 2 * BM * 4) / (A_STAGE + BLay<DT>::stage);
+    return (160 * 1024 - 3 * BM * 4) / (2 * a_stage<BM>() + BLay<DT>::stage);
 }
-template <int DT>
+template <int DT, int BM>
 constexpr int lds_bytes() {
-    return ring_stages<DT>() * (A_STAGE + BLay<DT>::stage) + 2 * BM * 4;
+    return ring_stages<DT, BM>() * (2 * a_stage<BM>() + BLay<DT>::stage) + 3 * BM * 4;
 }
-static_assert(ring_stages<MOE_DT_Q4_0>() == 5 && ring_stages<MOE_DT_Q5_0>() == 4 &&
-                  ring_stages<MOE_DT_Q8_0>() == 4,
-              "ring depth per format");
-static_assert(lds_bytes<MOE_DT_Q4_0>() <= 160 * 1024 && lds_bytes<MOE_DT_Q5_0>() <= 160 * 1024 &&
-                  lds_bytes<MOE_DT_Q8_0>() <= 160 * 1024,
-              "LDS budget");
+static_assert(ring_stages<MOE_DT_Q4_0, 160>() == 3 && ring_stages<MOE_DT_Q5_0, 160>() == 3 &&
+                  ring_stages<MOE_DT_Q8_0, 128>() == 3 && ring_stages<MOE_DT_Q4_0, 128>() == 3 &&
+                  ring_stages<MOE_DT_Q5_0, 128>() == 3,
+              "three-stage ring for every instantiated format and tile");
+static_assert(ring_stages<MOE_DT_Q8_0, 160>() < 3, "Q8_0 takes 128-token tiles");
 
 // ---- LDS DMA and exact waits ------------------------------------------------
 // global_load_lds writes lane l's 16 (or 4) bytes to LDS address m0 + 16 l
@@ -223,33 +245,36 @@ struct Slots<MOE_DT_Q8_0> {  // kb 0: scale 0..1, codes 2..33; kb 1: scale 34..3
     static constexpr int hm[2][7] = {{0, 1, 1, 1, 1, 1, 1}, {0, 1, 1, 1, 1}};
 };
 
+// Block kb's two MFMA operands (m = 0, 1) as hi and lo pieces; `wexp`
+// scales the block's d by 2^wexp first (exact: a power of two).
 template <int DT, int KB>
-__device__ inline void dequant(const uint32_t *v, half8 (&b)[2], int h) {
+__device__ inline void dequant(const uint32_t *v, half8 (&bh)[2], half8 (&bl)[2], int h, int wexp) {
     const uint32_t s = KB == 0 ? (v[0] & 0xffffu) : (v[0] >> 16);
-    const __half2 d2 = as_h2(s * 0x10001u);
-    uint32_t o[4];
+    const __half ds = __float2half_rn(ldexpf(__half2float(__ushort_as_half((unsigned short)s)), wexp));
+    const __half2 d2 = __halves2half2(ds, ds);
+    uint32_t oh[4], ol[4];
     if constexpr (DT == MOE_DT_Q4_0) {
         const __half2 off2 = __floats2half2_rn(1032.0f, 1032.0f);
         const uint32_t w0 = KB == 0 ? alignb(v[2], v[1], 2) : v[1];
         const uint32_t w1 = KB == 0 ? alignb(v[3], v[2], 2) : v[2];
-        codes4(w0 & 0x0f0f0f0fu, off2, d2, o[0], o[1]);
-        codes4(w1 & 0x0f0f0f0fu, off2, d2, o[2], o[3]);
-        b[0] = pack8(o);
-        codes4((w0 >> 4) & 0x0f0f0f0fu, off2, d2, o[0], o[1]);
-        codes4((w1 >> 4) & 0x0f0f0f0fu, off2, d2, o[2], o[3]);
-        b[1] = pack8(o);
+        codes4(w0 & 0x0f0f0f0fu, off2, d2, oh[0], oh[1], ol[0], ol[1]);
+        codes4(w1 & 0x0f0f0f0fu, off2, d2, oh[2], oh[3], ol[2], ol[3]);
+        bh[0] = pack8(oh), bl[0] = pack8(ol);
+        codes4((w0 >> 4) & 0x0f0f0f0fu, off2, d2, oh[0], oh[1], ol[0], ol[1]);
+        codes4((w1 >> 4) & 0x0f0f0f0fu, off2, d2, oh[2], oh[3], ol[2], ol[3]);
+        bh[1] = pack8(oh), bl[1] = pack8(ol);
     } else if constexpr (DT == MOE_DT_Q5_0) {
         const __half2 off2 = __floats2half2_rn(1040.0f, 1040.0f);
         const uint32_t qh = KB == 0 ? alignb(v[1], v[0], 2) : v[1];
         const uint32_t w0 = KB == 0 ? alignb(v[3], v[2], 2) : v[2];
         const uint32_t w1 = KB == 0 ? alignb(v[4], v[3], 2) : v[3];
         const uint32_t hb = qh >> (8 * h);  // bit i: element 8 h + i; bit 16 + i: element 16 + 8 h + i
-        codes4((w0 & 0x0f0f0f0fu) | spread4(hb & 0xfu), off2, d2, o[0], o[1]);
-        codes4((w1 & 0x0f0f0f0fu) | spread4((hb >> 4) & 0xfu), off2, d2, o[2], o[3]);
-        b[0] = pack8(o);
-        codes4(((w0 >> 4) & 0x0f0f0f0fu) | spread4((hb >> 16) & 0xfu), off2, d2, o[0], o[1]);
-        codes4(((w1 >> 4) & 0x0f0f0f0fu) | spread4((hb >> 20) & 0xfu), off2, d2, o[2], o[3]);
-        b[1] = pack8(o);
+        codes4((w0 & 0x0f0f0f0fu) | spread4(hb & 0xfu), off2, d2, oh[0], oh[1], ol[0], ol[1]);
+        codes4((w1 & 0x0f0f0f0fu) | spread4((hb >> 4) & 0xfu), off2, d2, oh[2], oh[3], ol[2], ol[3]);
+        bh[0] = pack8(oh), bl[0] = pack8(ol);
+        codes4(((w0 >> 4) & 0x0f0f0f0fu) | spread4((hb >> 16) & 0xfu), off2, d2, oh[0], oh[1], ol[0], ol[1]);
+        codes4(((w1 >> 4) & 0x0f0f0f0fu) | spread4((hb >> 20) & 0xfu), off2, d2, oh[2], oh[3], ol[2], ol[3]);
+        bh[1] = pack8(oh), bl[1] = pack8(ol);
     } else {  // Q8_0: int8 codes, read as uint8 + 128
         const __half2 off2 = __floats2half2_rn(1152.0f, 1152.0f);
 #pragma unroll
@@ -257,9 +282,9 @@ __device__ inline void dequant(const uint32_t *v, half8 (&b)[2], int h) {
             const uint32_t *c = v + 1 + (KB == 0 ? 3 : 2) * m;
             const uint32_t w0 = KB == 0 ? alignb(c[1], c[0], 2) : c[0];
             const uint32_t w1 = KB == 0 ? alignb(c[2], c[1], 2) : c[1];
-            codes4(w0 ^ 0x80808080u, off2, d2, o[0], o[1]);
-            codes4(w1 ^ 0x80808080u, off2, d2, o[2], o[3]);
-            b[m] = pack8(o);
+            codes4(w0 ^ 0x80808080u, off2, d2, oh[0], oh[1], ol[0], ol[1]);
+            codes4(w1 ^ 0x80808080u, off2, d2, oh[2], oh[3], ol[2], ol[3]);
+            bh[m] = pack8(oh), bl[m] = pack8(ol);
         }
     }
 }
@@ -274,6 +299,7 @@ struct TileInfo {
     int g, m0, n, row0, ntile, ksplit;
     bool shared;
 };
+template <int BM>
 __device__ inline bool tile_of(const MfmaArgs &a, int mode, int gx, TileInfo &ti) {
     const int gy = gridDim.y, gz = gridDim.z;
     const int total = gx * gy;
@@ -309,16 +335,21 @@ __device__ inline bool tile_of(const MfmaArgs &a, int mode, int gx, TileInfo &ti
     return true;
 }
 
-template <int DT, bool UP>
+template <int DT, bool UP, int BM>
 __global__ __launch_bounds__(256, 1) __attribute__((amdgpu_waves_per_eu(1, 1))) void mfma_kernel(MfmaArgs a, int mode, int gx, int ksplit) {
     using BL = BLay<DT>;
-    constexpr int NS = ring_stages<DT>();
+    constexpr int NS = ring_stages<DT, BM>();
+    constexpr int MTMAX = BM / 32;        // 32-token MFMA tiles per block tile
+    constexpr int AS = a_stage<BM>();     // bytes of one activation piece per stage
+    constexpr int RS = 2 * AS + BL::stage;  // bytes of one ring stage
+    static_assert(NS == 3, "the step loop below assumes three stages");
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
-    int *src_row = reinterpret_cast<int *>(smem + NS * (A_STAGE + BL::stage));
+    int *src_row = reinterpret_cast<int *>(smem + NS * RS);
     int *dst_row = src_row + BM;
+    int *ex_row = dst_row + BM;
 
     TileInfo ti;
-    if (!tile_of(a, mode, gx, ti)) return;
+    if (!tile_of<BM>(a, mode, gx, ti)) return;
     const ExpertDev &ex = a.experts[ti.g];
     const MatDev &W0 = UP ? ex.m[0] : ex.m[2];
     const MatDev &W1 = UP ? ex.m[1] : ex.m[2];
@@ -333,20 +364,27 @@ __global__ __launch_bounds__(256, 1) __attribute__((amdgpu_waves_per_eu(1, 1))) 
     const int Icol = ti.shared ? a.I_s : a.I;
     const int valid = min(BM, ti.n - ti.m0);
     const int mt = (valid + 31) / 32;
+    const int wexp0 = W0.wexp, wexp1 = W1.wexp;
 
+    // Activation pieces and their row exponents.
+    const uint16_t *ahi = UP ? a.xhi : (ti.shared ? a.hshi : a.hhi);
+    const uint16_t *alo = UP ? a.xlo : (ti.shared ? a.hslo : a.hlo);
+    const int32_t *aex = UP ? a.xex : (ti.shared ? a.hsex : a.hex);
     if (tid < BM) {
-        int s = -1, d = -1;
+        int s = -1, d = -1, e = 0;
         if (tid < valid) {
             d = ti.row0 + ti.m0 + tid;
             s = UP ? (ti.shared ? ti.m0 + tid : a.perm_tok[d]) : d;
+            e = aex[s];
         }
         src_row[tid] = s;
         dst_row[tid] = d;
+        ex_row[tid] = e;
     }
     __syncthreads();
 
     const uint32_t lds0 = lds_addr(smem);
-    const uint32_t ldsB = lds0 + NS * A_STAGE;
+    const uint32_t ldsB = lds0 + NS * 2 * AS;
     const lds_p sm = (lds_p)smem;
     const int l32 = lane & 31, hf = lane >> 5;
 
@@ -354,8 +392,7 @@ __global__ __launch_bounds__(256, 1) __attribute__((amdgpu_waves_per_eu(1, 1))) 
     // i = wv + 4 u; lane l takes row r = 8 i + l / 8 and stores slot l % 8 of
     // that row's 128 bytes, which holds logical chunk (l % 8) ^ ((r / 2) % 8).
     // Rows past the tile's tokens repeat token row 0 (their outputs are never
-    // stored).
-    const uint8_t *abase = reinterpret_cast<const uint8_t *>(UP ? a.xh : (ti.shared ? a.hs : a.h));
+    // stored).  The lo piece uses the same offsets in its own array.
     const uint32_t arow_bytes = (uint32_t)(UP ? a.H : Icol) * 2;
     // Weight DMA: region j of wave wv holds 32 weight rows.  woff: per DMA
     // (the region's dwordx4 DMAs, then its dword DMAs) the lane's byte offset
@@ -382,6 +419,9 @@ __global__ __launch_bounds__(256, 1) __attribute__((amdgpu_waves_per_eu(1, 1))) 
             woff[j][i] = off;
         }
     }
+    // The dequantisation's scale exponent of region j (gate, up: the two
+    // matrices of the up projection; down: one matrix).
+    const int wx[2] = {wexp0, UP ? wexp1 : wexp0};
 
     // Per-lane LDS offsets of the compute side.
     uint32_t aoff[4];  // group g = 2 kb + m: row l32, logical chunk 2 g + hf
@@ -399,8 +439,9 @@ __global__ __launch_bounds__(256, 1) __attribute__((amdgpu_waves_per_eu(1, 1))) 
 
     auto run = [&](auto mt_c) {
         constexpr int MT = decltype(mt_c)::value;
+        constexpr int NA = 2 * MT;        // activation DMAs per wave per step (hi, then lo)
         constexpr int NB = 2 * BL::inst;  // weight DMAs per wave per step
-        constexpr int ND = MT + NB;       // DMAs per wave per step
+        constexpr int ND = NA + NB;       // DMAs per wave per step
         uint32_t aoffg[MT];               // activation source offsets (step 0)
 #pragma unroll
         for (int u = 0; u < MT; u++) {
@@ -409,17 +450,20 @@ __global__ __launch_bounds__(256, 1) __attribute__((amdgpu_waves_per_eu(1, 1))) 
             aoffg[u] = (uint32_t)sr * arow_bytes + (uint32_t)kbeg * 2u +
                        (uint32_t)(((lane & 7) ^ ((r >> 1) & 7)) << 4);
         }
-        // DMA d of step `step` into ring stage `st`: d < MT activations, then
-        // the weight regions.  Steps past the end reload the last step into a
-        // stage nobody reads any more, so every step issues the same DMAs.
+        // DMA d of step `step` into ring stage `st`: d < NA activations
+        // (hi pieces, then lo), then the weight regions.  Steps past the end
+        // reload the last step into a stage nobody reads any more, so every
+        // step issues the same DMAs.
         auto dma = [&](auto d_c, int step, int st) {
             constexpr int d = decltype(d_c)::value;
             const int sc = step < nsteps ? step : nsteps - 1;
-            if constexpr (d < MT) {
-                dma16(abase + (size_t)sc * (BK * 2), aoffg[d],
-                      lds0 + (uint32_t)st * A_STAGE + (uint32_t)(wv + 4 * d) * 1024u);
+            if constexpr (d < NA) {
+                constexpr int p = d / MT, u = d % MT;
+                const uint16_t *src = p == 0 ? ahi : alo;
+                dma16(reinterpret_cast<const uint8_t *>(src) + (size_t)sc * (BK * 2), aoffg[u],
+                      lds0 + (uint32_t)st * 2 * AS + (uint32_t)p * AS + (uint32_t)(wv + 4 * u) * 1024u);
             } else {
-                constexpr int j = (d - MT) / BL::inst, i = (d - MT) % BL::inst;
+                constexpr int j = (d - NA) / BL::inst, i = (d - NA) % BL::inst;
                 const uint8_t *wb = wbase[j] + (size_t)(kbeg / 32 + 2 * sc) * Fmt<DT>::bytes;
                 const uint32_t lr = ldsB + (uint32_t)st * BL::stage + (uint32_t)(2 * wv + j) * BL::region;
                 if constexpr (i < BL::ix)
@@ -441,8 +485,8 @@ __global__ __launch_bounds__(256, 1) __attribute__((amdgpu_waves_per_eu(1, 1))) 
         // LDS reads (both lane halves read the same row, which the LDS
         // broadcasts); each lane then picks its dwords (Slots: base, or
         // base + 2 for the upper lane half).
-        half8 bq[2][2][2];  // [kb][j][m]
-        half8 af[4][MT];    // one per group, read two groups ahead
+        half8 bh[2][2][2], bl[2][2][2];  // [kb][j][m] hi and lo pieces
+        half8 ah[2][MT], al[2][MT];      // activation pieces of two groups
         uint32_t rowv[2][BL::rd];
         auto read_rows = [&](lds_p stage_b) {
 #pragma unroll
@@ -459,7 +503,7 @@ __global__ __launch_bounds__(256, 1) __attribute__((amdgpu_waves_per_eu(1, 1))) 
                     rowv[j][4 * BL::nx4 + e] = lds_u32(stage_b + reg + brow_d + 128 * e);
             }
         };
-        auto dequant_raw = [&](auto kb_c, half8 (&B)[2][2]) {
+        auto dequant_raw = [&](auto kb_c) {
             constexpr int kb = decltype(kb_c)::value;
 #pragma unroll
             for (int j = 0; j < 2; j++) {
@@ -469,107 +513,113 @@ __global__ __launch_bounds__(256, 1) __attribute__((amdgpu_waves_per_eu(1, 1))) 
                     const int b = SL::base[kb][k];
                     v[k] = SL::hm[kb][k] ? (hf ? rowv[j][b + 2] : rowv[j][b]) : rowv[j][b];
                 }
-                dequant<DT, kb>(v, B[j], hf);
+                dequant<DT, kb>(v, bh[kb][j], bl[kb][j], hf, wx[j]);
             }
         };
-        auto read_a = [&](lds_p sa, int g, half8 (&A)[MT]) {
+        auto read_a = [&](lds_p sa, int g, int slot) {
             const lds_p p = sa + aoff[g];
 #pragma unroll
-            for (int t = 0; t < MT; t++) A[t] = lds_h8(p + 4096 * t);
+            for (int t = 0; t < MT; t++) ah[slot][t] = lds_h8(p + 4096 * t), al[slot][t] = lds_h8(p + AS + 4096 * t);
         };
-        auto mfma = [&](const half8 (&A)[MT], const half8 (&B)[2][2], int m, int i) {
+        // MFMA pass q of tile i = 2 t + j for group (kb, m): q 0 = hi.lo,
+        // 1 = lo.hi, 2 = hi.hi.  A group runs pass 0 over all its tiles, then
+        // pass 1, then pass 2, so consecutive MFMAs never share an
+        // accumulator.
+        auto mfma = [&](int slot, int kb, int m, int q, int i) {
             const int t = i >> 1, j = i & 1;
-            acc[t][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(A[t], B[j][m], acc[t][j], 0, 0, 0);
+            const half8 &A = q == 1 ? al[slot][t] : ah[slot][t];
+            const half8 &B = q == 0 ? bl[kb][j][m] : bh[kb][j][m];
+            acc[t][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(A, B, acc[t][j], 0, 0, 0);
         };
-        // One group's 2 MT MFMAs with DMAs [LO, HI) of step `step` spread
+        // One group's 6 MT MFMAs with DMAs [LO, HI) of step `step` spread
         // between them: a DMA that the memory pipeline cannot take yet stalls
         // this wave, not the MFMAs already queued.
-        auto mfmas_dma = [&](const half8 (&A)[MT], const half8 (&B)[2][2], int m, auto lo_c, auto hi_c, int step,
-                             int st) {
+        auto mfmas_dma = [&](int slot, int kb, int m, auto lo_c, auto hi_c, int step, int st) {
             constexpr int LO = decltype(lo_c)::value, HI = decltype(hi_c)::value;
+            constexpr int N = 6 * MT;
             auto body = [&](auto i_c, auto self) {
                 constexpr int i = decltype(i_c)::value;
-                if constexpr (i < 2 * MT) {
-                    mfma(A, B, m, i);
-                    dma_range(std::integral_constant<int, LO + i * (HI - LO) / (2 * MT)>{},
-                              std::integral_constant<int, LO + (i + 1) * (HI - LO) / (2 * MT)>{}, step, st);
+                if constexpr (i < N) {
+                    mfma(slot, kb, m, i / (2 * MT), i % (2 * MT));
+                    dma_range(std::integral_constant<int, LO + i * (HI - LO) / N>{},
+                              std::integral_constant<int, LO + (i + 1) * (HI - LO) / N>{}, step, st);
                     self(std::integral_constant<int, i + 1>{}, self);
                 }
             };
             body(std::integral_constant<int, 0>{}, body);
         };
-        auto mfmas = [&](const half8 (&A)[MT], const half8 (&B)[2][2], int m) {
+        auto mfmas = [&](int slot, int kb, int m) {
 #pragma unroll
-            for (int i = 0; i < 2 * MT; i++) mfma(A, B, m, i);
+            for (int q = 0; q < 3; q++)
+#pragma unroll
+                for (int i = 0; i < 2 * MT; i++) mfma(slot, kb, m, q, i);
         };
         using I0 = std::integral_constant<int, 0>;
         using I1 = std::integral_constant<int, 1>;
-        constexpr int MA = MT / 2;  // activation DMAs in group 0; the rest in group 1
 
-        const lds_p smB = sm + NS * A_STAGE;
-        // Prologue: steps 0 .. NS - 2 into stages 0 .. NS - 2, then wait for
+        const lds_p smB = sm + NS * 2 * AS;
+        // Prologue: steps 0 .. NS - 1 into stages 0 .. NS - 1, then wait for
         // step 0.
-        for (int p = 0; p < NS - 1; p++) dma_range(I0{}, std::integral_constant<int, ND>{}, p, p);
-        wait_vm_barrier<(NS - 2) * ND>();
-        read_a(sm, 0, af[0]);
-        read_a(sm, 1, af[1]);
+        for (int p = 0; p < NS; p++) dma_range(I0{}, std::integral_constant<int, ND>{}, p, p);
+        wait_vm_barrier<(NS - 1) * ND>();
+        read_a(sm, 0, 0);
         read_rows(smB);
-        dequant_raw(I0{}, bq[0]);
+        dequant_raw(I0{});
         int st = 0;
-        // Per step, this wave's loads of step s + NS - 1 go out in order: the
-        // activation DMAs in groups 0 and 1, the weight DMAs in group 3, into
-        // the stage step s - 1 used.  At the wait in group 2 this wave's
-        // outstanding loads are those of steps s + 1 .. s + NS - 2 (ND each)
-        // and the MT activation DMAs of step s + NS - 1; leaving all but step
-        // s + 1's outstanding completes step s + 1.
-        constexpr int WAIT = (NS - 3) * ND + MT;
-        static_assert((NS - 1) * ND < 64 && WAIT >= 0, "vmcnt range");
+        // At the wait in group 2 of step s this wave's outstanding loads are
+        // those of steps s + 1 .. s + NS - 1 (ND each, in order); leaving the
+        // newest (NS - 2) ND outstanding completes step s + 1.  After the
+        // barrier that follows, no wave reads stage s again (its last reads,
+        // group 3's activations, come before the barrier), so group 3 sends
+        // step s + NS's loads into it.
+        constexpr int WAIT = (NS - 2) * ND;
+        static_assert(NS * ND < 64, "vmcnt range");
         for (int s = 0; s < nsteps; s++) {
-            const lds_p sa = sm + st * A_STAGE;
-            const int st1 = st + 1 == NS ? 0 : st + 1, stn = st == 0 ? NS - 1 : st - 1;
-            const int sn = s + NS - 1;
-            // g = 0 (kb 0, m 0): group 2's activations first.
-            read_a(sa, 2, af[2]);
+            const lds_p sa = sm + st * 2 * AS;
+            const int st1 = st + 1 == NS ? 0 : st + 1;
+            // g = 0 (kb 0, m 0); read group 1.
+            read_a(sa, 1, 1);
             __builtin_amdgcn_sched_barrier(0);
-            mfmas_dma(af[0], bq[0], 0, I0{}, std::integral_constant<int, MA>{}, sn, stn);
-            // g = 1 (kb 0, m 1): dequantise block 1, read group 3.
-            dequant_raw(I1{}, bq[1]);
-            read_a(sa, 3, af[3]);
-            mfmas_dma(af[1], bq[0], 1, std::integral_constant<int, MA>{}, std::integral_constant<int, MT>{}, sn, stn);
+            mfmas(0, 0, 0);
+            // g = 1 (kb 0, m 1): dequantise block 1, read group 2.
+            dequant_raw(I1{});
+            read_a(sa, 2, 0);
+            mfmas(1, 0, 1);
             __builtin_amdgcn_sched_barrier(0);
-            // g = 2 (kb 1, m 0); then wait for this wave's loads of step
-            // s + 1 and meet the other waves, after which step s + 1's stage
-            // is complete and nobody reads stage s any more.
-            mfmas(af[2], bq[1], 0);
+            // g = 2 (kb 1, m 0): read group 3; then wait for this wave's
+            // loads of step s + 1 and meet the other waves.
+            read_a(sa, 3, 1);
+            mfmas(0, 1, 0);
             __builtin_amdgcn_sched_barrier(0);
             wait_vm_barrier<WAIT>();
             __builtin_amdgcn_sched_barrier(0);
-            // g = 3 (kb 1, m 1): step s + 1's groups 0 and 1 and weight
-            // rows; step s + NS - 1's weight DMAs.
-            const lds_p sa1 = sm + st1 * A_STAGE;
-            read_a(sa1, 0, af[0]);
-            read_a(sa1, 1, af[1]);
+            // g = 3 (kb 1, m 1): step s + 1's group 0 and weight rows; step
+            // s + NS's DMAs into this step's stage.
+            read_a(sm + st1 * 2 * AS, 0, 0);
             read_rows(smB + st1 * BL::stage);
             __builtin_amdgcn_sched_barrier(0);
-            mfmas_dma(af[3], bq[1], 1, std::integral_constant<int, MT>{}, std::integral_constant<int, ND>{}, sn, stn);
-            dequant_raw(I0{}, bq[0]);
+            mfmas_dma(1, 1, 1, I0{}, std::integral_constant<int, ND>{}, s + NS, st);
+            dequant_raw(I0{});
             __builtin_amdgcn_sched_barrier(0);
             st = st1;
         }
     };
-    static_assert(MTMAX == 5, "one case per 32-token tile count");
+    static_assert(MTMAX == 5 || MTMAX == 4, "one case per 32-token tile count");
     switch (mt) {
     case 1: run(std::integral_constant<int, 1>{}); break;
     case 2: run(std::integral_constant<int, 2>{}); break;
     case 3: run(std::integral_constant<int, 3>{}); break;
     case 4: run(std::integral_constant<int, 4>{}); break;
-    default: run(std::integral_constant<int, 5>{}); break;
+    default:
+        if constexpr (MTMAX == 5) run(std::integral_constant<int, MTMAX>{});
+        break;
     }
     wait_vm<0>();
 
-    // ---- epilogue: lane holds C[32 t + 8 (v / 4) + 4 hf + v % 4][column l32 of set j].
+    // ---- epilogue: lane holds C[32 t + 8 (v / 4) + 4 hf + v % 4][column l32 of set j],
+    // scaled by 2^(ex_row + wexp).
     if (UP) {
-        uint16_t *hout = ti.shared ? a.hs : a.h;
+        float *hout = ti.shared ? a.hs : a.h;
         const int col = n0 + 32 * wv + l32;
         if (col < W0.rows) {
 #pragma unroll
@@ -577,11 +627,12 @@ __global__ __launch_bounds__(256, 1) __attribute__((amdgpu_waves_per_eu(1, 1))) 
                 if (t >= mt) continue;
 #pragma unroll
                 for (int v = 0; v < 16; v++) {
-                    const int d = dst_row[32 * t + 8 * (v / 4) + 4 * hf + (v % 4)];
+                    const int r = 32 * t + 8 * (v / 4) + 4 * hf + (v % 4);
+                    const int d = dst_row[r];
                     if (d < 0) continue;
-                    const float g = acc[t][0][v], u = acc[t][1][v];
-                    const float hv = (g / (1.0f + __expf(-g))) * u;
-                    hout[(size_t)d * Icol + col] = __half_as_ushort(__float2half_rn(hv));
+                    const int e = ex_row[r];
+                    const float g = ldexpf(acc[t][0][v], -(e + wexp0)), u = ldexpf(acc[t][1][v], -(e + wexp1));
+                    hout[(size_t)d * Icol + col] = (g / (1.0f + expf_exact(-g))) * u;
                 }
             }
         }
@@ -596,36 +647,118 @@ __global__ __launch_bounds__(256, 1) __attribute__((amdgpu_waves_per_eu(1, 1))) 
                 if (t >= mt) continue;
 #pragma unroll
                 for (int v = 0; v < 16; v++) {
-                    const int d = dst_row[32 * t + 8 * (v / 4) + 4 * hf + (v % 4)];
-                    if (d >= 0) yout[(size_t)d * a.H + col] = acc[t][j][v];
+                    const int r = 32 * t + 8 * (v / 4) + 4 * hf + (v % 4);
+                    const int d = dst_row[r];
+                    if (d >= 0) yout[(size_t)d * a.H + col] = ldexpf(acc[t][j][v], -(ex_row[r] + wexp0));
                 }
             }
         }
     }
 }
 
-template <int DT, bool UP>
+template <int DT, bool UP, int BM>
 hipError_t launch_one(dim3 grid, const MfmaArgs &a, int mode, int ksplit, hipStream_t s) {
-    static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void *>(&mfma_kernel<DT, UP>),
-                                                       hipFuncAttributeMaxDynamicSharedMemorySize, lds_bytes<DT>());
+    constexpr int lds = lds_bytes<DT, BM>();
+    static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void *>(&mfma_kernel<DT, UP, BM>),
+                                                       hipFuncAttributeMaxDynamicSharedMemorySize, lds);
     if (attr != hipSuccess) return attr;
-    hipLaunchKernelGGL((mfma_kernel<DT, UP>), grid, dim3(256), lds_bytes<DT>(), s, a, mode, (int)grid.x, ksplit);
+    hipLaunchKernelGGL((mfma_kernel<DT, UP, BM>), grid, dim3(256), lds, s, a, mode, (int)grid.x, ksplit);
     return hipGetLastError();
 }
 
 template <bool UP>
-hipError_t launch_dt(int dt, dim3 grid, const MfmaArgs &a, int mode, int ksplit, hipStream_t s) {
+hipError_t launch_dt(int dt, int bm, dim3 grid, const MfmaArgs &a, int mode, int ksplit, hipStream_t s) {
+    if (bm == 160) {
+        switch (dt) {
+        case MOE_DT_Q4_0: return launch_one<MOE_DT_Q4_0, UP, 160>(grid, a, mode, ksplit, s);
+        case MOE_DT_Q5_0: return launch_one<MOE_DT_Q5_0, UP, 160>(grid, a, mode, ksplit, s);
+        default: return hipErrorInvalidValue;
+        }
+    }
+    if (bm != 128) return hipErrorInvalidValue;
     switch (dt) {
-    case MOE_DT_Q8_0: return launch_one<MOE_DT_Q8_0, UP>(grid, a, mode, ksplit, s);
-    case MOE_DT_Q4_0: return launch_one<MOE_DT_Q4_0, UP>(grid, a, mode, ksplit, s);
-    case MOE_DT_Q5_0: return launch_one<MOE_DT_Q5_0, UP>(grid, a, mode, ksplit, s);
+    case MOE_DT_Q8_0: return launch_one<MOE_DT_Q8_0, UP, 128>(grid, a, mode, ksplit, s);
+    case MOE_DT_Q4_0: return launch_one<MOE_DT_Q4_0, UP, 128>(grid, a, mode, ksplit, s);
+    case MOE_DT_Q5_0: return launch_one<MOE_DT_Q5_0, UP, 128>(grid, a, mode, ksplit, s);
     default: return hipErrorInvalidValue;
     }
 }
 
+// ---- activation pieces ------------------------------------------------------
+// One block per row: the row's largest magnitude (a max over the block),
+// then every value's scaled hi and lo pieces, four values per thread step.
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+__global__ __launch_bounds__(256) void split_rows_kernel(const float *__restrict__ src, int cols,
+                                                         uint16_t *__restrict__ hi, uint16_t *__restrict__ lo,
+                                                         int32_t *__restrict__ ex) {
+    __shared__ float part[4];
+    const size_t row = blockIdx.x;
+    const f32x4 *s4 = reinterpret_cast<const f32x4 *>(src + row * cols);
+    const int n4 = cols / 4;
+    float m = 0.0f;
+    for (int i = threadIdx.x; i < n4; i += 256) {
+        const f32x4 v = gload(s4 + i);
+        m = fmaxf(m, fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
+    }
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
+    if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = m;
+    __syncthreads();
+    m = fmaxf(fmaxf(part[0], part[1]), fmaxf(part[2], part[3]));
+    int e = 0;
+    if (m > 0.0f && m <= 3.402823466e38f) {
+        int fe;
+        (void)frexpf(m, &fe);  // m in [2^(fe-1), 2^fe)
+        e = 15 - fe;
+    }
+    if (threadIdx.x == 0) ex[row] = e;
+    typedef uint16_t u16x4 __attribute__((ext_vector_type(4)));
+    u16x4 *h4 = reinterpret_cast<u16x4 *>(hi + row * cols);
+    u16x4 *l4 = reinterpret_cast<u16x4 *>(lo + row * cols);
+    for (int i = threadIdx.x; i < n4; i += 256) {
+        const f32x4 v = gload(s4 + i);
+        u16x4 ho, lw;
+#pragma unroll
+        for (int c = 0; c < 4; c++) {
+            const float x = ldexpf(v[c], e);
+            const __half h = __float2half_rn(x);
+            ho[c] = __half_as_ushort(h);
+            lw[c] = __half_as_ushort(__float2half_rn(x - __half2float(h)));
+        }
+        gstore(h4 + i, ho);
+        gstore(l4 + i, lw);
+    }
+}
+
+// ---- weight scales -------------------------------------------------------------
+// Block (g, m, z): slice z of matrix m of expert g; every 32-value block's
+// scale (the first two bytes of the block), as |d| in f16 bits.
+__global__ __launch_bounds__(256) void scale_max_kernel(const ExpertDev *__restrict__ experts,
+                                                        unsigned *__restrict__ out) {
+    const MatDev m = experts[blockIdx.x].m[blockIdx.y];
+    const int bb = block_bytes(m.dt);
+    unsigned best = 0;
+    if (m.dt == MOE_DT_Q4_0 || m.dt == MOE_DT_Q5_0 || m.dt == MOE_DT_Q8_0) {
+        const long long per_row = m.cols / 32, n = (long long)m.rows * per_row;
+        for (long long i = (long long)blockIdx.z * 256 + threadIdx.x; i < n; i += (long long)gridDim.z * 256) {
+            const long long r = i / per_row, b = i - r * per_row;
+            const uint8_t *p = m.ptr + (size_t)r * m.stride + (size_t)b * bb;
+            const unsigned bits = ((unsigned)gload(p) | ((unsigned)gload(p + 1) << 8)) & 0x7fffu;
+            best = bits > best && bits < 0x7c00u ? bits : best;  // skip inf / nan scales
+        }
+    }
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) best = max(best, (unsigned)__shfl_xor((int)best, o, 64));
+    if ((threadIdx.x & 63) == 0 && best) atomicMax(out + 3 * blockIdx.x + blockIdx.y, best);
+}
+
 }  // namespace
 
-int mfma_tile_m() { return BM; }
+int mfma_tile_m(const int *dts, int n) {
+    for (int i = 0; i < n; i++)
+        if (dts[i] == MOE_DT_Q8_0) return 128;
+    return 160;
+}
 
 bool mfma_format_ok(int dt) { return dt == MOE_DT_Q4_0 || dt == MOE_DT_Q5_0 || dt == MOE_DT_Q8_0; }
 
@@ -647,17 +780,31 @@ int mfma_down_ksplit(int m_tiles, int n_rows, int K, int K_shared) {
     return ks;
 }
 
-hipError_t launch_mfma(bool up, const MfmaArgs &a, int /*bm*/, const ExpertDev &e0, const ExpertDev *sh,
+hipError_t launch_mfma(bool up, const MfmaArgs &a, int bm, const ExpertDev &e0, const ExpertDev *sh,
                        hipStream_t s) {
     const MatDev &m = up ? e0.m[0] : e0.m[2];
     const int cols = up ? BW / 2 : BW;
     const int ks = up ? 1 : a.ksplit;
     dim3 grid(a.max_tiles, (m.rows + cols - 1) / cols, ks);
-    hipError_t err = up ? launch_dt<true>(m.dt, grid, a, 0, ks, s) : launch_dt<false>(m.dt, grid, a, 0, ks, s);
+    hipError_t err = up ? launch_dt<true>(m.dt, bm, grid, a, 0, ks, s) : launch_dt<false>(m.dt, bm, grid, a, 0, ks, s);
     if (err != hipSuccess || !sh) return err;
     const MatDev &ms = up ? sh->m[0] : sh->m[2];
-    dim3 gs((a.T + BM - 1) / BM, (ms.rows + cols - 1) / cols, ks);
-    return up ? launch_dt<true>(ms.dt, gs, a, 1, ks, s) : launch_dt<false>(ms.dt, gs, a, 1, ks, s);
+    dim3 gs((a.T + bm - 1) / bm, (ms.rows + cols - 1) / cols, ks);
+    return up ? launch_dt<true>(ms.dt, bm, gs, a, 1, ks, s) : launch_dt<false>(ms.dt, bm, gs, a, 1, ks, s);
+}
+
+hipError_t launch_split_rows(const float *src, int rows, int cols, uint16_t *hi, uint16_t *lo, int32_t *ex,
+                             hipStream_t s) {
+    if (rows <= 0) return hipSuccess;
+    if (cols % 4 != 0) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(split_rows_kernel, dim3(rows), dim3(256), 0, s, src, cols, hi, lo, ex);
+    return hipGetLastError();
+}
+
+hipError_t launch_scale_max(const ExpertDev *experts, int n, unsigned *out, hipStream_t s) {
+    if (n <= 0) return hipSuccess;
+    hipLaunchKernelGGL(scale_max_kernel, dim3(n, 3, 16), dim3(256), 0, s, experts, out);
+    return hipGetLastError();
 }
 
 }  // namespace moe

@@ -4,6 +4,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <cmath>
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
@@ -13,7 +14,6 @@
 #include <vector>
 
 #include "moe_internal.h"
-#include "qact.h"
 #include "qact.h"
 
 using namespace moe;
@@ -36,6 +36,7 @@ int fail(int code, const char *fmt, ...) {
 }
 
 }  // namespace moe
+
 
 namespace {
 
@@ -62,6 +63,19 @@ struct Region {
 // Forward path for a call.
 enum Path { kExact = 1, kGemv = 2, kMfma = 3, kDecode = 4, kBatch = 5 };
 
+// A normal or subnormal f16 magnitude (bits & 0x7fff, below inf) as float.
+float f16_bits_to_float(unsigned bits) {
+    const int e = (int)(bits >> 10) & 31, m = (int)(bits & 1023);
+    return e == 0 ? std::ldexp((float)m, -24) : std::ldexp((float)(1024 + m), e - 25);
+}
+
+// A workspace a layer owns for one stream (moe_layer_forward).
+struct StreamWs {
+    hipStream_t stream;
+    Workspace w;
+    int k;
+};
+
 }  // namespace
 
 struct moe_ctx {
@@ -78,22 +92,26 @@ struct moe_layer {
     float routed_scale = 1.0f;
     bool has_shared = false, has_shared_gate = false;
     bool fast_ok = false, mfma_ok = false, decode_ok = false, batch_ok = false;
-    int mode = 0;  // 0 auto, else a Path
-    // routing override
-    float temp = 0.0f;
-    int top_k_override = 0;
-    int n_forced = 0;
+    int mfma_bm = 160;  // token tile of the MFMA kernels for this layer's formats
     // device memory owned by the layer
     float *router = nullptr;             // [E + has_shared_gate, H]
     const float *e_bias = nullptr;       // points into a region
-    uint8_t *disabled = nullptr;         // [E]
-    int32_t *forced = nullptr;           // [kMaxForced]
     ExpertDev *experts_dev = nullptr;    // [E + 1]
     unsigned long long *expert_bytes = nullptr;  // [E]
     std::vector<ExpertDev> experts_host;
+    // Everything below may change between calls; `mu` guards it.  A call
+    // takes a snapshot of the routing and the mode under the lock.
+    std::mutex mu;
+    int mode = 0;  // 0 auto, else a Path
+    float temp = 0.0f;
+    int top_k_override = 0;
+    int n_forced = 0;
+    int32_t forced[kMaxForced] = {};
+    uint32_t disabled[kMaxExperts / 32] = {};
     bool any_disabled = false;
-    Workspace ws;
-    int ws_k = 0;
+    std::vector<StreamWs> ws;            // one workspace per stream used with moe_layer_forward
+    std::vector<void *> retired;         // outgrown workspaces, freed by moe_layer_destroy
+    int reserved_t = 0, reserved_k = 0;  // after moe_layer_reserve: calls beyond these fail
     // stage timing
     bool profile = false;
     struct StageRec {
@@ -122,19 +140,20 @@ hipEvent_t take_event(moe_layer *L) {
 // Runs `fn` (which launches one stage's kernels on `s`) between two events
 // when profiling is on.
 template <class F>
-int stage(moe_layer *L, int id, hipStream_t s, F fn) {
-    if (!L->profile) return fn();
-    hipEvent_t a = take_event(L), b = take_event(L);
+int stage(moe_layer *L, bool profile, int id, hipStream_t s, F fn) {
+    if (!profile) return fn();
+    hipEvent_t a, b;
+    {
+        std::lock_guard<std::mutex> g(L->mu);
+        a = take_event(L), b = take_event(L);
+    }
     hipEventRecord(a, s);
     const int rc = fn();
     hipEventRecord(b, s);
+    std::lock_guard<std::mutex> g(L->mu);
     L->pending.push_back({id, a, b});
     return rc;
 }
-
-}  // namespace
-
-namespace {
 
 const Region *region_of(moe_ctx *ctx, uint64_t id) {
     if (id >= ctx->regions.size() || !ctx->regions[id].ptr) return nullptr;
@@ -174,7 +193,8 @@ bool fast_mat(const MatDev &m) {
     return ((uintptr_t)m.ptr % 4 == 0) && (m.stride % 4 == 0) && (m.cols % 64 == 0) && (m.cols / 64 <= 256);
 }
 
-int effective_k(const moe_layer *L) {
+
+int effective_k_locked(const moe_layer *L) {
     int k = L->top_k_override > 0 ? L->top_k_override : L->top_k_spec;
     return std::min(k, L->E);
 }
@@ -191,81 +211,465 @@ bool batch_pays(int t, int k, int E, int nt) {
     return 2 * rows <= 3LL * nt * hit;
 }
 
-void free_ws(Workspace &w) {
-    if (w.base) hipFree(w.base);
-    w = Workspace();
-}
-
-int reserve(moe_layer *L, int max_t, int k) {
-    if (max_t <= L->ws.max_t && k <= L->ws_k) return MOE_OK;
-    max_t = std::max(max_t, L->ws.max_t);
-    k = std::max(k, L->ws_k);
+// Byte layout of a workspace for up to max_t tokens of k experts each.
+// The first 256 bytes hold the counters that must be zero between calls
+// (they sit at the same place whatever max_t is); every array starts on a
+// 256-byte boundary.  Assigns w's pointers when base is given; returns the
+// total size.
+size_t ws_layout(const moe_layer *L, int max_t, int k, Workspace *w, char *base) {
     const size_t T = (size_t)max_t, E = (size_t)L->E, H = (size_t)L->H;
     const size_t I = (size_t)std::max(L->I, 1), Is = (size_t)std::max(L->I_s, 1);
-    // Tiles of one token or more (the few-tokens path), or 160 (MFMA).
+    // Tiles of one token or more (the few-tokens path), or bm (MFMA).
     const size_t max_tiles = T * k + E + 2 + T;
     // Activation units for the few-tokens path, which runs up to kBatchMaxT tokens.
     const size_t Tb = L->batch_ok ? std::min<size_t>(T, kBatchMaxT) : 0;
+    // f16 pieces of the MFMA path.
+    const size_t Tm = L->mfma_ok ? T : 0;
+    // Room for the K parts of a split MFMA / few-tokens down projection.
+    // Splitting only pays for small grids, so parts after the first are
+    // bounded in rows.
+    const size_t extra = (L->mfma_ok || L->batch_ok) ? (kMaxKSplit - 1) * std::min<size_t>(T * k, 8192) : 0;
+    const size_t y_rows = T * k + extra, ys_rows = T + extra;
+    Workspace tmp;
+    Workspace &x = w ? *w : tmp;
+    x = Workspace();
+    x.max_t = max_t;
+    x.batch_t = (int)Tb;
+    x.y_rows = y_rows;
+    x.ys_rows = ys_rows;
     struct Item {
         void **dst;
         size_t bytes;
     };
-    Workspace w;
-    w.max_t = max_t;
-    w.batch_t = (int)Tb;
-    // Room for the K parts of a split MFMA down projection.  Splitting only
-    // pays for small grids, so parts after the first are bounded in rows.
-    const size_t extra = (L->mfma_ok || L->batch_ok) ? (kMaxKSplit - 1) * std::min<size_t>(T * k, 8192) : 0;
-    w.y_rows = T * k + extra;
-    w.ys_rows = T + extra;
-    Item items[] = {
-        {(void **)&w.logits, T * (E + 1) * 4},
-        {(void **)&w.sel, T * k * 4},
-        {(void **)&w.wsel, T * k * 4},
-        {(void **)&w.shgate, T * 4},
-        {(void **)&w.counts, (E + 2) * 4},
-        {(void **)&w.offsets, (E + 2) * 4},
-        {(void **)&w.perm_tok, T * k * 4},
-        {(void **)&w.perm_w, T * k * 4},
-        {(void **)&w.pos, T * k * 4},
-        {(void **)&w.hits, (E + 2) * 4},
-        {(void **)&w.tiles, 4 * max_tiles * 4},
-        {(void **)&w.dtasks, (size_t)(k + 1) * sizeof(DecodeTask)},
-        {(void **)&w.route_count, 4},
-        {(void **)&w.ntiles, 4},
-        {(void **)&w.chunks, (size_t)dispatch_chunks((int)T) * E * 4},
-        {(void **)&w.xh, T * H * 2},
-        {(void **)&w.xq, Tb * (H / 64) * kQUnitBytes},
-        {(void **)&w.hq, Tb * k * (I / 64) * kQUnitBytes},
-        {(void **)&w.hsq, Tb * (Is / 64) * kQUnitBytes},
-        {(void **)&w.h, T * k * I * 4},
-        {(void **)&w.hs, T * Is * 4},
-        {(void **)&w.y, w.y_rows * H * 4},
-        {(void **)&w.ys, w.ys_rows * H * 4},
-        {(void **)&w.stats, 4 * 8},
+    const Item items[] = {
+        {(void **)&x.route_count, 4},
+        {(void **)&x.logits, T * (E + 1) * 4},
+        {(void **)&x.sel, T * k * 4},
+        {(void **)&x.wsel, T * k * 4},
+        {(void **)&x.shgate, T * 4},
+        {(void **)&x.counts, (E + 2) * 4},
+        {(void **)&x.offsets, (E + 2) * 4},
+        {(void **)&x.perm_tok, T * k * 4},
+        {(void **)&x.perm_w, T * k * 4},
+        {(void **)&x.pos, T * k * 4},
+        {(void **)&x.hits, (E + 2) * 4},
+        {(void **)&x.tiles, 4 * max_tiles * 4},
+        {(void **)&x.dtasks, (size_t)(k + 1) * sizeof(DecodeTask)},
+        {(void **)&x.ntiles, 4},
+        {(void **)&x.chunks, (size_t)dispatch_chunks((int)T) * E * 4},
+        {(void **)&x.xhi, Tm * H * 2},
+        {(void **)&x.xlo, Tm * H * 2},
+        {(void **)&x.xex, Tm * 4},
+        {(void **)&x.hhi, Tm * k * I * 2},
+        {(void **)&x.hlo, Tm * k * I * 2},
+        {(void **)&x.hex, Tm * k * 4},
+        {(void **)&x.hshi, L->has_shared ? Tm * Is * 2 : 0},
+        {(void **)&x.hslo, L->has_shared ? Tm * Is * 2 : 0},
+        {(void **)&x.hsex, L->has_shared ? Tm * 4 : 0},
+        {(void **)&x.xq, Tb * (H / 64) * kQUnitBytes},
+        {(void **)&x.hq, Tb * k * (I / 64) * kQUnitBytes},
+        {(void **)&x.hsq, Tb * (Is / 64) * kQUnitBytes},
+        {(void **)&x.h, T * k * I * 4},
+        {(void **)&x.hs, T * Is * 4},
+        {(void **)&x.y, y_rows * H * 4},
+        {(void **)&x.ys, ys_rows * H * 4},
+        {(void **)&x.stats, 4 * 8},
     };
-    size_t total = 0;
-    for (auto &it : items) total += align_up(it.bytes, 256);
-    void *base = nullptr;
-    hipError_t e = hipMalloc(&base, total);
-    if (e != hipSuccess) return fail(MOE_ENOMEM, "workspace of %zu bytes for %d tokens: %s", total, max_t, hipGetErrorString(e));
     size_t off = 0;
-    for (auto &it : items) {
-        *it.dst = static_cast<char *>(base) + off;
-        off += align_up(it.bytes, 256);
+    for (const Item &it : items) {
+        if (base) *it.dst = base + off;
+        off += align_up(std::max<size_t>(it.bytes, 1), 256);
     }
-    w.base = base;
-    w.bytes = total;
-    if ((e = hipMemset(w.route_count, 0, 4)) != hipSuccess) {
-        hipFree(base);
-        return fail(MOE_EHIP, "workspace counter: %s", hipGetErrorString(e));
-    }
+    x.base = base;
+    x.bytes = off;
+    return off;
+}
 
-    // Old workspace may still be in use by queued work on some stream.
-    hipDeviceSynchronize();
-    free_ws(L->ws);
-    L->ws = w;
-    L->ws_k = k;
+// The workspace of `stream` for t tokens (moe_layer_forward): the layer
+// keeps one per stream, so calls on different streams never share scratch.
+// Grows (without waiting for the device: an outgrown workspace is kept
+// until moe_layer_destroy, since queued work may still use it) unless the
+// layer was reserved, in which case a larger call fails.
+int stream_ws(moe_layer *L, hipStream_t s, int t, int k, Workspace &out) {
+    std::lock_guard<std::mutex> g(L->mu);
+    StreamWs *cur = nullptr;
+    for (StreamWs &e : L->ws)
+        if (e.stream == s) cur = &e;
+    if (cur && t <= cur->w.max_t && k <= cur->k) {
+        out = cur->w;
+        return MOE_OK;
+    }
+    if (L->reserved_t > 0 && (t > L->reserved_t || k > L->reserved_k))
+        return fail(MOE_EINVAL, "%d tokens of %d experts exceed the reservation of %d tokens of %d experts", t, k,
+                    L->reserved_t, L->reserved_k);
+    int max_t = std::max(t, L->reserved_t), kk = std::max(k, L->reserved_k);
+    if (cur) max_t = std::max(max_t, cur->w.max_t), kk = std::max(kk, cur->k);
+    const size_t bytes = ws_layout(L, max_t, kk, nullptr, nullptr);
+    void *base = nullptr;
+    hipError_t e = hipMalloc(&base, bytes);
+    if (e != hipSuccess) return fail(MOE_ENOMEM, "workspace of %zu bytes for %d tokens: %s", bytes, max_t, hipGetErrorString(e));
+    if ((e = hipMemset(base, 0, 256)) != hipSuccess) {
+        hipFree(base);
+        return fail(MOE_EHIP, "workspace counters: %s", hipGetErrorString(e));
+    }
+    Workspace w;
+    ws_layout(L, max_t, kk, &w, static_cast<char *>(base));
+    if (cur) {
+        L->retired.push_back(cur->w.base);
+        cur->w = w;
+        cur->k = kk;
+    } else {
+        L->ws.push_back({s, w, kk});
+    }
+    out = w;
+    return MOE_OK;
+}
+
+// What a call reads of the layer's mutable state, taken under the lock.
+struct CallState {
+    int mode;
+    int k;
+    bool profile;
+    GateParams gp;
+};
+
+CallState snapshot(moe_layer *L) {
+    std::lock_guard<std::mutex> g(L->mu);
+    CallState c;
+    c.mode = L->mode;
+    c.k = effective_k_locked(L);
+    c.profile = L->profile;
+    GateParams &p = c.gp;
+    p = GateParams{};
+    p.n_experts = L->E;
+    p.top_k = c.k;
+    p.sigmoid = L->gate == MOE_GATE_SIGMOID;
+    p.norm_topk = L->norm_topk;
+    p.n_group = L->n_group;
+    p.topk_group = L->topk_group;
+    p.routed_scale = L->routed_scale;
+    p.temp = L->temp;
+    p.n_forced = L->n_forced;
+    p.has_shared_gate = L->has_shared_gate;
+    p.e_bias = L->e_bias;
+    p.any_disabled = L->any_disabled;
+    std::memcpy(p.disabled, L->disabled, sizeof p.disabled);
+    std::memcpy(p.forced, L->forced, sizeof p.forced);
+    return c;
+}
+
+// Router, gating and dispatch; shared by forward and route.
+int route_and_dispatch(moe_layer *L, const CallState &c, Workspace &w, const float *x, int t, int bm, bool decode,
+                       moe_route *routes, uint32_t *hits, const uint32_t *prev, uint64_t *stats, float *logits_out,
+                       hipStream_t s) {
+    const int k = c.k;
+    const int n_rows = L->E + (L->has_shared_gate ? 1 : 0);
+    hipError_t e = hipSuccess;
+    unsigned long long *st = stats ? reinterpret_cast<unsigned long long *>(stats) : w.stats;
+    const GateParams &p = c.gp;
+    DispatchArgs a{};
+    a.sel = w.sel;
+    a.wsel = w.wsel;
+    a.T = t;
+    a.k = k;
+    a.E = L->E;
+    a.has_shared = L->has_shared;
+    a.bm = bm;
+    a.expert_bytes = L->expert_bytes;
+    a.prev = prev;
+    a.counts = w.counts;
+    a.offsets = w.offsets;
+    a.perm_tok = w.perm_tok;
+    a.pos = w.pos;
+    a.hits = w.hits;
+    a.tiles = w.tiles;
+    a.ntiles = w.ntiles;
+    a.perm_w = w.perm_w;
+    a.routes = routes;
+    a.hits_out = hits;
+    a.stats = st;
+    a.shgate_out = w.shgate;
+    if (decode) {
+        a.dtasks = w.dtasks;
+        a.experts = L->experts_dev;
+        a.h = w.h;
+        a.hs = w.hs;
+        a.shgate = L->has_shared_gate ? w.shgate : nullptr;
+        a.I = L->I;
+        a.dk_bound = k;
+    }
+    auto copy_logits = [&]() -> int {
+        if (!logits_out) return MOE_OK;
+        if ((e = hipMemcpy2DAsync(logits_out, (size_t)L->E * 4, w.logits, (size_t)n_rows * 4, (size_t)L->E * 4, t,
+                                  hipMemcpyDeviceToDevice, s)) != hipSuccess)
+            return hip_fail(e, "logits copy");
+        return MOE_OK;
+    };
+    if (t == 1 && route_one_ok(L->H)) {
+        // One token: router, gating and dispatch in a single launch.
+        int rc = stage(L, c.profile, 0, s, [&] {
+            e = launch_route_one(L->router, x, n_rows, L->E, L->H, p.temp, w.logits, p, a, w.route_count, s);
+            return e == hipSuccess ? MOE_OK : hip_fail(e, "one-token route kernel");
+        });
+        return rc ? rc : copy_logits();
+    }
+    int rc = stage(L, c.profile, 0, s, [&] {
+        e = launch_router(L->router, x, t, n_rows, L->E, L->H, p.temp, w.logits, s);
+        return e == hipSuccess ? MOE_OK : hip_fail(e, "router kernel");
+    });
+    if (rc) return rc;
+    rc = stage(L, c.profile, 1, s, [&] {
+        e = launch_gating(w.logits, n_rows, t, p, w.sel, w.wsel, w.shgate, st, s);
+        return e == hipSuccess ? MOE_OK : hip_fail(e, "gating kernel");
+    });
+    if (rc) return rc;
+    if ((rc = copy_logits())) return rc;
+    return stage(L, c.profile, 2, s, [&] {
+        e = launch_dispatch(a, w.chunks, s);
+        return e == hipSuccess ? MOE_OK : hip_fail(e, "dispatch kernel");
+    });
+}
+
+// The routed layer on workspace w (sized for at least t tokens of c.k
+// experts).
+int forward_on(moe_layer *L, const CallState &c, Workspace &w, const float *x, int t, float *out, float *residual,
+               moe_route *routes, uint32_t *hits, const uint32_t *prev, uint64_t *stats, hipStream_t s) {
+    const int k = c.k;
+    // Path: the one-token kernels for one token, the few-tokens kernels
+    // while experts hold few tokens each, MFMA beyond (it beats the register
+    // GEMV at every size measured on MI355X), GEMV where the MFMA kernel does
+    // not take the shapes, the exact kernels when neither fits (or when
+    // asked).
+    Path path = kExact;
+    if (c.mode) {
+        path = (Path)c.mode;
+    } else if (L->fast_ok) {
+        path = L->mfma_ok ? kMfma : kGemv;
+        if (t == 1 && L->decode_ok)
+            path = kDecode;
+        else if (L->batch_ok && batch_pays(t, k, L->E, batch_tile_tokens(L->H, t, k, L->E)))
+            path = kBatch;
+    }
+    if (path == kBatch && (!L->batch_ok || t > w.batch_t)) path = L->mfma_ok ? kMfma : kGemv;
+    if (path == kDecode) {
+        const int dt_r = L->experts_host[0].m[0].dt;
+        const int dt_s = L->has_shared ? L->experts_host[L->E].m[0].dt : dt_r;
+        if (t != 1 || !decode_fits(L->I, L->I_s, k, L->has_shared, dt_r, dt_s)) path = kGemv;
+    }
+    if (path == kMfma && !mfma_fits(t, k, L->H, L->I, L->has_shared ? L->I_s : 0)) path = kGemv;
+    const int bm = path == kMfma ? L->mfma_bm : path == kBatch ? batch_tile_tokens(L->H, t, k, L->E) : 0;
+    int rc = route_and_dispatch(L, c, w, x, t, bm, path == kDecode, routes, hits, prev, stats, nullptr, s);
+    if (rc) return rc;
+
+    const ExpertDev &e0 = L->experts_host[0];
+    const ExpertDev *sh = L->has_shared ? &L->experts_host[L->E] : nullptr;
+    hipError_t e = hipSuccess;
+    int ksplit = 1;
+    if (path == kDecode) {
+        DecodeArgs d{};
+        d.tasks = w.dtasks;
+        d.hits = w.hits;
+        d.h = w.h;
+        d.hs = w.hs;
+        d.has_gate = L->has_shared_gate ? 1 : 0;
+        d.out = out;
+        d.residual = residual;
+        d.H = L->H;
+        d.I = L->I;
+        d.I_s = L->I_s;
+        d.E = L->E;
+        d.k_bound = k;
+        d.n_shared = L->has_shared ? 1 : 0;
+        const int dt_r = e0.m[0].dt, dt_s = sh ? sh->m[0].dt : dt_r;
+        rc = stage(L, c.profile, 3, s, [&] {
+            e = launch_decode_up(d, x, dt_r, dt_s, s);
+            return e == hipSuccess ? MOE_OK : hip_fail(e, "one-token gate/up kernel");
+        });
+        if (rc) return rc;
+        return stage(L, c.profile, 4, s, [&] {
+            e = launch_decode_down(d, dt_r, dt_s, s);
+            return e == hipSuccess ? MOE_OK : hip_fail(e, "one-token down kernel");
+        });
+    }
+    if (path == kBatch) {
+        BatchArgs b{};
+        b.experts = L->experts_dev;
+        b.tiles = w.tiles;
+        b.ntiles = w.ntiles;
+        b.counts = w.counts;
+        b.offsets = w.offsets;
+        b.perm_tok = w.perm_tok;
+        b.xq = w.xq;
+        b.h = w.h;
+        b.hs = w.hs;
+        b.hq = w.hq;
+        b.hsq = w.hsq;
+        b.y = w.y;
+        b.ys = w.ys;
+        b.T = t;
+        b.H = L->H;
+        b.I = L->I;
+        b.I_s = L->I_s;
+        b.E = L->E;
+        b.max_tiles = t * k / bm + std::min(L->E, t * k) + 1;
+        b.shared_tiles = L->has_shared ? (t + bm - 1) / bm : 0;
+        b.ypart = (size_t)t * k * L->H;
+        b.yspart = (size_t)t * L->H;
+        b.ksplit = batch_ksplit(L->I, L->has_shared ? L->I_s : 0);
+        b.nt = bm;
+        if ((size_t)b.ksplit * t * k > w.y_rows || (size_t)b.ksplit * t > w.ys_rows)
+            return fail(MOE_EUNSUP, "few-tokens path: %d K parts do not fit the workspace", b.ksplit);
+        ksplit = b.ksplit;
+        rc = stage(L, c.profile, 6, s, [&] {
+            e = launch_qenc(x, t, L->H, w.xq, s);
+            return e == hipSuccess ? MOE_OK : hip_fail(e, "activation encoding");
+        });
+        if (rc) return rc;
+        rc = stage(L, c.profile, 3, s, [&] {
+            e = launch_batch_up(b, e0, sh, s);
+            return e == hipSuccess ? MOE_OK : hip_fail(e, "few-tokens gate/up kernel");
+        });
+        if (rc) return rc;
+        rc = stage(L, c.profile, 6, s, [&] {
+            e = launch_qenc(w.h, t * k, L->I, w.hq, s);
+            if (e == hipSuccess && sh) e = launch_qenc(w.hs, t, L->I_s, w.hsq, s);
+            return e == hipSuccess ? MOE_OK : hip_fail(e, "activation encoding");
+        });
+        if (rc) return rc;
+        rc = stage(L, c.profile, 4, s, [&] {
+            e = launch_batch_down(b, e0, sh, s);
+            return e == hipSuccess ? MOE_OK : hip_fail(e, "few-tokens down kernel");
+        });
+        if (rc) return rc;
+    } else if (path == kMfma) {
+        MfmaArgs m{};
+        m.experts = L->experts_dev;
+        m.tiles = w.tiles;
+        m.ntiles = w.ntiles;
+        m.counts = w.counts;
+        m.offsets = w.offsets;
+        m.perm_tok = w.perm_tok;
+        m.xhi = w.xhi;
+        m.xlo = w.xlo;
+        m.xex = w.xex;
+        m.h = w.h;
+        m.hs = w.hs;
+        m.hhi = w.hhi;
+        m.hlo = w.hlo;
+        m.hex = w.hex;
+        m.hshi = w.hshi;
+        m.hslo = w.hslo;
+        m.hsex = w.hsex;
+        m.y = w.y;
+        m.ys = w.ys;
+        m.T = t;
+        m.H = L->H;
+        m.I = L->I;
+        m.I_s = L->I_s;
+        m.E = L->E;
+        // Routed tiles: sum over experts of ceil(n_e / bm) <= t k / bm +
+        // (experts with tokens); the shared expert's tiles follow them.
+        m.max_tiles = t * k / bm + std::min(L->E, t * k) + 1;
+        m.shared_tiles = L->has_shared ? (t + bm - 1) / bm : 0;
+        m.ypart = (size_t)t * k * L->H;
+        m.yspart = (size_t)t * L->H;
+        m.ksplit = mfma_down_ksplit((t * k + bm - 1) / bm + std::min(L->E, t * k) / 2, L->H, L->I,
+                                    L->has_shared ? L->I_s : 0);
+        while (m.ksplit > 1 && ((size_t)m.ksplit * t * k > w.y_rows || (size_t)m.ksplit * t > w.ys_rows))
+            m.ksplit /= 2;
+        ksplit = m.ksplit;
+        rc = stage(L, c.profile, 6, s, [&] {
+            e = launch_split_rows(x, t, L->H, w.xhi, w.xlo, w.xex, s);
+            return e == hipSuccess ? MOE_OK : hip_fail(e, "activation pieces");
+        });
+        if (rc) return rc;
+        rc = stage(L, c.profile, 3, s, [&] {
+            e = launch_mfma(true, m, bm, e0, sh, s);
+            return e == hipSuccess ? MOE_OK : hip_fail(e, "MFMA up kernel");
+        });
+        if (rc) return rc;
+        rc = stage(L, c.profile, 6, s, [&] {
+            e = launch_split_rows(w.h, t * k, L->I, w.hhi, w.hlo, w.hex, s);
+            if (e == hipSuccess && sh) e = launch_split_rows(w.hs, t, L->I_s, w.hshi, w.hslo, w.hsex, s);
+            return e == hipSuccess ? MOE_OK : hip_fail(e, "activation pieces");
+        });
+        if (rc) return rc;
+        rc = stage(L, c.profile, 4, s, [&] {
+            e = launch_mfma(false, m, bm, e0, sh, s);
+            return e == hipSuccess ? MOE_OK : hip_fail(e, "MFMA down kernel");
+        });
+        if (rc) return rc;
+    } else {
+        GemvArgs a{};
+        a.experts = L->experts_dev;
+        a.hits = w.hits;
+        a.counts = w.counts;
+        a.offsets = w.offsets;
+        a.perm_tok = w.perm_tok;
+        a.x = x;
+        a.h = w.h;
+        a.hs = w.hs;
+        a.y = w.y;
+        a.ys = w.ys;
+        a.T = t;
+        a.H = L->H;
+        a.I = L->I;
+        a.I_s = L->I_s;
+        a.E = L->E;
+        a.task_bound = std::min(L->E, t * k);
+        a.has_shared = L->has_shared;
+        a.perm_w = w.perm_w;
+        a.shgate = L->has_shared_gate ? w.shgate : nullptr;
+        a.out = out;
+        a.residual = residual;
+        const bool fast = path == kGemv;
+        rc = stage(L, c.profile, 3, s, [&] {
+            e = fast ? launch_gemv_up(a, e0, sh, s) : launch_gemv_exact(true, a, s);
+            return e == hipSuccess ? MOE_OK : hip_fail(e, "expert gate/up kernel");
+        });
+        if (rc) return rc;
+        // Few tokens: the down projection performs the combine, the shared
+        // expert and the residual add itself.
+        const bool fused = fast && t <= kFusedMaxT;
+        rc = stage(L, c.profile, 4, s, [&] {
+            e = fast ? (fused ? launch_gemv_down_combine(a, e0, sh, s) : launch_gemv_down(a, e0, sh, s))
+                     : launch_gemv_exact(false, a, s);
+            return e == hipSuccess ? MOE_OK : hip_fail(e, "expert down kernel");
+        });
+        if (rc || fused) return rc;
+    }
+    CombineArgs cb{};
+    cb.y = w.y;
+    cb.ys = w.ys;
+    cb.parts = ksplit;
+    cb.ypart = (size_t)t * k * L->H;
+    cb.yspart = (size_t)t * L->H;
+    cb.pos = w.pos;
+    cb.sel = w.sel;
+    cb.wsel = w.wsel;
+    cb.shgate = L->has_shared_gate ? w.shgate : nullptr;
+    cb.out = out;
+    cb.residual = residual;
+    cb.T = t;
+    cb.H = L->H;
+    cb.k = k;
+    cb.has_shared = L->has_shared;
+    return stage(L, c.profile, 5, s, [&] {
+        e = launch_combine(cb, s);
+        return e == hipSuccess ? MOE_OK : hip_fail(e, "combine kernel");
+    });
+}
+
+// A caller's workspace laid out for t tokens of k experts, after checking
+// that it is big enough.
+int caller_ws(const moe_layer *L, int t, int k, void *ws, uint64_t ws_bytes, Workspace &w) {
+    if (!ws) return fail(MOE_EINVAL, "workspace is NULL");
+    if ((uintptr_t)ws % 256) return fail(MOE_EINVAL, "workspace is not 256-byte aligned");
+    const size_t need = ws_layout(L, t, k, nullptr, nullptr);
+    if (need > ws_bytes)
+        return fail(MOE_EINVAL, "%d tokens of %d experts need a %zu-byte workspace; %llu given", t, k, need,
+                    (unsigned long long)ws_bytes);
+    ws_layout(L, t, k, &w, static_cast<char *>(ws));
     return MOE_OK;
 }
 
@@ -490,9 +894,38 @@ int moe_layer_create(moe_ctx *ctx, const moe_layer_desc *d, moe_layer **out) {
     if ((he = hipMalloc(&L->expert_bytes, 8 * E)) != hipSuccess) return hip_fail(he, "expert bytes");
     if ((he = hipMemcpy(L->expert_bytes, eb.data(), 8 * E, hipMemcpyHostToDevice)) != hipSuccess)
         return hip_fail(he, "expert bytes");
-    if ((he = hipMalloc(&L->disabled, E)) != hipSuccess) return hip_fail(he, "routing tables");
-    if ((he = hipMemset(L->disabled, 0, E)) != hipSuccess) return hip_fail(he, "routing tables");
-    if ((he = hipMalloc(&L->forced, 4 * kMaxForced)) != hipSuccess) return hip_fail(he, "routing tables");
+    if (L->mfma_ok) {
+        // Per matrix, the power of two that puts the largest |d q| in
+        // [2^14, 2^15) for the MFMA path's f16 pieces (|q| <= 8, 16, 128).
+        const int n = E + (L->has_shared ? 1 : 0);
+        unsigned *mx = nullptr;
+        std::vector<unsigned> host(3 * (size_t)n, 0u);
+        if ((he = hipMalloc(&mx, 4 * host.size())) != hipSuccess) return hip_fail(he, "scale maxima");
+        he = hipMemset(mx, 0, 4 * host.size());
+        if (he == hipSuccess) he = launch_scale_max(L->experts_dev, n, mx, nullptr);
+        if (he == hipSuccess) he = hipMemcpy(host.data(), mx, 4 * host.size(), hipMemcpyDeviceToHost);
+        hipFree(mx);
+        if (he != hipSuccess) return hip_fail(he, "scale maxima");
+        for (int e = 0; e < n; e++)
+            for (int m = 0; m < 3; m++) {
+                MatDev &md = L->experts_host[e].m[m];
+                const unsigned bits = host[3 * (size_t)e + m];
+                const float qmax = md.dt == MOE_DT_Q4_0 ? 8.0f : md.dt == MOE_DT_Q5_0 ? 16.0f : 128.0f;
+                md.wexp = 0;
+                if (bits) {
+                    int fe = 0;
+                    (void)std::frexp(f16_bits_to_float(bits) * qmax, &fe);  // < 2^fe
+                    md.wexp = 15 - fe;
+                }
+            }
+        if ((he = hipMemcpy(L->experts_dev, L->experts_host.data(), sizeof(ExpertDev) * (E + 1),
+                            hipMemcpyHostToDevice)) != hipSuccess)
+            return hip_fail(he, "expert table");
+        std::vector<int> dts;
+        for (int e = 0; e < n; e++)
+            for (int m = 0; m < 3; m++) dts.push_back(L->experts_host[e].m[m].dt);
+        L->mfma_bm = mfma_tile_m(dts.data(), (int)dts.size());
+    }
     *out = L.release();
     return MOE_OK;
 }
@@ -501,12 +934,11 @@ void moe_layer_destroy(moe_layer *L) {
     if (!L) return;
     DeviceGuard g(L->ctx->device);
     hipDeviceSynchronize();
-    free_ws(L->ws);
+    for (StreamWs &e : L->ws) hipFree(e.w.base);
+    for (void *p : L->retired) hipFree(p);
     hipFree(L->router);
     hipFree(L->experts_dev);
     hipFree(L->expert_bytes);
-    hipFree(L->disabled);
-    hipFree(L->forced);
     for (auto &r : L->pending) L->event_pool.push_back(r.a), L->event_pool.push_back(r.b);
     for (hipEvent_t ev : L->event_pool) hipEventDestroy(ev);
     delete L;
@@ -514,29 +946,33 @@ void moe_layer_destroy(moe_layer *L) {
 
 int moe_layer_set_routing(moe_layer *L, const moe_routing *r) {
     if (!L) return fail(MOE_EINVAL, "moe_layer_set_routing: layer is NULL");
-    DeviceGuard g(L->ctx->device);
-    std::vector<uint8_t> dis(L->E, 0);
-    std::vector<int32_t> forced;
+    uint32_t dis[kMaxExperts / 32] = {};
+    int32_t forced[kMaxForced] = {};
+    int n_forced = 0;
     float temp = 0.0f;
     int top_k = 0;
+    bool any = false;
     if (r) {
         if (r->n_disabled < 0 || r->n_forced < 0 || (r->n_disabled && !r->disabled) || (r->n_forced && !r->forced))
             return fail(MOE_EINVAL, "moe_layer_set_routing: bad lists");
-        for (int i = 0; i < r->n_disabled; i++)
-            if (r->disabled[i] >= 0 && r->disabled[i] < L->E) dis[r->disabled[i]] = 1;
-        for (int i = 0; i < r->n_forced; i++) forced.push_back(r->forced[i]);
-        if ((int)forced.size() > kMaxForced) return fail(MOE_EUNSUP, "at most %d forced experts", kMaxForced);
+        if (r->n_forced > kMaxForced) return fail(MOE_EUNSUP, "at most %d forced experts", kMaxForced);
+        for (int i = 0; i < r->n_disabled; i++) {
+            const int e = r->disabled[i];
+            if (e >= 0 && e < L->E) dis[e >> 5] |= 1u << (e & 31), any = true;
+        }
+        for (int i = 0; i < r->n_forced; i++) forced[n_forced++] = r->forced[i];
         temp = r->temp;
         top_k = r->top_k;
         if (top_k < 0) return fail(MOE_EINVAL, "top_k %d", top_k);
         if (std::min(top_k, L->E) > kMaxTopK) return fail(MOE_EUNSUP, "top_k %d; at most %d is supported", top_k, kMaxTopK);
     }
-    hipError_t he = hipMemcpy(L->disabled, dis.data(), L->E, hipMemcpyHostToDevice);
-    if (he == hipSuccess && !forced.empty())
-        he = hipMemcpy(L->forced, forced.data(), 4 * forced.size(), hipMemcpyHostToDevice);
-    if (he != hipSuccess) return hip_fail(he, "moe_layer_set_routing");
-    L->any_disabled = std::any_of(dis.begin(), dis.end(), [](uint8_t v) { return v != 0; });
-    L->n_forced = (int)forced.size();
+    // Takes effect for calls made after this one; calls already queued keep
+    // the routing they were launched with (it travels in their arguments).
+    std::lock_guard<std::mutex> g(L->mu);
+    std::memcpy(L->disabled, dis, sizeof dis);
+    std::memcpy(L->forced, forced, sizeof forced);
+    L->any_disabled = any;
+    L->n_forced = n_forced;
     L->temp = temp;
     L->top_k_override = top_k;
     return MOE_OK;
@@ -548,117 +984,48 @@ int moe_layer_set_mode(moe_layer *L, int mode) {
     if (mode == kDecode && !L->decode_ok) return fail(MOE_EUNSUP, "this layer's shapes do not fit the one-token kernels");
     if (mode == kGemv && !L->fast_ok) return fail(MOE_EUNSUP, "this layer's shapes do not fit the GEMV kernels");
     if (mode == kMfma && !L->mfma_ok) return fail(MOE_EUNSUP, "this layer's shapes do not fit the MFMA kernels");
+    std::lock_guard<std::mutex> g(L->mu);
     L->mode = mode;
     return MOE_OK;
 }
 
-int moe_layer_reserve(moe_layer *L, int32_t max_t) {
+int moe_layer_reserve_stream(moe_layer *L, int32_t max_t, void *stream) {
     if (!L || max_t <= 0) return fail(MOE_EINVAL, "moe_layer_reserve: bad argument");
     DeviceGuard g(L->ctx->device);
-    return reserve(L, max_t, std::max(effective_k(L), std::min(L->top_k_spec, L->E)));
+    int k;
+    {
+        std::lock_guard<std::mutex> lk(L->mu);
+        k = std::max(effective_k_locked(L), std::min(L->top_k_spec, L->E));
+        L->reserved_t = std::max(L->reserved_t, (int)max_t);
+        L->reserved_k = std::max(L->reserved_k, k);
+    }
+    Workspace w;
+    return stream_ws(L, (hipStream_t)stream, max_t, k, w);
 }
 
-int moe_layer_k(const moe_layer *L) { return L ? effective_k(L) : 0; }
+int moe_layer_reserve(moe_layer *L, int32_t max_t) { return moe_layer_reserve_stream(L, max_t, nullptr); }
 
-static GateParams gate_params(const moe_layer *L, int k) {
-    GateParams p{};
-    p.n_experts = L->E;
-    p.top_k = k;
-    p.sigmoid = L->gate == MOE_GATE_SIGMOID;
-    p.norm_topk = L->norm_topk;
-    p.n_group = L->n_group;
-    p.topk_group = L->topk_group;
-    p.routed_scale = L->routed_scale;
-    p.temp = L->temp;
-    p.n_forced = L->n_forced;
-    p.has_shared_gate = L->has_shared_gate;
-    p.e_bias = L->e_bias;
-    p.disabled = L->any_disabled ? L->disabled : nullptr;
-    p.forced = L->forced;
-    return p;
+int moe_layer_k(const moe_layer *L) {
+    if (!L) return 0;
+    std::lock_guard<std::mutex> g(const_cast<moe_layer *>(L)->mu);
+    return effective_k_locked(L);
 }
 
-// Router, gating and dispatch; shared by forward and route.
-static int route_and_dispatch(moe_layer *L, const float *x, int t, int k, int bm, bool decode, moe_route *routes,
-                              uint32_t *hits, const uint32_t *prev, uint64_t *stats, float *logits_out,
-                              uint16_t *xh, hipStream_t s) {
-    Workspace &w = L->ws;
-    const int n_rows = L->E + (L->has_shared_gate ? 1 : 0);
-    hipError_t e = hipSuccess;
-    unsigned long long *st = stats ? reinterpret_cast<unsigned long long *>(stats) : w.stats;
-    GateParams p = gate_params(L, k);
-    DispatchArgs a{};
-    a.sel = w.sel;
-    a.wsel = w.wsel;
-    a.T = t;
-    a.k = k;
-    a.E = L->E;
-    a.has_shared = L->has_shared;
-    a.bm = bm;
-    a.expert_bytes = L->expert_bytes;
-    a.prev = prev;
-    a.counts = w.counts;
-    a.offsets = w.offsets;
-    a.perm_tok = w.perm_tok;
-    a.pos = w.pos;
-    a.hits = w.hits;
-    a.tiles = w.tiles;
-    a.ntiles = w.ntiles;
-    a.perm_w = w.perm_w;
-    a.routes = routes;
-    a.hits_out = hits;
-    a.stats = st;
-    a.shgate_out = w.shgate;
-    if (decode) {
-        a.dtasks = w.dtasks;
-        a.experts = L->experts_dev;
-        a.h = w.h;
-        a.hs = w.hs;
-        a.shgate = L->has_shared_gate ? w.shgate : nullptr;
-        a.I = L->I;
-        a.dk_bound = k;
-    }
-    auto copy_logits = [&]() -> int {
-        if (!logits_out) return MOE_OK;
-        if ((e = hipMemcpy2DAsync(logits_out, (size_t)L->E * 4, w.logits, (size_t)n_rows * 4, (size_t)L->E * 4, t,
-                                  hipMemcpyDeviceToDevice, s)) != hipSuccess)
-            return hip_fail(e, "logits copy");
-        return MOE_OK;
-    };
-    if (t == 1 && route_one_ok(L->H)) {
-        // One token: router, gating and dispatch in a single launch.
-        int rc = stage(L, 0, s, [&] {
-            e = launch_route_one(L->router, x, n_rows, L->E, L->H, L->temp, w.logits, p, a, w.route_count, s);
-            if (e == hipSuccess && xh) e = launch_to_f16(x, xh, (size_t)L->H, s);
-            return e == hipSuccess ? MOE_OK : hip_fail(e, "one-token route kernel");
-        });
-        return rc ? rc : copy_logits();
-    }
-    int rc = stage(L, 0, s, [&] {
-        e = launch_router(L->router, x, t, n_rows, L->E, L->H, L->temp, w.logits, xh, s);
-        return e == hipSuccess ? MOE_OK : hip_fail(e, "router kernel");
-    });
-    if (rc) return rc;
-    rc = stage(L, 1, s, [&] {
-        e = launch_gating(w.logits, n_rows, t, p, w.sel, w.wsel, w.shgate, st, s);
-        return e == hipSuccess ? MOE_OK : hip_fail(e, "gating kernel");
-    });
-    if (rc) return rc;
-    if ((rc = copy_logits())) return rc;
-    return stage(L, 2, s, [&] {
-        e = launch_dispatch(a, w.chunks, s);
-        return e == hipSuccess ? MOE_OK : hip_fail(e, "dispatch kernel");
-    });
+int moe_layer_workspace_size(const moe_layer *L, int32_t max_t, uint64_t *bytes) {
+    if (!L || max_t <= 0 || !bytes) return fail(MOE_EINVAL, "moe_layer_workspace_size: bad argument");
+    *bytes = ws_layout(L, max_t, moe_layer_k(L), nullptr, nullptr);
+    return MOE_OK;
 }
 
 int moe_layer_route(moe_layer *L, const float *x, int32_t t, moe_route *routes, float *logits, void *stream) {
     if (!L || !x || t <= 0) return fail(MOE_EINVAL, "moe_layer_route: bad argument");
     DeviceGuard g(L->ctx->device);
-    const int k = effective_k(L);
-    int rc = reserve(L, t, k);
+    hipStream_t s = (hipStream_t)stream;
+    const CallState c = snapshot(L);
+    Workspace w;
+    int rc = stream_ws(L, s, t, c.k, w);
     if (rc) return rc;
-    return route_and_dispatch(L, x, t, k, 0, false, routes, nullptr, nullptr, nullptr, logits, nullptr,
-                              (hipStream_t)stream);
+    return route_and_dispatch(L, c, w, x, t, 0, false, routes, nullptr, nullptr, nullptr, logits, s);
 }
 
 int moe_layer_forward(moe_layer *L, const float *x, int32_t t, float *out, float *residual, moe_route *routes,
@@ -666,212 +1033,28 @@ int moe_layer_forward(moe_layer *L, const float *x, int32_t t, float *out, float
     if (!L || !x || !out || t <= 0) return fail(MOE_EINVAL, "moe_layer_forward: bad argument (t = %d)", t);
     DeviceGuard g(L->ctx->device);
     hipStream_t s = (hipStream_t)stream;
-    const int k = effective_k(L);
-    int rc = reserve(L, t, k);
+    const CallState c = snapshot(L);
+    Workspace w;
+    int rc = stream_ws(L, s, t, c.k, w);
     if (rc) return rc;
-    Workspace &w = L->ws;
+    return forward_on(L, c, w, x, t, out, residual, routes, hits, prev, stats, s);
+}
 
-    // Path: the one-token kernels for one token, the few-tokens kernels
-    // while experts hold few tokens each, MFMA beyond (it beats the register
-    // GEMV at every size measured on MI355X), GEMV where the MFMA kernel does
-    // not take the shapes, the exact kernels when neither fits (or when
-    // asked).
-    Path path = kExact;
-    if (L->mode) {
-        path = (Path)L->mode;
-    } else if (L->fast_ok) {
-        path = L->mfma_ok ? kMfma : kGemv;
-        if (t == 1 && L->decode_ok)
-            path = kDecode;
-        else if (L->batch_ok && batch_pays(t, k, L->E, batch_tile_tokens(L->H, t, k, L->E)))
-            path = kBatch;
-    }
-    if (path == kBatch && (!L->batch_ok || t > w.batch_t)) path = L->mfma_ok ? kMfma : kGemv;
-    if (path == kDecode) {
-        const int dt_r = L->experts_host[0].m[0].dt;
-        const int dt_s = L->has_shared ? L->experts_host[L->E].m[0].dt : dt_r;
-        if (t != 1 || !decode_fits(L->I, L->I_s, k, L->has_shared, dt_r, dt_s)) path = kGemv;
-    }
-    if (path == kMfma && !mfma_fits(t, k, L->H, L->I, L->has_shared ? L->I_s : 0)) path = kGemv;
-    const int bm = path == kMfma ? mfma_tile_m() : path == kBatch ? batch_tile_tokens(L->H, t, k, L->E) : 0;
-    if ((rc = route_and_dispatch(L, x, t, k, bm, path == kDecode, routes, hits, prev, stats, nullptr,
-                                 path == kMfma ? w.xh : nullptr, s)))
-        return rc;
-
-    const ExpertDev &e0 = L->experts_host[0];
-    const ExpertDev *sh = L->has_shared ? &L->experts_host[L->E] : nullptr;
-    hipError_t e = hipSuccess;
-    int ksplit = 1;
-    if (path == kDecode) {
-        DecodeArgs d{};
-        d.tasks = w.dtasks;
-        d.hits = w.hits;
-        d.h = w.h;
-        d.hs = w.hs;
-        d.has_gate = L->has_shared_gate ? 1 : 0;
-        d.out = out;
-        d.residual = residual;
-        d.H = L->H;
-        d.I = L->I;
-        d.I_s = L->I_s;
-        d.E = L->E;
-        d.k_bound = k;
-        d.n_shared = L->has_shared ? 1 : 0;
-        const int dt_r = e0.m[0].dt, dt_s = sh ? sh->m[0].dt : dt_r;
-        rc = stage(L, 3, s, [&] {
-            e = launch_decode_up(d, x, dt_r, dt_s, s);
-            return e == hipSuccess ? MOE_OK : hip_fail(e, "one-token gate/up kernel");
-        });
-        if (rc) return rc;
-        return stage(L, 4, s, [&] {
-            e = launch_decode_down(d, dt_r, dt_s, s);
-            return e == hipSuccess ? MOE_OK : hip_fail(e, "one-token down kernel");
-        });
-    }
-    if (path == kBatch) {
-        BatchArgs b{};
-        b.experts = L->experts_dev;
-        b.tiles = w.tiles;
-        b.ntiles = w.ntiles;
-        b.counts = w.counts;
-        b.offsets = w.offsets;
-        b.perm_tok = w.perm_tok;
-        b.xq = w.xq;
-        b.h = w.h;
-        b.hs = w.hs;
-        b.hq = w.hq;
-        b.hsq = w.hsq;
-        b.y = w.y;
-        b.ys = w.ys;
-        b.T = t;
-        b.H = L->H;
-        b.I = L->I;
-        b.I_s = L->I_s;
-        b.E = L->E;
-        b.max_tiles = t * k / bm + std::min(L->E, t * k) + 1;
-        b.shared_tiles = L->has_shared ? (t + bm - 1) / bm : 0;
-        b.ypart = (size_t)t * k * L->H;
-        b.yspart = (size_t)t * L->H;
-        b.ksplit = batch_ksplit(L->I, L->has_shared ? L->I_s : 0);
-        b.nt = bm;
-        if ((size_t)b.ksplit * t * k > w.y_rows || (size_t)b.ksplit * t > w.ys_rows)
-            return fail(MOE_EUNSUP, "few-tokens path: %d K parts do not fit the workspace", b.ksplit);
-        ksplit = b.ksplit;
-        rc = stage(L, 3, s, [&] {
-            e = launch_qenc(x, t, L->H, w.xq, s);
-            if (e == hipSuccess) e = launch_batch_up(b, e0, sh, s);
-            return e == hipSuccess ? MOE_OK : hip_fail(e, "few-tokens gate/up kernel");
-        });
-        if (rc) return rc;
-        rc = stage(L, 4, s, [&] {
-            e = launch_qenc(w.h, t * k, L->I, w.hq, s);
-            if (e == hipSuccess && sh) e = launch_qenc(w.hs, t, L->I_s, w.hsq, s);
-            if (e == hipSuccess) e = launch_batch_down(b, e0, sh, s);
-            return e == hipSuccess ? MOE_OK : hip_fail(e, "few-tokens down kernel");
-        });
-        if (rc) return rc;
-    } else if (path == kMfma) {
-        MfmaArgs m{};
-        m.experts = L->experts_dev;
-        m.tiles = w.tiles;
-        m.ntiles = w.ntiles;
-        m.counts = w.counts;
-        m.offsets = w.offsets;
-        m.perm_tok = w.perm_tok;
-        m.xh = w.xh;
-        m.h = reinterpret_cast<uint16_t *>(w.h);
-        m.hs = reinterpret_cast<uint16_t *>(w.hs);
-        m.y = w.y;
-        m.ys = w.ys;
-        m.T = t;
-        m.H = L->H;
-        m.I = L->I;
-        m.I_s = L->I_s;
-        m.E = L->E;
-        // Routed tiles: sum over experts of ceil(n_e / bm) <= t k / bm +
-        // (experts with tokens); the shared expert's tiles follow them.
-        m.max_tiles = t * k / bm + std::min(L->E, t * k) + 1;
-        m.shared_tiles = L->has_shared ? (t + bm - 1) / bm : 0;
-        m.ypart = (size_t)t * k * L->H;
-        m.yspart = (size_t)t * L->H;
-        m.ksplit = mfma_down_ksplit((t * k + bm - 1) / bm + std::min(L->E, t * k) / 2, L->H, L->I,
-                                    L->has_shared ? L->I_s : 0);
-        while (m.ksplit > 1 && ((size_t)m.ksplit * t * k > w.y_rows || (size_t)m.ksplit * t > w.ys_rows))
-            m.ksplit /= 2;
-        ksplit = m.ksplit;
-        rc = stage(L, 3, s, [&] {
-            e = launch_mfma(true, m, bm, e0, sh, s);
-            return e == hipSuccess ? MOE_OK : hip_fail(e, "MFMA up kernel");
-        });
-        if (rc) return rc;
-        rc = stage(L, 4, s, [&] {
-            e = launch_mfma(false, m, bm, e0, sh, s);
-            return e == hipSuccess ? MOE_OK : hip_fail(e, "MFMA down kernel");
-        });
-        if (rc) return rc;
-    } else {
-        GemvArgs a{};
-        a.experts = L->experts_dev;
-        a.hits = w.hits;
-        a.counts = w.counts;
-        a.offsets = w.offsets;
-        a.perm_tok = w.perm_tok;
-        a.x = x;
-        a.h = w.h;
-        a.hs = w.hs;
-        a.y = w.y;
-        a.ys = w.ys;
-        a.T = t;
-        a.H = L->H;
-        a.I = L->I;
-        a.I_s = L->I_s;
-        a.E = L->E;
-        a.task_bound = std::min(L->E, t * k);
-        a.has_shared = L->has_shared;
-        a.perm_w = w.perm_w;
-        a.shgate = L->has_shared_gate ? w.shgate : nullptr;
-        a.out = out;
-        a.residual = residual;
-        const bool fast = path == kGemv;
-        rc = stage(L, 3, s, [&] {
-            e = fast ? launch_gemv_up(a, e0, sh, s) : launch_gemv_exact(true, a, s);
-            return e == hipSuccess ? MOE_OK : hip_fail(e, "expert gate/up kernel");
-        });
-        if (rc) return rc;
-        // Few tokens: the down projection performs the combine, the shared
-        // expert and the residual add itself.
-        const bool fused = fast && t <= kFusedMaxT;
-        rc = stage(L, 4, s, [&] {
-            e = fast ? (fused ? launch_gemv_down_combine(a, e0, sh, s) : launch_gemv_down(a, e0, sh, s))
-                     : launch_gemv_exact(false, a, s);
-            return e == hipSuccess ? MOE_OK : hip_fail(e, "expert down kernel");
-        });
-        if (rc || fused) return rc;
-    }
-    CombineArgs c{};
-    c.y = w.y;
-    c.ys = w.ys;
-    c.parts = ksplit;
-    c.ypart = (size_t)t * k * L->H;
-    c.yspart = (size_t)t * L->H;
-    c.pos = w.pos;
-    c.sel = w.sel;
-    c.wsel = w.wsel;
-    c.shgate = L->has_shared_gate ? w.shgate : nullptr;
-    c.out = out;
-    c.residual = residual;
-    c.T = t;
-    c.H = L->H;
-    c.k = k;
-    c.has_shared = L->has_shared;
-    return stage(L, 5, s, [&] {
-        e = launch_combine(c, s);
-        return e == hipSuccess ? MOE_OK : hip_fail(e, "combine kernel");
-    });
+int moe_layer_forward_ws(moe_layer *L, const float *x, int32_t t, float *out, float *residual, moe_route *routes,
+                         uint32_t *hits, const uint32_t *prev, uint64_t *stats, void *workspace,
+                         uint64_t workspace_bytes, void *stream) {
+    if (!L || !x || !out || t <= 0) return fail(MOE_EINVAL, "moe_layer_forward_ws: bad argument (t = %d)", t);
+    DeviceGuard g(L->ctx->device);
+    const CallState c = snapshot(L);
+    Workspace w;
+    int rc = caller_ws(L, t, c.k, workspace, workspace_bytes, w);
+    if (rc) return rc;
+    return forward_on(L, c, w, x, t, out, residual, routes, hits, prev, stats, (hipStream_t)stream);
 }
 
 int moe_layer_profile(moe_layer *L, int enable) {
     if (!L) return fail(MOE_EINVAL, "moe_layer_profile: layer is NULL");
+    std::lock_guard<std::mutex> g(L->mu);
     L->profile = enable != 0;
     return MOE_OK;
 }
@@ -879,13 +1062,14 @@ int moe_layer_profile(moe_layer *L, int enable) {
 int moe_layer_stage_times(moe_layer *L, double *ms, uint64_t *n) {
     if (!L || !ms || !n) return fail(MOE_EINVAL, "moe_layer_stage_times: bad argument");
     DeviceGuard g(L->ctx->device);
+    std::lock_guard<std::mutex> lk(L->mu);
     if (!L->pending.empty()) {
         hipError_t e = hipEventSynchronize(L->pending.back().b);
         if (e != hipSuccess) return hip_fail(e, "hipEventSynchronize");
     }
     for (auto &r : L->pending) {
         float t = 0.0f;
-        if (hipEventElapsedTime(&t, r.a, r.b) == hipSuccess) {
+        if (hipEventSynchronize(r.b) == hipSuccess && hipEventElapsedTime(&t, r.a, r.b) == hipSuccess) {
             L->stage_ms[r.stage] += t;
             L->stage_n[r.stage] += 1;
         }

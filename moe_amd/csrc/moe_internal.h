@@ -30,6 +30,10 @@ struct MatDev {
     int32_t dt;
     int32_t rows;
     int32_t cols;
+    // MFMA path: the block scales are multiplied by 2^wexp before the
+    // weights are split into f16 pieces (exact: a power of two), so that the
+    // matrix's largest |d q| lies in [2^14, 2^15).
+    int32_t wexp;
 };
 
 // A SwiGLU expert: gate [I,H], up [I,H], down [H,I].  Routed experts occupy
@@ -65,8 +69,11 @@ struct GateParams {
     int32_t n_forced;
     int32_t has_shared_gate;
     const float *e_bias;        // [E] or null
-    const uint8_t *disabled;    // [E] 0/1 or null
-    const int32_t *forced;      // [n_forced]
+    // Interventions travel by value in the launch arguments, so a forward
+    // already queued keeps the routing it was launched with.
+    int32_t any_disabled;
+    uint32_t disabled[kMaxExperts / 32];  // bit e: expert e may not be selected
+    int32_t forced[kMaxForced];           // [n_forced]
 };
 
 // Per-call scratch, sized for max_t tokens (see moe_layer_reserve).
@@ -87,12 +94,17 @@ struct Workspace {
     unsigned *route_count = nullptr;  // [1] finished router blocks (one-token route), zero between calls
     int32_t *ntiles = nullptr;    // [1]
     int32_t *chunks = nullptr;    // [dispatch_chunks(T) * E] per-chunk expert counts / first rows
-    uint16_t *xh = nullptr;       // [T, H] f16 activations (MFMA path)
+    uint16_t *xhi = nullptr, *xlo = nullptr;  // [T, H] f16 pieces of x (MFMA path)
+    int32_t *xex = nullptr;       // [T] their row exponents
+    uint16_t *hhi = nullptr, *hlo = nullptr;  // [T*k, I] f16 pieces of h (MFMA path)
+    int32_t *hex = nullptr;       // [T*k]
+    uint16_t *hshi = nullptr, *hslo = nullptr;  // [T, I_s] pieces of hs
+    int32_t *hsex = nullptr;      // [T]
     uint8_t *xq = nullptr;        // [batch_t, H/64] activation units (few-tokens path)
     uint8_t *hq = nullptr;        // [batch_t * k, I/64] units of h
     uint8_t *hsq = nullptr;       // [batch_t, I_s/64] units of hs
     int batch_t = 0;              // tokens the unit buffers have room for
-    float *h = nullptr;           // [T*k, I] routed SwiGLU activations (f32, or f16 on the MFMA path)
+    float *h = nullptr;           // [T*k, I] routed SwiGLU activations (f32)
     float *hs = nullptr;          // [T, I_s] shared-expert activations
     float *y = nullptr;           // [parts][T*k, H] routed expert outputs (parts: split K of the down projection)
     float *ys = nullptr;          // [parts][T, H] shared-expert outputs
@@ -108,9 +120,8 @@ struct Workspace {
 // Router logits, bit-exact to the reference's dot (src/quant.rs:386-420):
 // logits[t][e] = W[e] . x[t] for e < n_rows, divided by temp (e < E only)
 // when temp > 0.  Row E (if n_rows == E+1) is the shared-expert gate.
-// When xh is given, also writes x rounded to f16 (the MFMA path's operand).
 hipError_t launch_router(const float *W, const float *x, int T, int n_rows, int E, int H, float temp, float *logits,
-                         uint16_t *xh, hipStream_t s);
+                         hipStream_t s);
 
 // Gating + top-k + weights per token (src/model.rs:855-897).
 hipError_t launch_gating(const float *logits, int ld, int T, const GateParams &p, int32_t *sel, float *wsel,
@@ -153,9 +164,6 @@ hipError_t launch_route_one(const float *W, const float *x, int n_rows, int E, i
 // y = the gates' exp (glibc expf port) over n values; diagnostics.
 hipError_t launch_expf(const float *x, float *y, size_t n, hipStream_t s);
 
-// f32 -> f16 conversion of the activations (MFMA path).
-hipError_t launch_to_f16(const float *x, uint16_t *xh, size_t n, hipStream_t s);
-
 // Decode-path expert GEMVs (fp32, weights dequantised exactly in registers).
 struct GemvArgs {
     const ExpertDev *experts;     // device table [E+1]
@@ -182,7 +190,7 @@ hipError_t launch_gemv_down_combine(const GemvArgs &a, const ExpertDev &host_e0,
 // Exact-order expert GEMVs (bit-identical to the reference's dot).
 hipError_t launch_gemv_exact(bool up, const GemvArgs &a, hipStream_t s);
 
-// One-token experts on integer dot products (two-level int8 activations).
+// One-token experts on integer dot products (three-level int8 activations).
 struct DecodeArgs {
     const DecodeTask *tasks;      // [k_bound + n_shared], written by the dispatch kernel
     const int32_t *hits;          // [E+2]
@@ -203,13 +211,22 @@ hipError_t launch_decode_up(const DecodeArgs &a, const float *x, int dt_routed, 
 // The down projection and combine; every lane encodes its own units of h.
 hipError_t launch_decode_down(const DecodeArgs &a, int dt_routed, int dt_shared, hipStream_t s);
 
-// Prefill-path grouped GEMMs on MFMA (f16 operands, f32 accumulation).
+// Prefill-path grouped GEMMs on MFMA in f32 precision: activations and the
+// dequantised weights are each split into two f16 pieces (hi + lo, exact for
+// d q; 22 significant bits for activations, with a per-row power-of-two scale
+// keeping both pieces in f16's normal range), and hi.hi + hi.lo + lo.hi are
+// accumulated in f32 by V_MFMA_F32_32X32X16_F16.
 struct MfmaArgs {
     const ExpertDev *experts;
     const int32_t *tiles, *ntiles;
     const int32_t *counts, *offsets, *perm_tok;
-    const uint16_t *xh;           // [T, H] f16
-    uint16_t *h, *hs;             // f16 [T*k, I], [T, I_s]
+    const uint16_t *xhi, *xlo;    // [T, H] f16 pieces of x * 2^xex[row]
+    const int32_t *xex;           // [T]
+    float *h, *hs;                // f32 [T*k, I], [T, I_s] (gate/up output)
+    const uint16_t *hhi, *hlo;    // [T*k, I] pieces of h (down input)
+    const int32_t *hex;           // [T*k]
+    const uint16_t *hshi, *hslo;  // [T, I_s] pieces of hs
+    const int32_t *hsex;          // [T]
     float *y, *ys;                // f32 [T*k, H], [T, H]
     size_t ypart, yspart;         // elements between the K parts of y, ys
     int T, H, I, I_s, E;
@@ -217,14 +234,25 @@ struct MfmaArgs {
     int shared_tiles;             // tiles of the shared expert at the end of the tile list (0 if none)
     int ksplit;                   // down projection: K parts (1, 2 or 4), part p written at y + p * ypart
 };
-int mfma_tile_m();
+// Token tile of the MFMA kernels for a layer whose matrices have formats
+// dts[0..n): 160, or 128 when a Q8_0 matrix leaves LDS room for fewer rows.
+int mfma_tile_m(const int *dts, int n);
 bool mfma_format_ok(int dt);
 bool mfma_fits(size_t t, size_t k, size_t H, size_t I, size_t I_s);
 constexpr int kMaxKSplit = 4;
 int mfma_down_ksplit(int m_tiles, int n_rows, int K, int K_shared);
 // up: gate/up + SwiGLU; down: down projection.  Routed tiles come from the
-// dispatch list; the shared expert (sh != null) gets its own launch.
+// dispatch list built with tile `bm`; the shared expert (sh != null) gets its
+// own launch.
 hipError_t launch_mfma(bool up, const MfmaArgs &a, int bm, const ExpertDev &e0, const ExpertDev *sh, hipStream_t s);
+// Rows [rows, cols] of f32 into f16 pieces: hi + lo = v * 2^ex[row] to
+// 22 bits, ex chosen per row so that its largest |v| scales into
+// [2^14, 2^15) (0 for an all-zero or non-finite row).  cols % 4 == 0.
+hipError_t launch_split_rows(const float *src, int rows, int cols, uint16_t *hi, uint16_t *lo, int32_t *ex,
+                             hipStream_t s);
+// Largest |d| (f16 bits) of every block scale of matrix m of expert g into
+// out[3 g + m], for the n experts of the table (F32 matrices give 0).
+hipError_t launch_scale_max(const ExpertDev *experts, int n, unsigned *out, hipStream_t s);
 
 // Weighted combine in ascending expert order + shared expert + residual
 // (src/model.rs:936-942, 956-970, 680-683).

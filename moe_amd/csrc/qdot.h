@@ -1,4 +1,4 @@
-// qdot.h — quantised weight units dotted with two-level int8 activations.
+// qdot.h — quantised weight units dotted with three-level int8 activations.
 //
 // Shared by the one-token kernels and the few-tokens-per-expert kernels: a
 // 64-value unit of a Q4_0 / Q5_0 / Q8_0 weight row (two 32-value blocks) is
@@ -70,61 +70,15 @@ __device__ inline void load_qunit(const uint8_t *p, uint32_t (&x)[kQUnitDw]) {
     }
 }
 
-// Dot of a weight unit with an activation unit.
-//   Q4_0 [dA qA0..15][dB qB0..15]: byte j holds value j (low nibble) and
-//        value j + 16 (high nibble), stored unsigned with offset 8.
-//   Q5_0 [dA hA(4) qA][dB hB qB]: bit j of h is bit 4 of value j, offset 16.
-//   Q8_0 [dA qA0..31][dB qB0..31]: signed bytes.
-// For a block: sum_i d (q_i - o) x_i = d s2 (254 A + B - o sq) with
-// A = sum q hi, B = sum q lo; B starts at -o sq.
+// Dot of a weight unit with an activation unit: qdot_multi for one token.
+template <int DT, int DN, int NT>
+__device__ inline void qdot_multi(const uint32_t (&d)[DN], const uint32_t (&x)[NT][kQUnitDw], float (&out)[NT]);
 template <int DT, int DN>
 __device__ inline float qdot(const uint32_t (&d)[DN], const uint32_t (&x)[kQUnitDw]) {
-    static_assert(DN >= WUnit<DT>::dw, "unit buffer too small");
-    const float s2a = __uint_as_float(x[32]), s2b = __uint_as_float(x[33]);
-    const int sqa = (int)x[34], sqb = (int)x[35];
-    int Aa = 0, Ab = 0, Ba, Bb;
-    float sa, sb;
-    if constexpr (DT == MOE_DT_Q4_0) {
-        sa = h2f(d[0]), sb = h2f(d[4] >> 16);
-        Ba = -8 * sqa, Bb = -8 * sqb;
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const uint32_t qa = alignb(d[i + 1], d[i], 2), qb = d[5 + i];
-            const uint32_t la = qa & 0x0f0f0f0fu, ha = (qa >> 4) & 0x0f0f0f0fu;
-            const uint32_t lb = qb & 0x0f0f0f0fu, hb = (qb >> 4) & 0x0f0f0f0fu;
-            Aa = sdot4(la, x[i], Aa), Aa = sdot4(ha, x[4 + i], Aa);
-            Ba = sdot4(la, x[16 + i], Ba), Ba = sdot4(ha, x[20 + i], Ba);
-            Ab = sdot4(lb, x[8 + i], Ab), Ab = sdot4(hb, x[12 + i], Ab);
-            Bb = sdot4(lb, x[24 + i], Bb), Bb = sdot4(hb, x[28 + i], Bb);
-        }
-    } else if constexpr (DT == MOE_DT_Q5_0) {
-        sa = h2f(d[0]), sb = h2f(d[5] >> 16);
-        Ba = -16 * sqa, Bb = -16 * sqb;
-        const uint32_t hA = alignb(d[1], d[0], 2), hB = d[6];
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const uint32_t qa = alignb(d[i + 2], d[i + 1], 2), qb = d[7 + i];
-            const uint32_t la = (qa & 0x0f0f0f0fu) | spread4((hA >> (4 * i)) & 0xfu);
-            const uint32_t ha = ((qa >> 4) & 0x0f0f0f0fu) | spread4((hA >> (16 + 4 * i)) & 0xfu);
-            const uint32_t lb = (qb & 0x0f0f0f0fu) | spread4((hB >> (4 * i)) & 0xfu);
-            const uint32_t hb = ((qb >> 4) & 0x0f0f0f0fu) | spread4((hB >> (16 + 4 * i)) & 0xfu);
-            Aa = sdot4(la, x[i], Aa), Aa = sdot4(ha, x[4 + i], Aa);
-            Ba = sdot4(la, x[16 + i], Ba), Ba = sdot4(ha, x[20 + i], Ba);
-            Ab = sdot4(lb, x[8 + i], Ab), Ab = sdot4(hb, x[12 + i], Ab);
-            Bb = sdot4(lb, x[24 + i], Bb), Bb = sdot4(hb, x[28 + i], Bb);
-        }
-    } else {
-        sa = h2f(d[0]), sb = h2f(d[8] >> 16);
-        Ba = 0, Bb = 0;
-#pragma unroll
-        for (int i = 0; i < 8; i++) {
-            const uint32_t qa = alignb(d[i + 1], d[i], 2), qb = d[9 + i];
-            Aa = sdot4(qa, x[i], Aa), Ba = sdot4(qa, x[16 + i], Ba);
-            Ab = sdot4(qb, x[8 + i], Ab), Bb = sdot4(qb, x[24 + i], Bb);
-        }
-    }
-    const float fa = (float)(254 * Aa + Ba), fb = (float)(254 * Ab + Bb);
-    return fmaf(sb * s2b, fb, (sa * s2a) * fa);
+    const uint32_t(&xs)[1][kQUnitDw] = reinterpret_cast<const uint32_t(&)[1][kQUnitDw]>(x);
+    float r[1];
+    qdot_multi<DT, DN, 1>(d, xs, r);
+    return r[0];
 }
 
 // Sum over groups of CG consecutive lanes (CG = 16, 32, 64); every lane of
@@ -162,18 +116,41 @@ __device__ inline int lanes_for(int units) { return units <= 16 ? 16 : units <= 
 
 // A weight unit dotted with the activation units of NT tokens: out[t] for
 // every t (the weights are unpacked once for all of them; callers pad with
-// all-zero units, whose dots are zero).  Same arithmetic as qdot per token.
+// all-zero units, whose dots are zero).
+//   Q4_0 [dA qA0..15][dB qB0..15]: byte j holds value j (low nibble) and
+//        value j + 16 (high nibble), stored unsigned with offset 8.
+//   Q5_0 [dA hA(4) qA][dB hB qB]: bit j of h is bit 4 of value j, offset 16.
+//   Q8_0 [dA qA0..31][dB qB0..31]: signed bytes.
+// For a block with codes c_i = q_i + o: sum_i d q_i x_i =
+// d s3 (254 (254 A + B) + C) with A = sum c a0, B = sum c a1 - o q01 and
+// C = sum c a2 - o q2 (the offset folded into the finer levels' starting
+// values).  Every sum is an exact int32 (|254 A + B| < 2^31); the two
+// conversions and the fma round as f32 arithmetic does.
 template <int DT, int DN, int NT>
 __device__ inline void qdot_multi(const uint32_t (&d)[DN], const uint32_t (&x)[NT][kQUnitDw], float (&out)[NT]) {
     static_assert(DN >= WUnit<DT>::dw, "unit buffer too small");
-    int Aa[NT], Ab[NT], Ba[NT], Bb[NT];
+    int A[NT][2], B[NT][2], Cs[NT][2];
     float sa, sb;
     constexpr int off = DT == MOE_DT_Q4_0 ? 8 : DT == MOE_DT_Q5_0 ? 16 : 0;
 #pragma unroll
-    for (int t = 0; t < NT; t++) {
-        Aa[t] = 0, Ab[t] = 0;
-        Ba[t] = -off * (int)x[t][34], Bb[t] = -off * (int)x[t][35];
-    }
+    for (int t = 0; t < NT; t++)
+#pragma unroll
+        for (int b = 0; b < 2; b++) {
+            A[t][b] = 0;
+            B[t][b] = -off * (int)x[t][kQ01 + b];
+            Cs[t][b] = -off * (int)x[t][kQ2 + b];
+        }
+    // Codes dword c of block b (four consecutive values starting at value
+    // 4 (c % 4) + 16 (c / 4) for nibble formats, 4 c for Q8_0) against the
+    // matching dword of every level.
+    auto dot3 = [&](uint32_t c, int b, int dw) {
+#pragma unroll
+        for (int t = 0; t < NT; t++) {
+            A[t][b] = sdot4(c, x[t][8 * b + dw], A[t][b]);
+            B[t][b] = sdot4(c, x[t][kQA1 + 8 * b + dw], B[t][b]);
+            Cs[t][b] = sdot4(c, x[t][kQA2 + 8 * b + dw], Cs[t][b]);
+        }
+    };
     if constexpr (DT == MOE_DT_Q4_0 || DT == MOE_DT_Q5_0) {
         constexpr bool q5 = DT == MOE_DT_Q5_0;
         sa = h2f(d[0]), sb = h2f(d[q5 ? 5 : 4] >> 16);
@@ -188,31 +165,23 @@ __device__ inline void qdot_multi(const uint32_t (&d)[DN], const uint32_t (&x)[N
                 la |= spread4((hA >> (4 * i)) & 0xfu), ha |= spread4((hA >> (16 + 4 * i)) & 0xfu);
                 lb |= spread4((hB >> (4 * i)) & 0xfu), hb |= spread4((hB >> (16 + 4 * i)) & 0xfu);
             }
-#pragma unroll
-            for (int t = 0; t < NT; t++) {
-                Aa[t] = sdot4(la, x[t][i], Aa[t]), Aa[t] = sdot4(ha, x[t][4 + i], Aa[t]);
-                Ba[t] = sdot4(la, x[t][16 + i], Ba[t]), Ba[t] = sdot4(ha, x[t][20 + i], Ba[t]);
-                Ab[t] = sdot4(lb, x[t][8 + i], Ab[t]), Ab[t] = sdot4(hb, x[t][12 + i], Ab[t]);
-                Bb[t] = sdot4(lb, x[t][24 + i], Bb[t]), Bb[t] = sdot4(hb, x[t][28 + i], Bb[t]);
-            }
+            dot3(la, 0, i), dot3(ha, 0, 4 + i);
+            dot3(lb, 1, i), dot3(hb, 1, 4 + i);
         }
     } else {
         sa = h2f(d[0]), sb = h2f(d[8] >> 16);
 #pragma unroll
         for (int i = 0; i < 8; i++) {
-            const uint32_t qa = alignb(d[i + 1], d[i], 2), qb = d[9 + i];
-#pragma unroll
-            for (int t = 0; t < NT; t++) {
-                Aa[t] = sdot4(qa, x[t][i], Aa[t]), Ba[t] = sdot4(qa, x[t][16 + i], Ba[t]);
-                Ab[t] = sdot4(qb, x[t][8 + i], Ab[t]), Bb[t] = sdot4(qb, x[t][24 + i], Bb[t]);
-            }
+            dot3(alignb(d[i + 1], d[i], 2), 0, i);
+            dot3(d[9 + i], 1, i);
         }
     }
 #pragma unroll
     for (int t = 0; t < NT; t++) {
-        const float fa = (float)(254 * Aa[t] + Ba[t]), fb = (float)(254 * Ab[t] + Bb[t]);
-        const float s2a = __uint_as_float(x[t][32]), s2b = __uint_as_float(x[t][33]);
-        out[t] = fmaf(sb * s2b, fb, (sa * s2a) * fa);
+        const float fa = fmaf((float)(254 * A[t][0] + B[t][0]), 254.0f, (float)Cs[t][0]);
+        const float fb = fmaf((float)(254 * A[t][1] + B[t][1]), 254.0f, (float)Cs[t][1]);
+        const float s3a = __uint_as_float(x[t][kQS]), s3b = __uint_as_float(x[t][kQS + 1]);
+        out[t] = fmaf(sb * s3b, fb, (sa * s3a) * fa);
     }
 }
 

@@ -116,11 +116,9 @@ __host__ __device__ inline int router_lds_stride(int H) { return (H % 64 == 0) ?
 // Latency-bound router: a block stages RB router rows and TB token rows in
 // LDS (the whole of H), then thread (pair, j) runs lane j of dot_avx2 for one
 // (row, token) pair — one chain per thread, read eight steps at a time.
-// Blocks of the first row range also write the tokens' f16 copy (xh, the
-// MFMA path's activations) from LDS when xh is given.
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 2))) void router_lds_kernel(const float *__restrict__ W, const float *__restrict__ x,
                                                          int T, int n_rows, int E, int H, int RB, int TB, float temp,
-                                                         float *__restrict__ logits, __half *__restrict__ xh) {
+                                                         float *__restrict__ logits) {
     extern __shared__ __attribute__((aligned(16))) float lds[];
     const int r0 = blockIdx.x * RB, t0 = blockIdx.y * TB;
     const int nr = min(RB, n_rows - r0), nt = min(TB, T - t0);
@@ -138,26 +136,6 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 2))) voi
     }
     __syncthreads();
     const int tid = threadIdx.x, j = tid & 15, p = tid >> 4;
-    if (xh && blockIdx.x == 0) {
-        if ((H & 7) == 0) {
-            // Eight values per 16-byte store.
-            const int H8 = H >> 3;
-            for (int i = tid; i < nt * H8; i += blockDim.x) {
-                const int r = i / H8, c = (i % H8) * 8;
-                const float *src = xl + (size_t)r * LS + c;
-                uint4 v;
-                uint32_t *vw = reinterpret_cast<uint32_t *>(&v);
-#pragma unroll
-                for (int q = 0; q < 4; q++)
-                    vw[q] = (uint32_t)__half_as_ushort(__float2half_rn(src[2 * q])) |
-                            ((uint32_t)__half_as_ushort(__float2half_rn(src[2 * q + 1])) << 16);
-                *reinterpret_cast<uint4 *>(xh + (size_t)(t0 + r) * H + c) = v;
-            }
-        } else {
-            for (int i = tid; i < nt * H; i += blockDim.x)
-                xh[(size_t)t0 * H + i] = __float2half_rn(xl[(size_t)(i / H) * LS + i % H]);
-        }
-    }
     if (p >= nr * nt) return;  // whole 16-lane groups leave together
     const int rl = p / nt, tl = p % nt;
     const float *a = wl + (size_t)rl * LS;
@@ -197,7 +175,7 @@ constexpr int kKC = 64;   // K chunk
 template <int TPT>
 __global__ __launch_bounds__(256) void router_tiled_kernel(const float *__restrict__ W, const float *__restrict__ x,
                                                            int T, int n_rows, int E, int H, float temp,
-                                                           float *__restrict__ logits, __half *__restrict__ xh) {
+                                                           float *__restrict__ logits) {
     // A chunk row holds its 64 values transposed, value 16 s + j at 4 j + s,
     // so that chain lane j reads its four values of the chunk (s = 0..3) with
     // one 16-byte read; eight lanes then read 128 contiguous bytes.
@@ -253,15 +231,6 @@ __global__ __launch_bounds__(256) void router_tiled_kernel(const float *__restri
                 float *xr = &xt[rr][0];
                 xr[4 * (j0 + 0) + s0] = px[u].x, xr[4 * (j0 + 1) + s0] = px[u].y;
                 xr[4 * (j0 + 2) + s0] = px[u].z, xr[4 * (j0 + 3) + s0] = px[u].w;
-            }
-            // The first row range writes the f16 copy (launched only when
-            // the chunks cover all of H, i.e. H % 16 == 0).
-            if (xh && blockIdx.x == 0 && rr < kTTv && t0 + rr < T && k0 + kk < kfull) {
-                __half *o = xh + (size_t)(t0 + rr) * H + k0 + kk;
-                o[0] = __float2half_rn(px[u].x);
-                o[1] = __float2half_rn(px[u].y);
-                o[2] = __float2half_rn(px[u].z);
-                o[3] = __float2half_rn(px[u].w);
             }
         }
         __syncthreads();
@@ -519,11 +488,11 @@ __device__ void gate_token(const float *__restrict__ lg, int t, const GateParams
             }
         }
     }
-    if (p.disabled) {
+    if (p.any_disabled) {
 #pragma unroll
         for (int i = 0; i < EPL; i++) {
             const int e = lane * EPL + i;
-            if (e < E && p.disabled[e]) rank[i] = -INFINITY;
+            if (e < E && ((p.disabled[e >> 5] >> (e & 31)) & 1u)) rank[i] = -INFINITY;
         }
     }
     wave_sync();
@@ -1103,17 +1072,10 @@ __global__ void expf_kernel(const float *__restrict__ x, float *__restrict__ y, 
     for (; i < n; i += stride) y[i] = expf_exact(x[i]);
 }
 
-__global__ void to_f16_kernel(const float *__restrict__ x, __half *__restrict__ xh, size_t n) {
-    size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
-    size_t stride = (size_t)gridDim.x * blockDim.x;
-    for (; i < n; i += stride) xh[i] = __float2half_rn(x[i]);
-}
-
 }  // namespace
 
 hipError_t launch_router(const float *W, const float *x, int T, int n_rows, int E, int H, float temp, float *logits,
-                         uint16_t *xh_raw, hipStream_t s) {
-    __half *xh = reinterpret_cast<__half *>(xh_raw);
+                         hipStream_t s) {
     const double budget = 160.0 * 1024;
     const double clk_us = 2400.0;  // cycles per microsecond
     // Cost model (microseconds) of the row-staging kernel for an RB x TB
@@ -1151,22 +1113,15 @@ hipError_t launch_router(const float *W, const float *x, int T, int n_rows, int 
                                       160 * 1024);
             raised = true;
         }
-        hipLaunchKernelGGL(router_lds_kernel, grid, dim3(256), lds, s, W, x, T, n_rows, E, H, RB, TB, temp, logits,
-                           xh);
+        hipLaunchKernelGGL(router_lds_kernel, grid, dim3(256), lds, s, W, x, T, n_rows, E, H, RB, TB, temp, logits);
     } else {
         dim3 grid((n_rows + kRT - 1) / kRT, (T + 4 * tpt - 1) / (4 * tpt));
-        __half *xo = (H % 16 == 0) ? xh : nullptr;
         if (tpt == 8)
-            hipLaunchKernelGGL(router_tiled_kernel<8>, grid, dim3(256), 0, s, W, x, T, n_rows, E, H, temp, logits, xo);
+            hipLaunchKernelGGL(router_tiled_kernel<8>, grid, dim3(256), 0, s, W, x, T, n_rows, E, H, temp, logits);
         else if (tpt == 4)
-            hipLaunchKernelGGL(router_tiled_kernel<4>, grid, dim3(256), 0, s, W, x, T, n_rows, E, H, temp, logits, xo);
+            hipLaunchKernelGGL(router_tiled_kernel<4>, grid, dim3(256), 0, s, W, x, T, n_rows, E, H, temp, logits);
         else
-            hipLaunchKernelGGL(router_tiled_kernel<2>, grid, dim3(256), 0, s, W, x, T, n_rows, E, H, temp, logits, xo);
-        if (xh && H % 16 != 0) {
-            hipError_t e = hipGetLastError();
-            if (e != hipSuccess) return e;
-            return launch_to_f16(x, xh_raw, (size_t)T * H, s);
-        }
+            hipLaunchKernelGGL(router_tiled_kernel<2>, grid, dim3(256), 0, s, W, x, T, n_rows, E, H, temp, logits);
     }
     return hipGetLastError();
 }
@@ -1221,14 +1176,6 @@ hipError_t launch_expf(const float *x, float *y, size_t n, hipStream_t s) {
     if (blocks > 8192) blocks = 8192;
     if (blocks < 1) blocks = 1;
     hipLaunchKernelGGL(expf_kernel, dim3((unsigned)blocks), dim3(256), 0, s, x, y, n);
-    return hipGetLastError();
-}
-
-hipError_t launch_to_f16(const float *x, uint16_t *xh, size_t n, hipStream_t s) {
-    size_t blocks = (n + 255) / 256;
-    if (blocks > 4096) blocks = 4096;
-    if (blocks < 1) blocks = 1;
-    hipLaunchKernelGGL(to_f16_kernel, dim3((unsigned)blocks), dim3(256), 0, s, x, reinterpret_cast<__half *>(xh), n);
     return hipGetLastError();
 }
 

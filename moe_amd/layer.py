@@ -313,19 +313,39 @@ class MoeLayer:
     def set_mode(self, mode: int) -> None:
         L.check(L.lib().moe_layer_set_mode(self.handle, mode), "moe_layer_set_mode")
 
-    def reserve(self, max_t: int) -> None:
-        L.check(L.lib().moe_layer_reserve(self.handle, max_t), "moe_layer_reserve")
+    def reserve(self, max_t: int, stream=None) -> None:
+        """Allocate the workspace for `stream` up front (no later call on it
+        allocates; calls beyond max_t tokens fail)."""
+        L.check(L.lib().moe_layer_reserve_stream(self.handle, max_t, C.c_void_p(_stream_ptr(stream))),
+                "moe_layer_reserve_stream")
+
+    def workspace_size(self, max_t: int) -> int:
+        """Bytes of a caller-owned workspace for up to max_t tokens."""
+        n = C.c_uint64()
+        L.check(L.lib().moe_layer_workspace_size(self.handle, max_t, C.byref(n)), "moe_layer_workspace_size")
+        return int(n.value)
+
+    @staticmethod
+    def new_workspace(nbytes: int, device="cuda"):
+        """A zero-filled, 256-byte-aligned device buffer of at least nbytes
+        for feed_forward(workspace=...)."""
+        buf = torch.zeros(nbytes + 256, dtype=torch.uint8, device=device)
+        off = (-buf.data_ptr()) % 256
+        return buf[off:off + nbytes]
 
     @property
     def k(self) -> int:
         return int(L.lib().moe_layer_k(self.handle))
 
     # -- the forward -------------------------------------------------------
-    def feed_forward(self, x, out, state: Optional[State] = None, residual=None, routes=None, stream=None):
+    def feed_forward(self, x, out, state: Optional[State] = None, residual=None, routes=None, stream=None,
+                     workspace=None):
         """out = the routed layer over x ([t, H] f32 CUDA tensors); residual
         += out when given.  With a State: its prev selection drives the reuse
         counter and is replaced by this call's, its stats accumulate, and
-        with tracing on the routes are appended (src/model.rs:943-954)."""
+        with tracing on the routes are appended (src/model.rs:943-954).
+        With `workspace` (a device buffer from new_workspace) the call runs
+        on it and allocates nothing (moe_layer_forward_ws)."""
         t = int(x.shape[0])
         self._check_io(x, out, residual)
         k = self.k
@@ -337,15 +357,19 @@ class MoeLayer:
             hits = torch.empty(self.spec.n_experts + 1, dtype=torch.int32, device=x.device)
             prev = state.prev[self.li]
             stats = state.stats_dev
-        rc = L.lib().moe_layer_forward(
-            self.handle, C.c_void_p(x.data_ptr()), t, C.c_void_p(out.data_ptr()),
-            C.c_void_p(residual.data_ptr() if residual is not None else None),
-            C.c_void_p(routes.data_ptr() if routes is not None else None),
-            C.c_void_p(hits.data_ptr() if hits is not None else None),
-            C.c_void_p(prev.data_ptr() if prev is not None else None),
-            C.c_void_p(stats.data_ptr() if stats is not None else None),
-            C.c_void_p(_stream_ptr(stream)))
-        L.check(rc, "moe_layer_forward")
+        args = (self.handle, C.c_void_p(x.data_ptr()), t, C.c_void_p(out.data_ptr()),
+                C.c_void_p(residual.data_ptr() if residual is not None else None),
+                C.c_void_p(routes.data_ptr() if routes is not None else None),
+                C.c_void_p(hits.data_ptr() if hits is not None else None),
+                C.c_void_p(prev.data_ptr() if prev is not None else None),
+                C.c_void_p(stats.data_ptr() if stats is not None else None))
+        if workspace is None:
+            rc = L.lib().moe_layer_forward(*args, C.c_void_p(_stream_ptr(stream)))
+            L.check(rc, "moe_layer_forward")
+        else:
+            rc = L.lib().moe_layer_forward_ws(*args, C.c_void_p(workspace.data_ptr()), workspace.numel(),
+                                              C.c_void_p(_stream_ptr(stream)))
+            L.check(rc, "moe_layer_forward_ws")
         if state is not None:
             state.prev[self.li] = hits
             if state.trace is not None:

@@ -90,6 +90,12 @@ SHAPES = {
                      shared_dt=L.DT_Q8_0),
     # configs[0]'s MoE layer: tiny Mixtral, hidden 512, 8 experts top-2, Q8_0.
     "tiny_mixtral": Shape("tiny_mixtral", 512, 1408, 8, 2, L.DT_Q8_0),
+    # A Qwen2-MoE layer (Qwen1.5-MoE-A2.7B: 60 experts of 1408, top-4, not
+    # renormalised, one 5632-wide shared expert scaled by the sigmoid of
+    # mlp.shared_expert_gate.weight . x, src/model.rs:956-970), Q8_0: the
+    # layer family whose shared expert carries a gate.
+    "qwen2_moe": Shape("qwen2_moe", 2048, 1408, 60, 4, L.DT_Q8_0, norm_topk=False, shared_inter=5632,
+                       shared_dt=L.DT_Q8_0, shared_gate=True),
 }
 
 

@@ -1,12 +1,35 @@
 """Shared helpers for the GPU parity tests."""
 from __future__ import annotations
 
+import json
+import os
 import sys
 import time
 
 import numpy as np
 
-TOL = 1e-3  # max |gpu - ref| / max |ref| per output tensor (fp32 accumulation)
+# Bar of every output comparison: max |gpu - ref| / max |ref| per output
+# tensor.  BASELINE.json's north_star asks for 1e-3 with f32 accumulation;
+# every kernel path computes in f32 precision (f32 GEMV, three-level int8
+# activations with exact integer dots, two-piece f16 MFMA operands with f32
+# accumulation), and the committed error table (profiles/parity_errors.md)
+# shows the measured errors lie below 1e-5 on every case, so the tests hold
+# them to that.
+TOL = 1e-5
+
+# Where the per-case errors go (one JSON object per line), for the table.
+ERR_LOG = os.environ.get("MOE_PARITY_LOG", os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))),
+                                                         "gpurun_out", "parity_errors.jsonl"))
+
+
+def record(test: str, case: str, err: float, **extra) -> None:
+    """Append one measured error to ERR_LOG (best effort)."""
+    try:
+        os.makedirs(os.path.dirname(ERR_LOG), exist_ok=True)
+        with open(ERR_LOG, "a") as f:
+            f.write(json.dumps(dict(test=test, case=case, err=err, **extra)) + "\n")
+    except OSError:
+        pass
 
 
 def log(msg: str) -> None:

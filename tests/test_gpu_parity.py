@@ -2,13 +2,15 @@
 
 Bar: selected experts and their order bit-exact,
 routing weights bit-exact (the gating is exact by construction), layer output
-within max|gpu - ref| / max|ref| <= 1e-3 with fp32 accumulation; the exact
-kernel path bit-identical.
+within max|gpu - ref| / max|ref| <= 1e-3 with fp32 accumulation — held here
+to TOL = 1e-5, since every path computes in f32 precision; the exact kernel
+path bit-identical.  Every measured error is appended to the parity log
+(gpu_util.ERR_LOG) for the committed error table.
 """
 import numpy as np
 import pytest
 
-from gpu_util import TOL, assert_routing_equal, log, rel_err, run_gpu
+from gpu_util import TOL, assert_routing_equal, log, record, rel_err, run_gpu
 
 pytestmark = pytest.mark.gpu
 
@@ -99,6 +101,9 @@ def test_routing_bit_exact(ctx, oracle, name, t):
         f"router logits differ in {(g_logits != logits).sum()} of {logits.size}")
     assert_routing_equal(dict(sel=gsel.cpu().numpy(), w=gw.cpu().numpy()), sel, w, f"{name} T={t}")
     log(f"{name} T={t}: routing bit-exact ({ties} tie tokens)")
+    # Exact rank ties in the selected prefix are the one case the reference
+    # leaves unspecified for E > 20; the seeded inputs must not meet one.
+    assert ties == 0, f"{name} T={t}: {ties} tokens with an exact rank tie in the selected prefix"
 
 
 LAYER_CASES = [
@@ -116,6 +121,12 @@ LAYER_CASES = [
     ("v2_lite", 5, 5), ("deepseek_v3", 8, 5), ("deepseek_v3", 37, 5),
     # MFMA at few tokens per expert, where the automatic choice is the few-tokens path
     ("mixtral", 32, 3), ("v2_lite", 32, 3), ("deepseek_v3", 64, 3),
+    # MFMA with 128-token tiles (Q8_0) across tile boundaries, GEMV at many tokens
+    ("qwen3", 300, 3), ("tiny_mixtral", 257, 3), ("qwen3", 128, 2),
+    # Qwen2-MoE: the shared expert's sigmoid gate on every path (decode takes
+    # the GEMV here: its 5632-wide shared rows need two units per lane)
+    ("qwen2_moe", 1, None), ("qwen2_moe", 1, 2), ("qwen2_moe", 6, 5), ("qwen2_moe", 64, None),
+    ("qwen2_moe", 64, 3), ("qwen2_moe", 17, 2), ("qwen2_moe", 512, None),
 ]
 
 
@@ -135,39 +146,34 @@ def test_layer_parity(ctx, oracle, name, t, mode):
     assert np.isfinite(g["out"]).all()
     err = rel_err(g["out"], out)
     log(f"{name} T={t} mode={mode}: max rel err {err:.2e}")
+    record("layer", f"{name} T={t} mode={mode if mode is not None else 'auto'}", err)
     assert err <= TOL, f"{name} T={t}: max rel err {err:.3e} > {TOL}"
 
 
 @pytest.mark.parametrize("name,t", [("deepseek_v3_zipf", 4096), ("v2_lite", 8192)])
-def test_layer_parity_sampled(ctx, oracle, name, t):
+def test_layer_parity_full_size(ctx, oracle, name, t):
     """A full-size prefill (DeepSeek-V3 with Zipf-skewed popularity: the top
     expert takes about half of the tokens, many experts none; V2-Lite at 32
-    sequences x 256 tokens): routing, hits and counters for every token against the CPU
-    path, and output rows within 1e-3 of it on a sample of tokens (each row
-    depends on its own token only) that includes the most popular expert's."""
+    sequences x 256 tokens): routing, hits and counters for every token, and
+    every output row, against the CPU path."""
     from moe_amd import synth
 
     host, gl, ol = layer_pair(ctx, oracle, name)
     x = synth.activations(SEED, t, host.shape.hidden)
-    sel, w, _, _ = ol.route(x)
+    log(f"{name} T={t}: CPU path")
+    out, sel, w, hits, stats = ol.forward(x)
+    log(f"{name} T={t}: GPU")
     g = run_gpu(gl, x)
     assert_routing_equal(g, sel, w, f"{name} T={t}")
+    assert np.array_equal(g["hits"][:hits[0] + 1], hits[:hits[0] + 1]), "hit lists differ"
+    assert np.array_equal(g["stats"][:3], stats[:3]), f"counters gpu {g['stats']} ref {stats}"
     counts = np.bincount(sel.ravel(), minlength=host.shape.n_experts)
-    hits = np.flatnonzero(counts)
-    assert g["hits"][0] == hits.size and np.array_equal(g["hits"][1:1 + hits.size], hits)
-    assert g["stats"][0] == t * gl.k
-    assert g["stats"][2] == hits.size * host.shape.expert_bytes()
     top = int(np.argmax(counts))
-    rng = np.random.default_rng(0)
-    idx = np.unique(np.concatenate([np.flatnonzero((sel == top).any(1))[:16], rng.choice(t, 32, replace=False)]))
-    ref = ol.forward(np.ascontiguousarray(x[idx]))[0]
-    err = rel_err(g["out"][idx], ref)
-    log(f"{name} T={t}: top expert {top} has {counts[top]} tokens, {hits.size} experts hit; "
-        f"{idx.size} sampled rows max rel err {err:.2e}")
+    err = rel_err(g["out"], out)
+    log(f"{name} T={t}: top expert {top} has {counts[top]} tokens, {hits[0]} experts hit; "
+        f"all {t} rows max rel err {err:.2e}")
+    record("layer_full", f"{name} T={t}", err)
     assert err <= TOL
-
-
-DECODE_TOL = 1e-4  # one-token kernels: 2^-16 activation steps, exact integer dots
 
 
 @pytest.mark.parametrize("name,scale", [
@@ -176,11 +182,12 @@ DECODE_TOL = 1e-4  # one-token kernels: 2^-16 activation steps, exact integer do
     ("v2_lite", dict(hidden=1024, inter=256, shared_inter=512)),
     ("mixtral", dict(hidden=1024, inter=5120)),   # down rows of 80 units: two per lane
     ("qwen3", dict(hidden=6144, inter=512)),      # gate/up rows of 96 units: two per lane
+    ("qwen2_moe", dict(shared_inter=2816)),       # the shared expert's sigmoid gate on the one-token kernels
 ])
 def test_decode_repeated_calls(ctx, oracle, name, scale):
     """The one-token kernels over several tokens in a row: each call's output
-    within DECODE_TOL of the CPU path, so the per-range counters the down
-    kernel uses return to zero after every call."""
+    within TOL of the CPU path, so nothing one call leaves behind (the route
+    kernel's block counter) disturbs the next."""
     from moe_amd import synth
 
     host, gl, ol = layer_pair(ctx, oracle, name, **scale)
@@ -193,9 +200,10 @@ def test_decode_repeated_calls(ctx, oracle, name, scale):
         assert_routing_equal(g, sel, w, f"{name} call {i}")
         err = rel_err(g["out"], out)
         worst = max(worst, err)
-        assert err <= DECODE_TOL, f"{name} call {i}: max rel err {err:.3e}"
+        assert err <= TOL, f"{name} call {i}: max rel err {err:.3e}"
     gl.set_mode(0)
     log(f"{name} {scale or ''} one-token x3: max rel err {worst:.2e}")
+    record("decode", f"{name} {scale or 'full size'} x3", worst)
 
 
 @pytest.mark.parametrize("kind", ["disabled", "forced", "top1", "topE", "forced2"])
@@ -220,7 +228,7 @@ def test_decode_interventions(ctx, oracle, kind):
         gl.set_routing(None)
         gl.set_mode(0)
     assert_routing_equal(g, sel, w, kind)
-    assert rel_err(g["out"], out) <= DECODE_TOL
+    assert rel_err(g["out"], out) <= TOL
 
 
 @pytest.mark.parametrize("name,t", [("tiny_mixtral", 1), ("tiny_mixtral", 16), ("tiny_mixtral", 5)])
@@ -236,6 +244,20 @@ def test_exact_path_bit_identical(ctx, oracle, name, t):
     assert_routing_equal(g, sel, w, f"{name} T={t}")
     bad = g["out"].view(np.uint32) != out.view(np.uint32)
     assert not bad.any(), f"{bad.sum()} output values differ; max rel err {rel_err(g['out'], out):.2e}"
+
+
+def test_exact_path_bit_identical_shared_gate(ctx, oracle):
+    """Exact path with the shared expert's sigmoid gate (Qwen2-MoE routing
+    at reduced width): bit-identical to the CPU path."""
+    from moe_amd import synth
+
+    host, gl, ol = layer_pair(ctx, oracle, "qwen2_moe", hidden=512, inter=128, shared_inter=256)
+    x = synth.activations(SEED, 7, 512)
+    out, sel, w, hits, stats = ol.forward(x)
+    g = run_gpu(gl, x, mode=1)
+    gl.set_mode(0)
+    assert_routing_equal(g, sel, w, "qwen2_moe reduced")
+    assert np.array_equal(g["out"].view(np.uint32), out.view(np.uint32))
 
 
 def test_exact_path_bit_identical_shared_and_groups(ctx, oracle):
@@ -338,3 +360,113 @@ def test_trace_file_from_gpu_routes(ctx, oracle, tmp_path):
     assert c.tokens == 13 and c.experts == 8 and c.top_k == 2
     for e in range(8):
         assert c.count(0, e) == sum(sel.count(e) for _, sel, _ in want)
+
+
+# ---------------------------------------------------------------- boundary
+# The C ABI is reentrant per stream: moe_layer_forward keeps a workspace per
+# stream, moe_layer_forward_ws runs on the caller's.  The reference's
+# Model::feed_forward takes &self with one State per sequence
+# (src/model.rs:836), so several sequences may run the same layer at once.
+
+
+def _forward_async(gl, x, stream, workspace=None):
+    import torch
+
+    with torch.cuda.stream(stream):
+        xd = torch.from_numpy(x).to("cuda:0", non_blocking=False)
+        out = torch.full_like(xd, float("nan"))
+        routes = gl.feed_forward(xd, out, routes=torch.empty((x.shape[0], gl.k, 2), dtype=torch.int32,
+                                                               device="cuda:0"), stream=stream, workspace=workspace)
+    return out, routes
+
+
+@pytest.mark.parametrize("use_ws", [False, True])
+def test_two_streams_one_layer(ctx, oracle, use_ws):
+    """Two streams run the same layer at once (MFMA-sized and one-token
+    calls interleaved, nothing synchronised in between): each output equals
+    the CPU path's for its own input."""
+    import torch
+
+    from moe_amd import synth
+
+    host, gl, ol = layer_pair(ctx, oracle, "qwen3")
+    streams = [torch.cuda.Stream(), torch.cuda.Stream()]
+    xs = [synth.activations(SEED + 60 + i, t, host.shape.hidden) for i, t in enumerate([300, 1, 200, 1])]
+    wss = [None, None]
+    if use_ws:
+        wss = [gl.new_workspace(gl.workspace_size(300)) for _ in streams]
+    torch.cuda.synchronize()
+    outs = []
+    for i, x in enumerate(xs):
+        outs.append(_forward_async(gl, x, streams[i % 2], wss[i % 2]))
+    torch.cuda.synchronize()
+    for i, (x, (out, routes)) in enumerate(zip(xs, outs)):
+        ref, sel, w, _, _ = ol.forward(x)
+        r = routes.cpu().numpy()
+        assert_routing_equal(dict(sel=r[..., 0], w=r[..., 1].view(np.float32)), sel, w, f"call {i}")
+        err = rel_err(out.cpu().numpy(), ref)
+        record("streams", f"qwen3 T={x.shape[0]} stream {i % 2} ws={use_ws}", err)
+        assert err <= TOL, f"call {i}: max rel err {err:.2e}"
+
+
+def test_routing_change_between_queued_calls(ctx, oracle):
+    """set_routing between two calls queued on one stream: the first call
+    keeps the routing it was made with (interventions travel by value)."""
+    import torch
+
+    from moe_amd import synth
+    from moe_amd.layer import Routing
+
+    host, gl, ol = layer_pair(ctx, oracle, "tiny_mixtral")
+    x = synth.activations(SEED + 70, 24, 512)
+    base_sel, *_ = ol.route(x)
+    victim = int(base_sel[0, 0])
+    s = torch.cuda.Stream()
+    # A long call first keeps the stream busy while the routing changes.
+    big = synth.activations(SEED + 71, 2048, 512)
+    torch.cuda.synchronize()
+    try:
+        _forward_async(gl, big, s)
+        o1, r1 = _forward_async(gl, x, s)
+        gl.set_routing(Routing(disabled=[(0, victim)], top_k=1))
+        o2, r2 = _forward_async(gl, x, s)
+        torch.cuda.synchronize()
+    finally:
+        gl.set_routing(None)
+    ref1, sel1, w1, _, _ = ol.forward(x)
+    ref2, sel2, w2, _, _ = ol.forward(x, oracle.OracleLayer.routing(disabled=[victim], top_k=1))
+    a1, a2 = r1.cpu().numpy(), r2.cpu().numpy()
+    assert_routing_equal(dict(sel=a1[..., 0], w=a1[..., 1].view(np.float32)), sel1, w1, "before")
+    assert_routing_equal(dict(sel=a2[..., 0], w=a2[..., 1].view(np.float32)), sel2, w2, "after")
+    assert rel_err(o1.cpu().numpy(), ref1) <= TOL and rel_err(o2.cpu().numpy(), ref2) <= TOL
+
+
+def test_reservation_is_a_limit(ctx, oracle):
+    """After moe_layer_reserve the layer allocates nothing more: a call with
+    more tokens than reserved fails cleanly (MOE_EINVAL) instead of growing,
+    and calls within the reservation still run."""
+    import torch
+
+    from moe_amd import _lib as L
+    from moe_amd import synth
+
+    host = synth.build_host_layer(synth.SHAPES["tiny_mixtral"], SEED)
+    gl = synth.make_layer(ctx, host)
+    ol = oracle.from_host_layer(host)
+    try:
+        gl.reserve(8)
+        x = synth.activations(SEED, 16, 512)
+        xd = torch.from_numpy(x).cuda()
+        out = torch.empty_like(xd)
+        with pytest.raises(L.MoeError) as ei:
+            gl.feed_forward(xd, out)
+        assert ei.value.code == L.MOE_EINVAL and "reservation" in str(ei.value)
+        small = np.ascontiguousarray(x[:8])
+        g = run_gpu(gl, small)
+        assert rel_err(g["out"], ol.forward(small)[0]) <= TOL
+        # A workspace too small for the call is refused the same way.
+        ws = gl.new_workspace(gl.workspace_size(4))
+        with pytest.raises(L.MoeError):
+            gl.feed_forward(xd[:8], out[:8], workspace=ws)
+    finally:
+        gl.close()

@@ -226,3 +226,52 @@ def test_mlp_is_swiglu_of_the_matmuls(oracle):
     # A plausible mistake, g * (1 / (1 + e)), rounds differently.
     h2 = (g * (np.float32(1.0) / (np.float32(1.0) + e))).astype(np.float32) * u
     assert not np.array_equal(oracle.matmul(qts["down"], h2).view(np.uint32), got.view(np.uint32))
+
+
+def test_shared_expert_gate_closed_form(oracle):
+    """The shared expert's sigmoid gate (src/model.rs:956-970): the layer's
+    output is the routed sum plus s * Mlp_shared(x), s = 1 / (1 + exp(-g)),
+    g = shared_gate . x, applied after the routed sum and not scaled by
+    routed_scale.  A zero gate row gives s = 1/2 exactly; a general row is
+    composed from the pinned matmul, MLP and expf bit for bit.  Plausible
+    mistakes — no gate, the gate on the routed sum too, routed_scale on the
+    shared expert, or sigmoid(g) written as exp(g) / (1 + exp(g)) — each
+    break the equality."""
+    from moe_amd import synth
+
+    H, I, Is, t = 64, 32, 48, 6
+    rng = np.random.default_rng(17)
+
+    def mats(r_i):
+        return [(rng.standard_normal(s) * 0.2).astype(np.float32) for s in ((r_i, H), (r_i, H), (H, r_i))]
+
+    routed = mats(I)
+    shared = mats(Is)
+    as_qt = lambda ws: [(F32, a.shape[0], a.shape[1], a.view(np.uint8).reshape(-1)) for a in ws]
+    x = synth.normal(9, 2, t * H).reshape(t, H)
+    qs = [oracle.qt(F32, a.shape[0], a.shape[1], a.view(np.uint8).reshape(-1)) for a in shared]
+    qr = [oracle.qt(F32, a.shape[0], a.shape[1], a.view(np.uint8).reshape(-1)) for a in routed]
+    y_r = oracle.mlp_forward(*qr, x)   # one routed expert, weight 1 * routed_scale
+    y_s = oracle.mlp_forward(*qs, x)
+    scale = np.float32(1.5)
+    for gate_row in (np.zeros(H, np.float32), (rng.standard_normal(H) * 0.3).astype(np.float32)):
+        ol = oracle.OracleLayer(H, 1, 1, np.ones((1, H), dtype=np.float32), [as_qt(routed)],
+                                routed_scale=float(scale), shared=as_qt(shared), shared_gate=gate_row)
+        out, sel, w, _, _ = ol.forward(x)
+        assert (sel == 0).all() and (w == scale).all()
+        g = oracle.matmul(oracle.qt(F32, 1, H, gate_row.view(np.uint8)), x).reshape(t)
+        s = (np.float32(1.0) / (np.float32(1.0) + oracle.expf_array(-g))).astype(np.float32)
+        if not gate_row.any():
+            assert (s == np.float32(0.5)).all()
+        want = (np.float32(0.0) + scale * y_r).astype(np.float32) + (y_s * s[:, None]).astype(np.float32)
+        assert np.array_equal(out.view(np.uint32), want.astype(np.float32).view(np.uint32))
+        wrong = [
+            (np.float32(0.0) + scale * y_r) + y_s,                                  # gate dropped
+            ((np.float32(0.0) + scale * y_r) + y_s) * s[:, None],                   # gate on everything
+            (np.float32(0.0) + scale * y_r) + (scale * y_s * s[:, None]),           # routed_scale on shared
+        ]
+        if gate_row.any():  # at g = 0 both spellings give 1/2
+            eg = np.exp(g.astype(np.float32))
+            wrong.append((np.float32(0.0) + scale * y_r) + y_s * (eg / (np.float32(1.0) + eg))[:, None])
+        for bad in wrong:
+            assert not np.array_equal(out.view(np.uint32), bad.astype(np.float32).view(np.uint32))

@@ -12,10 +12,11 @@ import numpy as np
 # tensor.  BASELINE.json's north_star asks for 1e-3 with f32 accumulation;
 # every kernel path computes in f32 precision (f32 GEMV, three-level int8
 # activations with exact integer dots, two-piece f16 MFMA operands with f32
-# accumulation), and the committed error table (profiles/parity_errors.md)
-# shows the measured errors lie below 1e-5 on every case, so the tests hold
-# them to that.
-TOL = 1e-5
+# accumulation).  Measured on MI355X over every case of the GPU tests: the
+# f32 GEMV 5e-7 .. 1e-6, the integer-dot paths 3e-7 .. 8e-7, the MFMA path
+# 6e-7 .. 2.1e-6 (22-bit activation pieces); the tests hold every path to
+# 5e-6, a 2.5x margin over the worst case.
+TOL = 5e-6
 
 # Where the per-case errors go (one JSON object per line), for the table.
 ERR_LOG = os.environ.get("MOE_PARITY_LOG", os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))),

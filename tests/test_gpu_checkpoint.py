@@ -8,7 +8,7 @@ import numpy as np
 import pytest
 
 from gguf_writer import GgufWriter
-from gpu_util import TOL, assert_routing_equal, log, rel_err, run_gpu
+from gpu_util import TOL, assert_routing_equal, log, record, rel_err, run_gpu
 
 pytestmark = pytest.mark.gpu
 
@@ -70,6 +70,7 @@ def test_layer_from_checkpoint(tmp_path, oracle, fmt, name, scale, t):
         assert_routing_equal(g, sel, w, f"{name} from .{fmt}")
         err = rel_err(g["out"], out)
         log(f"{name} from .{fmt}: {len(names)} tensors, max rel err {err:.2e}")
+        record("checkpoint", f"{name} from .{fmt} T={t}", err)
         assert err <= TOL
     finally:
         c.close()

@@ -3,7 +3,7 @@ src/model.rs:840) on the expert kernels, against the CPU path's MLP."""
 import numpy as np
 import pytest
 
-from gpu_util import TOL, log, rel_err
+from gpu_util import TOL, log, record, rel_err
 
 pytestmark = pytest.mark.gpu
 
@@ -81,7 +81,9 @@ def test_mlp_matches_cpu_path(ctx, oracle, name, kw, t):
     log(f"MLP {name} {kw} T={t}")
     got, _ = run(mlp, x)
     assert np.isfinite(got).all()
-    assert rel_err(got, want) <= TOL, f"max rel err {rel_err(got, want):.2e}"
+    err = rel_err(got, want)
+    record("mlp", f"{name}{' Q5_0' if kw else ''} T={t}", err)
+    assert err <= TOL, f"max rel err {err:.2e}"
 
 
 @pytest.mark.parametrize("t", [1, 5, 33])

@@ -197,6 +197,36 @@ def summarize_pmc(fetch_dir: str, write_dir: str, out_json: str) -> int:
     return 0
 
 
+def summarize_trace(trace_dir: str, out_md: str, title: str, command: str) -> int:
+    """Turn a rocprofv3 kernel trace (bench_kernel_trace.csv) into a markdown
+    table of per-kernel durations, one row per (kernel, grid size): the
+    grid size tells the bench phases (T=1, T=32, T=512) apart."""
+    import csv
+    import re
+
+    acc = {}
+    for r in csv.DictReader(open(os.path.join(trace_dir, "bench_kernel_trace.csv"))):
+        m = re.search(r"::(\w+_kernel(<[^>]*>)?)", r["Kernel_Name"])
+        name = m.group(1) if m else r["Kernel_Name"][:48]
+        grid = int(r["Grid_Size_X"]) * int(r["Grid_Size_Y"]) * int(r["Grid_Size_Z"])
+        dur = (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3
+        acc.setdefault((name, grid), []).append(dur)
+    total = sum(sum(v) for v in acc.values())
+    lines = [f"# {title}", "", "Kernel trace (from the repo root on the GPU box):", "", "    " + command, "",
+             "Rows are split by grid size (threads), which tells the bench phases apart; durations in µs.", "",
+             "| kernel | grid | calls | avg | median | min | max | share |", "|---|---|---|---|---|---|---|---|"]
+    for (name, grid), v in sorted(acc.items(), key=lambda kv: -sum(kv[1])):
+        if sum(v) < 0.001 * total:
+            continue
+        v = sorted(v)
+        lines.append(f"| `{name}` | {grid} | {len(v)} | {sum(v) / len(v):.2f} | {v[len(v) // 2]:.2f} | {v[0]:.2f} | "
+                     f"{v[-1]:.2f} | {sum(v) / total:.1%} |")
+    with open(out_md, "w") as f:
+        f.write("\n".join(lines) + "\n")
+    print(json.dumps(dict(written=out_md, kernels=len(acc))))
+    return 0
+
+
 def traffic_of(kernel_prefix: str):
     """HBM bytes per launch of the kernel whose name starts with
     kernel_prefix, from the committed counter summary (None if absent).  The
@@ -226,6 +256,8 @@ def main() -> int:
     ap.add_argument("--mode", type=int, default=0, help="kernel path (moe_layer_set_mode): 0 automatic")
     ap.add_argument("--summarize-pmc", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
                     help="write the HBM traffic summary from two rocprofv3 counter passes and exit")
+    ap.add_argument("--summarize-trace", nargs=2, metavar=("TRACE_DIR", "OUT_MD"),
+                    help="write a markdown table of kernel durations from a rocprofv3 kernel trace and exit")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="only copy MIB MiB device-to-device 5 times (a plain copy kernel of known size, the "
                          "reference point for the FETCH_SIZE / WRITE_SIZE counters) and exit")
@@ -238,6 +270,11 @@ def main() -> int:
         return copy_calibration(args.copy_calibration)
     if args.summarize_pmc:
         return summarize_pmc(args.summarize_pmc[0], args.summarize_pmc[1], TRAFFIC_FILE)
+    if args.summarize_trace:
+        return summarize_trace(args.summarize_trace[0], args.summarize_trace[1],
+                               "Mixtral-8x7B-shape routed layer (Q4_0, top-2), T=1, T=32 and T=512: kernel durations",
+                               "cd /tmp && export TMPDIR=/tmp && rocprofv3 --kernel-trace --stats --output-format csv "
+                               "-d $REPO/gpurun_out/prof -o bench -- python3 $REPO/bench.py --no-cpu --steps 20")
 
     import torch
 

@@ -209,6 +209,18 @@ int moe_layer_forward_ws(moe_layer *layer, const float *x, int32_t t, float *out
                          moe_route *routes, uint32_t *hits, const uint32_t *prev, uint64_t *stats, void *workspace,
                          uint64_t workspace_bytes, void *stream);
 
+/* moe_layer_forward on a fixed 64 MiB device array that the library's code
+ * object carries (one per device, looked up once per device on the first
+ * call there): allocates nothing, ever.  No counterpart in the reference;
+ * for callers that cannot allocate device memory (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc).  A call
+ * whose workspace would exceed the array (moe_layer_workspace_size) fails
+ * with MOE_EINVAL; calls that overlap on one device share the array and race,
+ * so order them on one stream.  Stage timing is not recorded. */
+int moe_layer_forward_noalloc(moe_layer *layer, const float *x, int32_t t, float *out, float *residual,
+                              moe_route *routes, uint32_t *hits, const uint32_t *prev, uint64_t *stats,
+                              void *stream);
+
 /* Router logits and gating only: routes [t, k] for x [t, H], as
  * src/model.rs:844-898 computes them.  `logits` (device f32 [t, E]) may be
  * NULL; if given it receives the router logits after the temperature. */

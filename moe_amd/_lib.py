@@ -72,6 +72,8 @@ PROTOTYPES = {
     "moe_layer_reserve": (C.c_int, [C.c_void_p, C.c_int32]),
     "moe_layer_reserve_stream": (C.c_int, [C.c_void_p, C.c_int32, C.c_void_p]),
     "moe_layer_workspace_size": (C.c_int, [C.c_void_p, C.c_int32, C.POINTER(C.c_uint64)]),
+    "moe_layer_forward_noalloc": (C.c_int, [C.c_void_p, C.c_void_p, C.c_int32, C.c_void_p, C.c_void_p,
+                                            C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p]),
     "moe_layer_forward_ws": (C.c_int, [C.c_void_p, C.c_void_p, C.c_int32, C.c_void_p, C.c_void_p, C.c_void_p,
                                        C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_uint64, C.c_void_p]),
     "moe_layer_set_mode": (C.c_int, [C.c_void_p, C.c_int]),

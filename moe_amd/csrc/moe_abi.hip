@@ -660,6 +660,39 @@ int forward_on(moe_layer *L, const CallState &c, Workspace &w, const float *x, i
     });
 }
 
+// ---- the allocation-free entry point -------------------------------------
+// moe_layer_forward_noalloc runs on this array: device memory the code
+// object itself carries, so no call allocates.  In host code `scratch` is
+// only a stand-in for the symbol, never a device address: every host use
+// goes through the per-device address hipGetSymbolAddress returns.  The
+// counters at its start are zero at load (static storage) and every call
+// leaves them at zero again; set-up clears them once more.  Every call on a
+// device shares that device's array, so calls that overlap on one device
+// race.
+constexpr size_t kScratchBytes = (size_t)64 << 20;
+constexpr int kMaxDevices = 64;
+static __device__ __align__(256) uint8_t scratch[kScratchBytes];
+
+std::mutex g_scratch_mu;
+void *g_scratch_ptr[kMaxDevices] = {};
+
+// The device address of `scratch` on `device` (which is current), looked up
+// and cleared once per device.
+int scratch_on(int device, void *&out) {
+    if (device < 0 || device >= kMaxDevices) return fail(MOE_EUNSUP, "device %d: at most %d devices", device, kMaxDevices);
+    std::lock_guard<std::mutex> g(g_scratch_mu);
+    if (!g_scratch_ptr[device]) {
+        void *p = nullptr;
+        hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess) return hip_fail(e, "hipGetSymbolAddress(scratch)");
+        if (!p || (uintptr_t)p % 256) return fail(MOE_EHIP, "scratch array at %p is not 256-byte aligned", p);
+        if ((e = hipMemset(p, 0, 256)) != hipSuccess) return hip_fail(e, "clearing the scratch counters");
+        g_scratch_ptr[device] = p;
+    }
+    out = g_scratch_ptr[device];
+    return MOE_OK;
+}
+
 // A caller's workspace laid out for t tokens of k experts, after checking
 // that it is big enough.
 int caller_ws(const moe_layer *L, int t, int k, void *ws, uint64_t ws_bytes, Workspace &w) {
@@ -1049,6 +1082,26 @@ int moe_layer_forward_ws(moe_layer *L, const float *x, int32_t t, float *out, fl
     Workspace w;
     int rc = caller_ws(L, t, c.k, workspace, workspace_bytes, w);
     if (rc) return rc;
+    return forward_on(L, c, w, x, t, out, residual, routes, hits, prev, stats, (hipStream_t)stream);
+}
+
+int moe_layer_forward_noalloc(moe_layer *L, const float *x, int32_t t, float *out, float *residual,
+                              moe_route *routes, uint32_t *hits, const uint32_t *prev, uint64_t *stats, void *stream) {
+    if (!L || !x || !out || t <= 0) return fail(MOE_EINVAL, "moe_layer_forward_noalloc: bad argument (t = %d)", t);
+    DeviceGuard g(L->ctx->device);
+    CallState c = snapshot(L);
+    c.profile = false;  // stage timing creates events; this entry point allocates nothing
+    const size_t need = ws_layout(L, t, c.k, nullptr, nullptr);
+    if (need > kScratchBytes)
+        return fail(MOE_EINVAL,
+                    "moe_layer_forward_noalloc: %d tokens of %d experts need %zu bytes of scratch; the static "
+                    "array holds %zu (use moe_layer_forward_ws with a larger workspace)",
+                    t, c.k, need, kScratchBytes);
+    void *base = nullptr;
+    int rc = scratch_on(L->ctx->device, base);
+    if (rc) return rc;
+    Workspace w;
+    ws_layout(L, t, c.k, &w, static_cast<char *>(base));
     return forward_on(L, c, w, x, t, out, residual, routes, hits, prev, stats, (hipStream_t)stream);
 }
 

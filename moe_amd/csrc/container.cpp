@@ -38,11 +38,20 @@ struct Rec {
     uint64_t slabs, rows, cols, offset;
 };
 
+// a * b, or UINT64_MAX when it does not fit: sizes come from file headers,
+// and a corrupt one must not wrap into a small size that then passes a
+// bounds check (the reference saturates for the same reason,
+// src/store.rs:36-43).
+uint64_t sat_mul(uint64_t a, uint64_t b) {
+    uint64_t r;
+    return __builtin_mul_overflow(a, b, &r) ? UINT64_MAX : r;
+}
+
 uint64_t row_bytes_of(int32_t dt, uint64_t cols) {
     switch (dt) {
-    case MOE_DT_F32: return cols * 4;
+    case MOE_DT_F32: return sat_mul(cols, 4);
     case MOE_DT_F16:
-    case MOE_DT_BF16: return cols * 2;
+    case MOE_DT_BF16: return sat_mul(cols, 2);
     case MOE_DT_Q4_0: return cols / 32 * 18;
     case MOE_DT_Q5_0: return cols / 32 * 22;
     case MOE_DT_Q8_0: return cols / 32 * 34;
@@ -54,11 +63,7 @@ uint64_t row_bytes_of(int32_t dt, uint64_t cols) {
 }
 
 // Saturating slabs * rows * row_bytes (src/store.rs:36-43).
-uint64_t rec_len(const Rec &r) {
-    const uint64_t rb = row_bytes_of(r.dt, r.cols);
-    unsigned __int128 n = (unsigned __int128)r.slabs * r.rows * rb;
-    return n > (unsigned __int128)UINT64_MAX ? UINT64_MAX : (uint64_t)n;
-}
+uint64_t rec_len(const Rec &r) { return sat_mul(sat_mul(r.slabs, r.rows), row_bytes_of(r.dt, r.cols)); }
 
 bool fits(const Rec &r, uint64_t len) {
     const uint64_t n = rec_len(r);
@@ -383,7 +388,7 @@ int open_gguf(const uint8_t *b, uint64_t len, moe_container &c) {
         r.cols = d[0];
         r.rows = dims >= 2 ? d[1] : 1;
         r.slabs = dims >= 3 ? d[2] : 1;
-        if (dims == 4) r.slabs *= d[3];
+        if (dims == 4) r.slabs = sat_mul(r.slabs, d[3]);
         r.dt = (int32_t)t;
         r.offset = off;
         infos.push_back(std::move(r));

@@ -243,10 +243,13 @@ void parallel_for(uint64_t n, F f) {
 extern "C" {
 
 uint64_t moe_row_bytes(int32_t dt, uint64_t cols) {
+    // Saturating, like the container reader: a row too wide for 64 bits of
+    // bytes reports UINT64_MAX rather than a wrapped small size.
+    uint64_t r;
     switch (dt) {
-    case MOE_DT_F32: return cols * 4;
+    case MOE_DT_F32: return __builtin_mul_overflow(cols, (uint64_t)4, &r) ? UINT64_MAX : r;
     case MOE_DT_F16:
-    case MOE_DT_BF16: return cols * 2;
+    case MOE_DT_BF16: return __builtin_mul_overflow(cols, (uint64_t)2, &r) ? UINT64_MAX : r;
     case MOE_DT_Q8_0: return cols / 32 * 34;
     case MOE_DT_Q4_0: return cols / 32 * 18;
     case MOE_DT_Q5_0: return cols / 32 * 22;

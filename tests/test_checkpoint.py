@@ -222,3 +222,36 @@ def test_truncated_or_corrupted_gguf_is_refused(lib):
     r = Rand(11)
     for _ in range(400):
         parse(lib, r.mutate(data[:data_start]) + data[data_start:])
+
+
+def _moe_with(entries: dict, payload: bytes) -> bytes:
+    header = json.dumps({"config": {}, "tensors": entries}, separators=(",", ":")).encode()
+    return b"MOEF" + struct.pack("<IQ", 1, len(header)) + header + payload
+
+
+@pytest.mark.parametrize("dt,shape", [
+    ("F32", [2**63 + 2**32 + 1, 2**63 - 2**32 + 1, 1]),   # slabs * rows * 4 wraps past 2^128 to 4 bytes
+    ("F32", [1, 2**62]),                                 # cols * 4 wraps to 0 in 64 bits
+    ("F32", [2**62, 2**62, 4]),
+    ("Q8", [3, 2**61, 2**60]),
+    ("F16", [1, 2**63]),
+])
+def test_wrapping_shapes_are_refused(lib, dt, shape):
+    """Header shapes whose byte size overflows 64 bits (or 128) are
+    refused: every size multiply saturates, as the reference's Rec::len does
+    (src/store.rs:36-43), so no wrapped small size can pass the bounds check."""
+    data = _moe_with({"w": {"dt": dt, "shape": shape, "off": 0, "len": 4}}, b"\0" * 64)
+    rc, recs = parse(lib, data)
+    assert rc != 0, f"accepted {shape} as {recs}"
+
+
+def test_gguf_four_dimension_product_saturates(lib):
+    """A 4-D GGUF tensor whose outer dimensions multiply past 2^64 is refused
+    (the slab count saturates instead of wrapping)."""
+    from moe_amd import _lib as L
+
+    w = GgufWriter(32)
+    w.tensor("x.weight", [2**40, 2**40, 1, 64], L.DT_F32, b"\0" * 256)
+    data = w.build()
+    rc, recs = parse(lib, data)
+    assert rc != 0, f"accepted {recs}"

@@ -244,6 +244,85 @@ const char *moe_last_error(void);
  * device f32 [n].  No counterpart in the reference. */
 int moe_debug_expf(const float *x, float *y, uint64_t n, void *stream);
 
+/* ------------------------------------------------ the model around the layer
+ * The rest of the reference's forward (src/model.rs:646-834) as device
+ * operations, so that a whole decoder runs with its routed layers on the
+ * kernels above.  All tensors are device f32 unless stated; `stream` as
+ * above.  These compute in f32 and reduce in their own order: results agree
+ * with the CPU path to f32 rounding. */
+
+typedef struct moe_linear moe_linear;
+
+/* A plain projection y = W x over an uploaded view W [N, K] in any format of
+ * this library (F32, Q4_0, Q5_0, Q8_0).  Replaces quant::matmul
+ * (src/quant.rs:482-506) for the attention projections, the dense layers'
+ * matrices and lm_head (src/model.rs:641, 704-706, 742-771, 833), on the
+ * expert kernels: the f32 GEMV for up to 8 tokens, the MFMA kernel (two-piece
+ * f16 operands, f32 accumulation) beyond, the exact kernel (the reference's
+ * dot, bit for bit) for formats and widths those do not take. */
+int moe_linear_create(moe_ctx *ctx, const moe_tensor *w, moe_linear **out);
+void moe_linear_destroy(moe_linear *linear);
+/* Bytes of workspace moe_linear_forward needs for up to max_t tokens. */
+int moe_linear_workspace_size(const moe_linear *linear, int32_t max_t, uint64_t *bytes);
+/* y [t, N] = x [t, K] W^T; residual (or NULL) += y.  `workspace`: device,
+ * 256-byte aligned, moe_linear_workspace_size bytes (ordered on one stream). */
+int moe_linear_forward(moe_linear *linear, const float *x, int32_t t, float *y, float *residual, void *workspace,
+                       uint64_t workspace_bytes, void *stream);
+
+/* x[i] = the dequantised row tokens[i] % rows of a table stored in `dt`
+ * (trunk's embedding lookup, src/model.rs:669-671).  table: device bytes of
+ * rows x Dt::row_bytes(cols); tokens: device int32 [t]. */
+int moe_embed_rows(const void *table, int32_t dt, int32_t rows, int32_t cols, const int32_t *tokens, int32_t t,
+                   float *x, void *stream);
+
+/* rmsnorm (src/model.rs:211-216) of `rows` rows of n values, x_stride and
+ * out_stride floats apart, weight w [n]. */
+int moe_rmsnorm(const float *x, int64_t x_stride, const float *w, int32_t rows, int32_t n, float eps, float *out,
+                int64_t out_stride, void *stream);
+
+/* rope (src/model.rs:324-333) in place: for each row r (row_stride floats
+ * apart) and head h < heads (head_stride floats apart), the dim values from
+ * `offset` rotate pairwise (i, i + dim/2) by pos[r] * inv_freq[i].
+ * pos: device int32 [rows]; inv_freq: device f32 [n_inv]. */
+int moe_rope(float *x, int32_t rows, int64_t row_stride, int32_t heads, int32_t head_stride, int32_t offset,
+             int32_t dim, const int32_t *pos, const float *inv_freq, int32_t n_inv, void *stream);
+
+/* Rope::inv_freqs (src/spec.rs:89-145) on the host into out[head_dim / 2]:
+ * kind 0 none, 1 linear, 2 dynamic (NTK), 3 YaRN, 4 Llama 3. */
+int moe_rope_inv_freqs(int32_t kind, float theta, float factor, uint64_t original_ctx, float low_freq_factor,
+                       float high_freq_factor, float beta_fast, float beta_slow, int32_t head_dim, float *out);
+
+/* x[i] += bias[i % bias_len] over `total` values (src/model.rs:707-713). */
+int moe_add_bias(float *x, uint64_t total, const float *bias, int32_t bias_len, void *stream);
+
+/* dst row dst_rows[r] (dst_stride floats apart) = src row r (n values,
+ * src_stride apart): the KV-cache write (src/model.rs:732-733).
+ * dst_rows: device int64 [rows]. */
+int moe_scatter_rows(const float *src, int32_t rows, int32_t n, int64_t src_stride, float *dst, int64_t dst_stride,
+                     const int64_t *dst_rows, void *stream);
+
+/* MLA's cache rows (src/model.rs:773-787): for row r and head h, key
+ * [kv nope part, c's rope part (k_pe, already rotated)] and value kv's value
+ * part, written at cache row dst_rows[r].  kv [rows, heads * (qk_nope +
+ * v_head)], c [rows, >= kv_lora + qk_rope] c_stride apart. */
+int moe_mla_kv_store(const float *kv, const float *c, int64_t c_stride, int32_t kv_lora, int32_t rows,
+                     int32_t heads, int32_t qk_nope, int32_t qk_rope, int32_t v_head, float *kcache, float *vcache,
+                     const int64_t *dst_rows, void *stream);
+
+/* Causal attention (src/model.rs:790-831): row r of q (heads x qd values,
+ * q_stride apart) belongs to sequence seq[r] at position pos[r] and attends
+ * to cache positions [lo, pos[r]] of that sequence (lo = pos + 1 - window
+ * for window > 0, else 0), head h reading kv head h / (heads / n_kv).
+ * Cache layout: [sequence][ctx][n_kv * qd] keys, [sequence][ctx][n_kv * vd]
+ * values.  out row r: heads x vd values.  max_pos bounds every pos[r]. */
+int moe_attention(const float *q, int64_t q_stride, int32_t rows, int32_t heads, int32_t n_kv, int32_t qd,
+                  int32_t vd, float scale, const float *kcache, const float *vcache, int64_t ctx, const int32_t *seq,
+                  const int32_t *pos, int32_t max_pos, int32_t window, float *out, int64_t out_stride, void *stream);
+
+/* out[r] = the first index of row r's maximum (greedy sampling,
+ * src/sample.rs:87-95).  x [rows, n]; out: device int32 [rows]. */
+int moe_argmax(const float *x, int32_t rows, int32_t n, int32_t *out, void *stream);
+
 /* --------------------------------------------------- checkpoint containers */
 
 /* One tensor of a single-file checkpoint: Store's Rec (src/store.rs:25-47).

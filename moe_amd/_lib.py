@@ -102,6 +102,28 @@ PROTOTYPES = {
                                      C.POINTER(C.c_uint64), C.c_int64, C.POINTER(C.c_uint64),
                                      C.POINTER(C.c_uint64)]),
     "moe_layer_stage_times": (C.c_int, [C.c_void_p, C.POINTER(C.c_double), C.POINTER(C.c_uint64)]),
+    "moe_linear_create": (C.c_int, [C.c_void_p, C.POINTER(Tensor), C.POINTER(C.c_void_p)]),
+    "moe_linear_destroy": (None, [C.c_void_p]),
+    "moe_linear_workspace_size": (C.c_int, [C.c_void_p, C.c_int32, C.POINTER(C.c_uint64)]),
+    "moe_linear_forward": (C.c_int, [C.c_void_p, C.c_void_p, C.c_int32, C.c_void_p, C.c_void_p, C.c_void_p,
+                                     C.c_uint64, C.c_void_p]),
+    "moe_embed_rows": (C.c_int, [C.c_void_p, C.c_int32, C.c_int32, C.c_int32, C.c_void_p, C.c_int32, C.c_void_p,
+                                 C.c_void_p]),
+    "moe_rmsnorm": (C.c_int, [C.c_void_p, C.c_int64, C.c_void_p, C.c_int32, C.c_int32, C.c_float, C.c_void_p,
+                              C.c_int64, C.c_void_p]),
+    "moe_rope": (C.c_int, [C.c_void_p, C.c_int32, C.c_int64, C.c_int32, C.c_int32, C.c_int32, C.c_int32, C.c_void_p,
+                           C.c_void_p, C.c_int32, C.c_void_p]),
+    "moe_rope_inv_freqs": (C.c_int, [C.c_int32, C.c_float, C.c_float, C.c_uint64, C.c_float, C.c_float, C.c_float,
+                                     C.c_float, C.c_int32, C.c_void_p]),
+    "moe_add_bias": (C.c_int, [C.c_void_p, C.c_uint64, C.c_void_p, C.c_int32, C.c_void_p]),
+    "moe_scatter_rows": (C.c_int, [C.c_void_p, C.c_int32, C.c_int32, C.c_int64, C.c_void_p, C.c_int64, C.c_void_p,
+                                   C.c_void_p]),
+    "moe_mla_kv_store": (C.c_int, [C.c_void_p, C.c_void_p, C.c_int64, C.c_int32, C.c_int32, C.c_int32, C.c_int32,
+                                   C.c_int32, C.c_int32, C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p]),
+    "moe_attention": (C.c_int, [C.c_void_p, C.c_int64, C.c_int32, C.c_int32, C.c_int32, C.c_int32, C.c_int32,
+                                C.c_float, C.c_void_p, C.c_void_p, C.c_int64, C.c_void_p, C.c_void_p, C.c_int32,
+                                C.c_int32, C.c_void_p, C.c_int64, C.c_void_p]),
+    "moe_argmax": (C.c_int, [C.c_void_p, C.c_int32, C.c_int32, C.c_void_p, C.c_void_p]),
 }
 
 STAGES = ("router", "gating", "dispatch", "expert_up", "expert_down", "combine", "encode")

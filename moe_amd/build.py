@@ -36,7 +36,8 @@ HIP_FLAGS = [
 # Sources whose arithmetic must follow the reference operation by operation.
 EXACT = {"route.hip", "combine.hip", "expert_gemv.hip", "expert_decode.hip"}
 
-SOURCES = ["route.hip", "expert_gemv.hip", "expert_decode.hip", "expert_batch.hip", "expert_mfma.hip", "combine.hip", "moe_abi.hip"]
+SOURCES = ["route.hip", "expert_gemv.hip", "expert_decode.hip", "expert_batch.hip", "expert_mfma.hip", "combine.hip",
+           "model_ops.hip", "moe_abi.hip"]
 HOST_SOURCES = ["host_util.cpp", "container.cpp"]
 
 

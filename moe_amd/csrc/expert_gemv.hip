@@ -747,6 +747,10 @@ hipError_t launch_gemv_down(const GemvArgs &a, const ExpertDev &e0, const Expert
     return err;
 }
 
+hipError_t launch_gemv_down_single(const GemvArgs &a, const ExpertDev &ex, hipStream_t s) {
+    return gemv_launch(kDown, a, ex, true, s);
+}
+
 hipError_t launch_gemv_down_combine(const GemvArgs &a, const ExpertDev &e0, const ExpertDev *sh, hipStream_t s) {
     hipError_t err = gemv_launch(kDownCombine, a, e0, false, s);
     if (err == hipSuccess && a.has_shared && sh) err = gemv_launch(kDownCombine, a, *sh, true, s);

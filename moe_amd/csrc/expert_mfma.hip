@@ -793,6 +793,14 @@ hipError_t launch_mfma(bool up, const MfmaArgs &a, int bm, const ExpertDev &e0, 
     return up ? launch_dt<true>(ms.dt, bm, gs, a, 1, ks, s) : launch_dt<false>(ms.dt, bm, gs, a, 1, ks, s);
 }
 
+hipError_t launch_mfma_single(bool up, const MfmaArgs &a, int bm, const ExpertDev &ex, hipStream_t s) {
+    const MatDev &m = up ? ex.m[0] : ex.m[2];
+    const int cols = up ? BW / 2 : BW;
+    const int ks = up ? 1 : a.ksplit;
+    dim3 gs((a.T + bm - 1) / bm, (m.rows + cols - 1) / cols, ks);
+    return up ? launch_dt<true>(m.dt, bm, gs, a, 1, ks, s) : launch_dt<false>(m.dt, bm, gs, a, 1, ks, s);
+}
+
 hipError_t launch_split_rows(const float *src, int rows, int cols, uint16_t *hi, uint16_t *lo, int32_t *ex,
                              hipStream_t s) {
     if (rows <= 0) return hipSuccess;

@@ -13,6 +13,11 @@
 
 #include "../../include/moe_hip.h"
 
+namespace moe {
+int fail(int code, const char *fmt, ...);
+}
+using moe::fail;
+
 namespace {
 
 inline uint32_t bits_of(float f) {
@@ -255,6 +260,48 @@ uint64_t moe_row_bytes(int32_t dt, uint64_t cols) {
     case MOE_DT_Q5_0: return cols / 32 * 22;
     default: return 0;
     }
+}
+
+int moe_rope_inv_freqs(int32_t kind, float theta, float factor, uint64_t original_ctx, float low_freq_factor,
+                       float high_freq_factor, float beta_fast, float beta_slow, int32_t head_dim, float *out) {
+    if (!out || head_dim < 2 || kind < 0 || kind > 4) return fail(MOE_EINVAL, "moe_rope_inv_freqs: bad argument");
+    // Rope::inv_freqs (src/spec.rs:89-145) in f32 with libm's powf, logf:
+    // the same operations in the same order, so the table is the engine's.
+    const int half = head_dim / 2;
+    const float dim = (float)head_dim;
+    const float s = factor > 1e-6f ? factor : 1e-6f;
+    float th = theta;
+    if (kind == 2) th = theta * std::pow(s, dim / std::max(dim - 2.0f, 1.0f));
+    for (int i = 0; i < half; i++) out[i] = std::pow(th, -2.0f * (float)i / dim);
+    const float pi = 3.14159265358979323846f;
+    if (kind == 1) {
+        for (int i = 0; i < half; i++) out[i] = out[i] / s;
+    } else if (kind == 4) {
+        const float l = (float)original_ctx;
+        const float lo_wave = l / low_freq_factor, hi_wave = l / high_freq_factor;
+        const float span = std::max(high_freq_factor - low_freq_factor, 1e-6f);
+        for (int i = 0; i < half; i++) {
+            const float f = out[i], wave = 2.0f * pi / f;
+            if (wave > lo_wave) {
+                out[i] = f / s;
+            } else if (wave >= hi_wave) {
+                const float t = ((l / wave) - low_freq_factor) / span;
+                out[i] = (1.0f - t) * f / s + t * f;
+            }
+        }
+    } else if (kind == 3) {
+        const float l = (float)original_ctx;
+        const float ln_base = std::max(std::log(theta), 1e-6f);
+        auto bound = [&](float beta) { return dim * std::log(l / (beta * 2.0f * pi)) / (2.0f * ln_base); };
+        const float low = std::floor(bound(beta_fast)), high = std::ceil(bound(beta_slow));
+        const float span = std::max(high - low, 1e-3f);
+        for (int i = 0; i < half; i++) {
+            const float f = out[i];
+            const float ramp = std::min(std::max(((float)i - low) / span, 0.0f), 1.0f);
+            out[i] = (1.0f - ramp) * (f / s) + ramp * f;
+        }
+    }
+    return MOE_OK;
 }
 
 int moe_quantize_rows(int32_t dt, const float *src, uint64_t rows, uint64_t cols, uint8_t *dst) {

@@ -1105,6 +1105,157 @@ int moe_layer_forward_noalloc(moe_layer *L, const float *x, int32_t t, float *ou
     return forward_on(L, c, w, x, t, out, residual, routes, hits, prev, stats, (hipStream_t)stream);
 }
 
+}  // extern "C"
+
+// ---- plain projections ------------------------------------------------------
+// quant::matmul (src/quant.rs:482-506) for the weights around the routed
+// layers: attention projections, the dense path's projections and lm_head.
+// The matrix is held like a shared expert's down projection (table entry
+// 0 = the matrix), so the expert kernels run it unchanged: the f32 GEMV for
+// a few tokens, the MFMA kernel (f16 pieces, f32 accumulation) beyond, the
+// exact kernel (the reference's dot, bit for bit) for formats and widths
+// those do not take.
+struct moe_linear {
+    moe_ctx *ctx = nullptr;
+    ExpertDev host{};
+    ExpertDev *dev = nullptr;
+    bool fast = false, mfma = false;
+    int bm = 160;
+};
+
+namespace {
+
+// Tokens up to which the GEMV beats the MFMA path for one matrix.
+constexpr int kLinearGemvMaxT = 8;
+
+size_t linear_ws_layout(const moe_linear *l, int max_t, char *base, uint16_t **hi, uint16_t **lo, int32_t **ex) {
+    const size_t T = (size_t)max_t, K = (size_t)l->host.m[2].cols;
+    const bool pieces = l->mfma && max_t > kLinearGemvMaxT;
+    const size_t a = pieces ? align_up(T * K * 2, 256) : 0, b = pieces ? align_up(T * 4, 256) : 0;
+    if (base && pieces) {
+        *hi = reinterpret_cast<uint16_t *>(base);
+        *lo = reinterpret_cast<uint16_t *>(base + a);
+        *ex = reinterpret_cast<int32_t *>(base + 2 * a);
+    }
+    return std::max<size_t>(2 * a + b, 256);
+}
+
+}  // namespace
+
+extern "C" {
+
+int moe_linear_create(moe_ctx *ctx, const moe_tensor *w, moe_linear **out) {
+    if (!ctx || !w || !out) return fail(MOE_EINVAL, "moe_linear_create: bad argument");
+    if (w->rows <= 0 || w->cols <= 0) return fail(MOE_EINVAL, "moe_linear_create: shape [%d, %d]", w->rows, w->cols);
+    DeviceGuard g(ctx->device);
+    auto l = std::make_unique<moe_linear>();
+    l->ctx = ctx;
+    MatDev m;
+    int rc;
+    {
+        std::lock_guard<std::mutex> lk(ctx->mu);
+        rc = resolve(ctx, *w, w->rows, w->cols, "linear weight", m);
+    }
+    if (rc) return rc;
+    l->host.m[0] = l->host.m[1] = l->host.m[2] = m;
+    l->host.inter = m.cols;
+    l->fast = fast_mat(m) && m.dt != MOE_DT_F32;
+    l->mfma = l->fast && mfma_format_ok(m.dt) && m.cols % 64 == 0 && (size_t)m.rows * m.stride < ((size_t)1 << 32);
+    hipError_t he;
+    if ((he = hipMalloc(&l->dev, sizeof(ExpertDev))) != hipSuccess) return hip_fail(he, "linear table");
+    if (l->mfma) {
+        unsigned *mx = nullptr, host[3] = {0, 0, 0};
+        if ((he = hipMemcpy(l->dev, &l->host, sizeof(ExpertDev), hipMemcpyHostToDevice)) != hipSuccess ||
+            (he = hipMalloc(&mx, 12)) != hipSuccess)
+            return hip_fail(he, "linear scale maxima");
+        he = hipMemset(mx, 0, 12);
+        if (he == hipSuccess) he = launch_scale_max(l->dev, 1, mx, nullptr);
+        if (he == hipSuccess) he = hipMemcpy(host, mx, 12, hipMemcpyDeviceToHost);
+        hipFree(mx);
+        if (he != hipSuccess) return hip_fail(he, "linear scale maxima");
+        const float qmax = m.dt == MOE_DT_Q4_0 ? 8.0f : m.dt == MOE_DT_Q5_0 ? 16.0f : 128.0f;
+        int wexp = 0;
+        if (host[2]) {
+            int fe = 0;
+            (void)std::frexp(f16_bits_to_float(host[2]) * qmax, &fe);
+            wexp = 15 - fe;
+        }
+        for (int i = 0; i < 3; i++) l->host.m[i].wexp = wexp;
+        const int dt = m.dt;
+        l->bm = mfma_tile_m(&dt, 1);
+    }
+    if ((he = hipMemcpy(l->dev, &l->host, sizeof(ExpertDev), hipMemcpyHostToDevice)) != hipSuccess)
+        return hip_fail(he, "linear table");
+    *out = l.release();
+    return MOE_OK;
+}
+
+void moe_linear_destroy(moe_linear *l) {
+    if (!l) return;
+    DeviceGuard g(l->ctx->device);
+    hipDeviceSynchronize();
+    hipFree(l->dev);
+    delete l;
+}
+
+int moe_linear_workspace_size(const moe_linear *l, int32_t max_t, uint64_t *bytes) {
+    if (!l || max_t <= 0 || !bytes) return fail(MOE_EINVAL, "moe_linear_workspace_size: bad argument");
+    *bytes = linear_ws_layout(l, max_t, nullptr, nullptr, nullptr, nullptr);
+    return MOE_OK;
+}
+
+int moe_linear_forward(moe_linear *l, const float *x, int32_t t, float *y, float *residual, void *workspace,
+                       uint64_t workspace_bytes, void *stream) {
+    if (!l || !x || !y || t <= 0) return fail(MOE_EINVAL, "moe_linear_forward: bad argument (t = %d)", t);
+    DeviceGuard g(l->ctx->device);
+    hipStream_t s = (hipStream_t)stream;
+    const MatDev &m = l->host.m[2];
+    hipError_t e = hipSuccess;
+    if (l->mfma && t > kLinearGemvMaxT) {
+        const size_t need = linear_ws_layout(l, t, nullptr, nullptr, nullptr, nullptr);
+        if (!workspace || workspace_bytes < need || (uintptr_t)workspace % 256)
+            return fail(MOE_EINVAL, "moe_linear_forward: %d tokens need a 256-byte-aligned workspace of %zu bytes", t,
+                        need);
+        uint16_t *hi = nullptr, *lo = nullptr;
+        int32_t *ex = nullptr;
+        linear_ws_layout(l, t, static_cast<char *>(workspace), &hi, &lo, &ex);
+        MfmaArgs a{};
+        a.experts = l->dev;
+        a.E = 0;
+        a.T = t;
+        a.H = m.rows;
+        a.I = a.I_s = m.cols;
+        a.hshi = hi;
+        a.hslo = lo;
+        a.hsex = ex;
+        a.ys = y;
+        a.yspart = (size_t)t * m.rows;
+        a.ksplit = 1;
+        a.shared_tiles = (t + l->bm - 1) / l->bm;
+        e = launch_split_rows(x, t, m.cols, hi, lo, ex, s);
+        if (e == hipSuccess) e = launch_mfma_single(false, a, l->bm, l->host, s);
+    } else {
+        GemvArgs a{};
+        a.experts = l->dev;
+        a.E = 0;
+        a.T = t;
+        a.H = m.rows;
+        a.I = a.I_s = m.cols;
+        a.hs = const_cast<float *>(x);
+        a.ys = y;
+        a.task_bound = 0;
+        a.has_shared = 1;
+        e = l->fast ? launch_gemv_down_single(a, l->host, s) : launch_gemv_exact(false, a, s);
+    }
+    if (e != hipSuccess) return hip_fail(e, "linear kernels");
+    if (residual) {
+        // residual += y, as the attention block's x += o(ctx) (src/model.rs:676-679).
+        e = launch_add(residual, y, (size_t)t * m.rows, s);
+        if (e != hipSuccess) return hip_fail(e, "residual add");
+    }
+    return MOE_OK;
+}
+
 int moe_layer_profile(moe_layer *L, int enable) {
     if (!L) return fail(MOE_EINVAL, "moe_layer_profile: layer is NULL");
     std::lock_guard<std::mutex> g(L->mu);

@@ -181,6 +181,11 @@ struct GemvArgs {
 };
 hipError_t launch_gemv_up(const GemvArgs &a, const ExpertDev &host_e0, const ExpertDev *host_shared, hipStream_t s);
 hipError_t launch_gemv_down(const GemvArgs &a, const ExpertDev &host_e0, const ExpertDev *host_shared, hipStream_t s);
+// The down projection of table entry a.E alone (a.task_bound == 0): the
+// plain projection ys = W hs over all a.T tokens.
+hipError_t launch_gemv_down_single(const GemvArgs &a, const ExpertDev &ex, hipStream_t s);
+// dst[i] += src[i] for n values.
+hipError_t launch_add(float *dst, const float *src, size_t n, hipStream_t s);
 // Down projection with the combine, shared expert and residual folded in
 // (T <= kFusedMaxT): writes out (and residual) directly.
 constexpr int kFusedMaxT = 8;
@@ -245,6 +250,11 @@ int mfma_down_ksplit(int m_tiles, int n_rows, int K, int K_shared);
 // dispatch list built with tile `bm`; the shared expert (sh != null) gets its
 // own launch.
 hipError_t launch_mfma(bool up, const MfmaArgs &a, int bm, const ExpertDev &e0, const ExpertDev *sh, hipStream_t s);
+// One matrix over all T tokens (the shared-expert tiles alone): the plain
+// projection y = W x on the matrix cores.  The matrix is table entry
+// a.E (a.experts[a.E]); the activations are the shared expert's pieces
+// (hshi, hslo, hsex for the down form) and the output goes to ys.
+hipError_t launch_mfma_single(bool up, const MfmaArgs &a, int bm, const ExpertDev &ex, hipStream_t s);
 // Rows [rows, cols] of f32 into f16 pieces: hi + lo = v * 2^ex[row] to
 // 22 bits, ex chosen per row so that its largest |v| scales into
 // [2^14, 2^15) (0 for an all-zero or non-finite row).  cols % 4 == 0.

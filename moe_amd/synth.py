@@ -283,3 +283,179 @@ def make_layer(ctx, host: HostLayer, layer_index: int = 0):
                      shared_gate=shared_gate, layer_index=layer_index)
     layer._region = region  # keep the region alive with the layer
     return layer
+
+
+# ------------------------------------------------------------ whole models
+
+
+@dataclass(frozen=True)
+class ModelShape:
+    """A decoder's architecture as a Hugging Face config states it
+    (BASELINE.json configs[0] and configs[4])."""
+
+    name: str
+    hidden: int
+    layers: int
+    heads: int
+    kv_heads: int
+    head_dim: int
+    vocab: int
+    moe_inter: int
+    n_experts: int
+    top_k: int
+    dt: int
+    style: str                      # "mixtral" (block_sparse_moe names) or "deepseek"
+    dense_inter: int = 0            # the dense MLP of layers before first_dense
+    first_dense: int = 0
+    shared_inter: int = 0
+    norm_topk: bool = True
+    mla: Optional[tuple] = None     # (q_lora, kv_lora, qk_nope, qk_rope, v_head)
+    rope_theta: float = 10000.0
+    rope_scaling: Optional[dict] = None
+    eps: float = 1e-6
+    max_pos: int = 4096
+    weight_std: float = 0.02
+
+    def config(self) -> dict:
+        c = {"hidden_size": self.hidden, "num_hidden_layers": self.layers, "num_attention_heads": self.heads,
+             "num_key_value_heads": self.kv_heads, "vocab_size": self.vocab, "rms_norm_eps": self.eps,
+             "rope_theta": self.rope_theta, "max_position_embeddings": self.max_pos,
+             "num_experts_per_tok": self.top_k, "norm_topk_prob": self.norm_topk, "tie_word_embeddings": False}
+        if self.style == "mixtral":
+            c.update(architectures=["MixtralForCausalLM"], model_type="mixtral", head_dim=self.head_dim,
+                     intermediate_size=self.moe_inter, num_local_experts=self.n_experts)
+        else:
+            q_lora, kv_lora, nope, rope, v = self.mla
+            c.update(architectures=["DeepseekV2ForCausalLM"], model_type="deepseek_v2",
+                     q_lora_rank=q_lora or None, kv_lora_rank=kv_lora, qk_nope_head_dim=nope,
+                     qk_rope_head_dim=rope, v_head_dim=v, intermediate_size=self.dense_inter,
+                     moe_intermediate_size=self.moe_inter, n_routed_experts=self.n_experts,
+                     n_shared_experts=self.shared_inter // self.moe_inter, first_k_dense_replace=self.first_dense,
+                     scoring_func="softmax", routed_scaling_factor=1.0, n_group=1, topk_group=1)
+        if self.rope_scaling:
+            c["rope_scaling"] = dict(self.rope_scaling)
+        return c
+
+    def plan(self) -> list:
+        """(name, dt, shape, fill) of every tensor; fill is "ones" (norms),
+        "router" (F32 N(0, std)) or "weight" (N(0, std) in the model's
+        format)."""
+        H, dt, p = self.hidden, self.dt, "model.layers."
+        out = [("model.embed_tokens.weight", dt, (self.vocab, H), "weight"),
+               ("model.norm.weight", 0, (H,), "ones"), ("lm_head.weight", dt, (self.vocab, H), "weight")]
+        for l in range(self.layers):
+            a = f"{p}{l}.self_attn."
+            out += [(f"{p}{l}.input_layernorm.weight", 0, (H,), "ones"),
+                    (f"{p}{l}.post_attention_layernorm.weight", 0, (H,), "ones")]
+            if self.mla is None:
+                hd = self.head_dim
+                out += [(a + "q_proj.weight", dt, (self.heads * hd, H), "weight"),
+                        (a + "k_proj.weight", dt, (self.kv_heads * hd, H), "weight"),
+                        (a + "v_proj.weight", dt, (self.kv_heads * hd, H), "weight"),
+                        (a + "o_proj.weight", dt, (H, self.heads * hd), "weight")]
+            else:
+                q_lora, kv_lora, nope, rope, v = self.mla
+                if q_lora:
+                    out += [(a + "q_a_proj.weight", dt, (q_lora, H), "weight"),
+                            (a + "q_a_layernorm.weight", 0, (q_lora,), "ones"),
+                            (a + "q_b_proj.weight", dt, (self.heads * (nope + rope), q_lora), "weight")]
+                else:
+                    out.append((a + "q_proj.weight", dt, (self.heads * (nope + rope), H), "weight"))
+                out += [(a + "kv_a_proj_with_mqa.weight", dt, (kv_lora + rope, H), "weight"),
+                        (a + "kv_a_layernorm.weight", 0, (kv_lora,), "ones"),
+                        (a + "kv_b_proj.weight", dt, (self.heads * (nope + v), kv_lora), "weight"),
+                        (a + "o_proj.weight", dt, (H, self.heads * v), "weight")]
+            m = f"{p}{l}.mlp."
+            if l < self.first_dense:
+                I = self.dense_inter
+                out += [(m + "gate_proj.weight", dt, (I, H), "weight"), (m + "up_proj.weight", dt, (I, H), "weight"),
+                        (m + "down_proj.weight", dt, (H, I), "weight")]
+                continue
+            I = self.moe_inter
+            if self.style == "mixtral":
+                b = f"{p}{l}.block_sparse_moe."
+                out.append((b + "gate.weight", 0, (self.n_experts, H), "router"))
+                for e in range(self.n_experts):
+                    out += [(b + f"experts.{e}.w1.weight", dt, (I, H), "weight"),
+                            (b + f"experts.{e}.w3.weight", dt, (I, H), "weight"),
+                            (b + f"experts.{e}.w2.weight", dt, (H, I), "weight")]
+            else:
+                out.append((m + "gate.weight", 0, (self.n_experts, H), "router"))
+                for e in range(self.n_experts):
+                    out += [(m + f"experts.{e}.gate_proj.weight", dt, (I, H), "weight"),
+                            (m + f"experts.{e}.up_proj.weight", dt, (I, H), "weight"),
+                            (m + f"experts.{e}.down_proj.weight", dt, (H, I), "weight")]
+                if self.shared_inter:
+                    S = self.shared_inter
+                    out += [(m + "shared_experts.gate_proj.weight", dt, (S, H), "weight"),
+                            (m + "shared_experts.up_proj.weight", dt, (S, H), "weight"),
+                            (m + "shared_experts.down_proj.weight", dt, (H, S), "weight")]
+        return out
+
+
+MODEL_SHAPES = {
+    # configs[0]: tiny Mixtral, 2 layers, hidden 512, 8 heads (2 key/value
+    # heads: Mixtral's 4:1 grouping), 8 experts of 1408 top-2, vocab 32000,
+    # every big weight Q8_0 from N(0, 0.02).
+    "tiny_mixtral": ModelShape("tiny_mixtral", 512, 2, 8, 2, 64, 32000, 1408, 8, 2, L.DT_Q8_0, "mixtral",
+                               rope_theta=1e6, eps=1e-5, max_pos=32768),
+    # configs[4]: DeepSeek-V2-Lite, 27 layers, hidden 2048, 16 MLA heads
+    # (no query LoRA, kv_lora 512, 128 + 64 key dims, 128 value dims, YaRN
+    # factor 40 as its config states), layer 0 a dense 10944 MLP, then 64
+    # routed experts of 1408 top-6 (not renormalised) plus 2 shared experts
+    # (one 2816-wide MLP), vocab 102400, Q8_0 from N(0, 0.02).
+    "v2_lite": ModelShape("v2_lite", 2048, 27, 16, 16, 64, 102400, 1408, 64, 6, L.DT_Q8_0, "deepseek",
+                          dense_inter=10944, first_dense=1, shared_inter=2816, norm_topk=False,
+                          mla=(0, 512, 128, 64, 128),
+                          rope_scaling={"type": "yarn", "factor": 40.0, "original_max_position_embeddings": 4096,
+                                        "beta_fast": 32.0, "beta_slow": 1.0, "mscale": 0.707,
+                                        "mscale_all_dim": 0.707},
+                          max_pos=163840),
+}
+
+
+def model_shape(name: str, **kw) -> ModelShape:
+    """A named model shape, optionally with fields replaced (fewer layers or
+    experts for quick cases)."""
+    return replace(MODEL_SHAPES[name], **kw)
+
+
+def _name_stream(name: str) -> int:
+    import zlib
+
+    return 0x1000000 + zlib.crc32(name.encode())
+
+
+def build_host_model(shape: ModelShape, seed: int):
+    """Every tensor of a random-init model in one host buffer (each on a
+    256-byte boundary): returns (config, HostCheckpoint).  Values come from
+    the library's seeded generator, one stream per tensor name, and are
+    quantised with the reference's quantiser."""
+    from .model import HostCheckpoint, HostTensor
+
+    plan = shape.plan()
+    offs, off = [], 0
+    for name, dt, sh, fill in plan:
+        rows = int(np.prod(sh[:-1])) if len(sh) > 1 else 1
+        offs.append(off)
+        off = _align(off + rows * row_bytes(dt, sh[-1]))
+    buf = np.empty(max(off, 256), dtype=np.uint8)
+    ck = HostCheckpoint(buf)
+    for (name, dt, sh, fill), o in zip(plan, offs):
+        rows = int(np.prod(sh[:-1])) if len(sh) > 1 else 1
+        n = rows * row_bytes(dt, sh[-1])
+        dst = buf[o:o + n]
+        if fill == "ones":
+            dst.view(np.float32)[:] = 1.0
+        elif fill == "router":
+            L.check(L.lib().moe_synth_normal(seed, _name_stream(name), rows * sh[-1], 0.0, shape.weight_std,
+                                             dst.ctypes.data_as(C.c_void_p)), "moe_synth_normal")
+        else:
+            _fill(dst, seed, _name_stream(name), dt, rows, sh[-1], 0.0, shape.weight_std)
+        ck.add(name, HostTensor(dt, tuple(sh), dst), o)
+    return shape.config(), ck
+
+
+def prompt_ids(seed: int, n: int, vocab: int) -> list:
+    """n token ids uniform in [0, vocab) (numpy's PCG64 seeded with `seed`)."""
+    return [int(v) for v in np.random.default_rng(seed).integers(0, vocab, n)]

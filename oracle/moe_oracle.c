@@ -645,3 +645,164 @@ void orc_expf_array(const float *x, float *y, size_t n) {
 #pragma omp parallel for schedule(static)
     for (size_t i = 0; i < n; i++) y[i] = expf(x[i]);
 }
+
+/* ======================================================= the model around it
+ * The rest of the reference's forward (src/model.rs:646-834), restated so
+ * that a whole model can run on the CPU path for the end-to-end checks:
+ * RMSNorm, the rotary embedding with its context-extension schemes, and the
+ * causal attention loop.  Projections reuse matmul, FFNs mlp_forward and
+ * orc_moe_forward. */
+
+/* src/model.rs:211-216: scale = 1 / sqrt(sum(v*v) / n + eps) (Rust's f32
+ * Sum folds from -0.0 in order), out = v * scale * g.  `rows` rows of `n`
+ * values, `xs` / `os` apart. */
+void orc_rmsnorm_rows(const float *x, size_t rows, size_t n, size_t xs, const float *w, float eps, float *out,
+                      size_t os) {
+    for (size_t r = 0; r < rows; r++) {
+        const float *v = x + r * xs;
+        float *o = out + r * os;
+        float ss = -0.0f;
+        for (size_t i = 0; i < n; i++) {
+            float sq = v[i] * v[i];
+            ss += sq;
+        }
+        float mean = ss / (float)n;
+        float den = sqrtf(mean + eps);
+        float scale = 1.0f / den;
+        for (size_t i = 0; i < n; i++) {
+            float a = v[i] * scale;
+            o[i] = a * w[i];
+        }
+    }
+}
+
+/* src/model.rs:324-333: rotate pairs (i, i + half) of x[0..dim) by pos * inv[i]
+ * with f32 sin and cos (Rust's f32::sin_cos, glibc's sinf and cosf). */
+static void rope1(float *x, size_t dim, float pos, const float *inv, size_t n_inv) {
+    size_t half = dim / 2;
+    for (size_t i = 0; i < n_inv && i < half; i++) {
+        float ang = pos * inv[i];
+        float s = sinf(ang), c = cosf(ang);
+        float a = x[i], b = x[i + half];
+        float ac = a * c, bs = b * s, as = a * s, bc = b * c;
+        x[i] = ac - bs;
+        x[i + half] = as + bc;
+    }
+}
+
+/* The rotary embedding of `heads` heads (each `dim` values, `hs` apart,
+ * starting `off` into the row) of `rows` rows `rs` apart; row r is at
+ * position pos[r]. */
+void orc_rope_rows(float *x, size_t rows, size_t rs, size_t heads, size_t hs, size_t off, size_t dim,
+                   const int32_t *pos, const float *inv, size_t n_inv) {
+    for (size_t r = 0; r < rows; r++)
+        for (size_t h = 0; h < heads; h++) rope1(x + r * rs + h * hs + off, dim, (float)pos[r], inv, n_inv);
+}
+
+/* src/spec.rs:89-145: per-pair inverse frequencies for a head of head_dim
+ * values.  kind: 0 none, 1 linear, 2 dynamic (NTK), 3 YaRN, 4 Llama 3. */
+void orc_inv_freqs(int kind, float theta, float factor, size_t original_ctx, float low_freq_factor,
+                   float high_freq_factor, float beta_fast, float beta_slow, size_t head_dim, float *out) {
+    size_t half = head_dim / 2;
+    float dim = (float)head_dim;
+    float s = factor > 1e-6f ? factor : 1e-6f;
+    float th = theta;
+    if (kind == 2) {
+        float d2 = dim - 2.0f;
+        if (d2 < 1.0f) d2 = 1.0f;
+        th = theta * powf(s, dim / d2);
+    }
+    for (size_t i = 0; i < half; i++) {
+        float e = -2.0f * (float)i / dim;
+        out[i] = powf(th, e);
+    }
+    if (kind == 1) {
+        for (size_t i = 0; i < half; i++) out[i] = out[i] / s;
+    } else if (kind == 4) {
+        float l = (float)original_ctx;
+        float lo_wave = l / low_freq_factor, hi_wave = l / high_freq_factor;
+        float span = high_freq_factor - low_freq_factor;
+        if (span < 1e-6f) span = 1e-6f;
+        for (size_t i = 0; i < half; i++) {
+            float f = out[i];
+            float wave = 2.0f * 3.14159265358979323846f / f;
+            if (wave > lo_wave) {
+                out[i] = f / s;
+            } else if (wave < hi_wave) {
+                out[i] = f;
+            } else {
+                float t = ((l / wave) - low_freq_factor) / span;
+                float a = (1.0f - t) * f / s;
+                float b = t * f;
+                out[i] = a + b;
+            }
+        }
+    } else if (kind == 3) {
+        float l = (float)original_ctx;
+        float ln_base = logf(theta);
+        if (ln_base < 1e-6f) ln_base = 1e-6f;
+        float twopi = 2.0f * 3.14159265358979323846f;
+        float bf = dim * logf(l / (beta_fast * twopi)) / (2.0f * ln_base);
+        float bs = dim * logf(l / (beta_slow * twopi)) / (2.0f * ln_base);
+        float low = floorf(bf), high = ceilf(bs);
+        float span = high - low;
+        if (span < 1e-3f) span = 1e-3f;
+        for (size_t i = 0; i < half; i++) {
+            float f = out[i];
+            float ramp = ((float)i - low) / span;
+            ramp = ramp < 0.0f ? 0.0f : (ramp > 1.0f ? 1.0f : ramp);
+            float a = (1.0f - ramp) * (f / s);
+            float b = ramp * f;
+            out[i] = a + b;
+        }
+    }
+}
+
+/* src/spec.rs:64-70, 147-160: the attention-scale multiplier (YaRN only). */
+static float yarn_mscale(float scale, float mscale) { return scale <= 1.0f ? 1.0f : 0.1f * mscale * logf(scale) + 1.0f; }
+float orc_attn_scale(int kind, float factor, float mscale, float mscale_all_dim, float attn_factor) {
+    if (kind != 3) return 1.0f;
+    if (mscale > 0.0f || mscale_all_dim > 0.0f) {
+        float num = yarn_mscale(factor, mscale), den = yarn_mscale(factor, mscale_all_dim);
+        if (den < 1e-6f) den = 1e-6f;
+        return num / den * attn_factor;
+    }
+    return yarn_mscale(factor, 1.0f) * attn_factor;
+}
+
+/* src/model.rs:797-831: causal scaled dot-product attention of t tokens at
+ * positions base .. base + t - 1 against the cache (rows of kd keys and vdim
+ * values per position; head h of a key is kd values [kvh * qd, +qd)).  Per
+ * (token, head): scores = dot(q, k_j) * scale for j in [lo, p] (lo = p + 1 -
+ * window for a windowed layer), softmax, then acc += w * v_j in position
+ * order from +0.  q is [t, heads * qd], out [t, heads * vd]. */
+void orc_attention(const float *q, const float *kc, const float *vc, size_t t, size_t base, size_t heads, size_t n_kv,
+                   size_t qd, size_t vd, float scale, size_t window, float *out) {
+    size_t kd = n_kv * qd, vdim = n_kv * vd;
+    size_t rep = heads / (n_kv > 0 ? n_kv : 1);
+#pragma omp parallel for schedule(dynamic, 1)
+    for (size_t idx = 0; idx < t * heads; idx++) {
+        size_t i = idx / heads, hi = idx % heads, p = base + i;
+        size_t lo = window ? (p + 1 > window ? p + 1 - window : 0) : 0;
+        size_t kvh = rep > 1 ? hi / rep : (hi < n_kv - 1 ? hi : n_kv - 1);
+        const float *qv = q + i * heads * qd + hi * qd;
+        size_t n = p + 1 - lo;
+        float *sc = (float *)malloc(n * sizeof(float));
+        for (size_t j = lo; j <= p; j++) {
+            float d = orc_dot(qv, kc + j * kd + kvh * qd, qd);
+            sc[j - lo] = d * scale;
+        }
+        softmax(sc, n);
+        float *acc = out + i * heads * vd + hi * vd;
+        for (size_t c = 0; c < vd; c++) acc[c] = 0.0f;
+        for (size_t k = 0; k < n; k++) {
+            const float *vj = vc + (lo + k) * vdim + kvh * vd;
+            float w = sc[k];
+            for (size_t c = 0; c < vd; c++) {
+                float prod = w * vj[c];
+                acc[c] += prod;
+            }
+        }
+        free(sc);
+    }
+}

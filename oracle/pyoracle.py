@@ -66,6 +66,12 @@ def lib() -> C.CDLL:
             "orc_mlp_forward": (None, [C.POINTER(QT), C.POINTER(QT), C.POINTER(QT), vp, C.c_int, vp]),
             "orc_expf": (C.c_float, [C.c_float]),
             "orc_expf_array": (None, [vp, vp, sz]),
+            "orc_rmsnorm_rows": (None, [vp, sz, sz, sz, vp, C.c_float, vp, sz]),
+            "orc_rope_rows": (None, [vp, sz, sz, sz, sz, sz, sz, vp, vp, sz]),
+            "orc_inv_freqs": (None, [C.c_int, C.c_float, C.c_float, sz, C.c_float, C.c_float, C.c_float, C.c_float,
+                                     sz, vp]),
+            "orc_attn_scale": (C.c_float, [C.c_int, C.c_float, C.c_float, C.c_float, C.c_float]),
+            "orc_attention": (None, [vp, vp, vp, sz, sz, sz, sz, sz, sz, C.c_float, sz, vp]),
             "orc_set_threads": (None, [C.c_int]),
             "orc_max_threads": (C.c_int, []),
         }
@@ -259,3 +265,241 @@ def from_host_layer(host) -> OracleLayer:
     return OracleLayer(H, E, s.top_k, router, experts, sigmoid=s.sigmoid, norm_topk=s.norm_topk,
                        routed_scale=s.routed_scale, n_group=s.n_group, topk_group=s.topk_group, e_bias=e_bias,
                        shared=shared, shared_gate=sg)
+
+
+# ------------------------------------------------------- the whole model
+
+
+def inv_freqs(rope, head_dim: int) -> np.ndarray:
+    """Rope::inv_freqs (src/spec.rs:89-145) for a rope description with the
+    reference's fields (kind 0 none, 1 linear, 2 dynamic, 3 YaRN, 4 Llama 3)."""
+    out = np.zeros(head_dim // 2, dtype=np.float32)
+    lib().orc_inv_freqs(rope.kind, rope.theta, rope.factor, rope.original_ctx, rope.low_freq_factor,
+                        rope.high_freq_factor, rope.beta_fast, rope.beta_slow, head_dim, _p(out))
+    return out
+
+
+def attn_scale(rope) -> np.float32:
+    return np.float32(lib().orc_attn_scale(rope.kind, rope.factor, rope.mscale, rope.mscale_all_dim,
+                                           rope.attn_factor))
+
+
+def rmsnorm_rows(x: np.ndarray, w: np.ndarray, eps: float, n: Optional[int] = None) -> np.ndarray:
+    """rmsnorm (src/model.rs:211-216) of every row of x (the first n values
+    of each row when n is given)."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    rows, width = x.shape
+    n = width if n is None else n
+    w = np.ascontiguousarray(w, dtype=np.float32)
+    out = np.empty((rows, n), dtype=np.float32)
+    lib().orc_rmsnorm_rows(_p(x), rows, n, width, _p(w), eps, _p(out), n)
+    return out
+
+
+class OracleModel:
+    """The reference's CPU forward of a whole decoder (src/model.rs:565-834)
+    over host tensors: `spec` carries the Spec fields (moe_amd.model.Spec),
+    `tensors` maps Hugging Face names to (dt, shape, uint8 bytes) records.
+    One sequence per State, as the reference runs them."""
+
+    def __init__(self, spec, tensors: dict):
+        self.spec, self.tensors = spec, tensors
+        s = spec
+        self._keep = []
+        self.inv = inv_freqs(s.rope, s.mla.qk_rope if s.mla else s.head_dim)
+        self.scale_mult = attn_scale(s.rope)
+        self.embed = self._qt("model.embed_tokens.weight")
+        self.out_norm = self._f32("model.norm.weight")
+        self.lm_head = self._qt("lm_head.weight") if "lm_head.weight" in tensors else self.embed
+        self.layers = [self._layer(l) for l in range(s.layers)]
+
+    # -- weights ---------------------------------------------------------
+    def _rec(self, name):
+        t = self.tensors[name]
+        return t.dt, t.shape, np.ascontiguousarray(t.data).view(np.uint8).reshape(-1)
+
+    def _qt(self, name, slab: Optional[int] = None):
+        dt, shape, data = self._rec(name)
+        rows, cols = (shape[-2] if len(shape) > 1 else 1), shape[-1]
+        if slab is not None:
+            n = row_bytes(dt, cols) * rows
+            data = data[slab * n:(slab + 1) * n]
+        self._keep.append(data)
+        return qt(dt, rows, cols, data)
+
+    def _qt_tuple(self, name, slab: Optional[int] = None):
+        dt, shape, data = self._rec(name)
+        rows, cols = (shape[-2] if len(shape) > 1 else 1), shape[-1]
+        if slab is not None:
+            n = row_bytes(dt, cols) * rows
+            data = data[slab * n:(slab + 1) * n]
+        return (dt, rows, cols, data)
+
+    def _f32(self, name, optional=False):
+        if name not in self.tensors:
+            if optional:
+                return None
+            raise KeyError(name)
+        dt, shape, data = self._rec(name)
+        assert dt == DT_F32, name
+        return data.view(np.float32)
+
+    def _layer(self, l: int) -> dict:
+        s, p = self.spec, f"{self.spec.prefix}{l}."
+        a = p + "self_attn."
+        lay = dict(ln1=self._f32(p + "input_layernorm.weight"), ln2=self._f32(p + "post_attention_layernorm.weight"),
+                   o=self._qt(a + "o_proj.weight"), window=s.windows[l] if l < len(s.windows) else None)
+        if s.mla is None:
+            lay.update(q=self._qt(a + "q_proj.weight"), k=self._qt(a + "k_proj.weight"), v=self._qt(a + "v_proj.weight"),
+                       bias=[self._f32(a + f"{m}_proj.bias", True) for m in "qkv"],
+                       q_norm=self._f32(a + "q_norm.weight", True), k_norm=self._f32(a + "k_norm.weight", True))
+        else:
+            has_qa = (a + "q_a_proj.weight") in self.tensors
+            lay.update(q_a=self._qt(a + "q_a_proj.weight") if has_qa else None,
+                       q_a_norm=self._f32(a + "q_a_layernorm.weight", True),
+                       q_b=self._qt(a + ("q_b_proj.weight" if has_qa else "q_proj.weight")),
+                       kv_a=self._qt(a + "kv_a_proj_with_mqa.weight"), kv_a_norm=self._f32(a + "kv_a_layernorm.weight"),
+                       kv_b=self._qt(a + "kv_b_proj.weight"))
+        m = p + "mlp."
+        router = m + "gate.weight" if (m + "gate.weight") in self.tensors else p + "block_sparse_moe.gate.weight"
+        if router in self.tensors:
+            lay["moe"] = self._moe(l, router)
+        else:
+            lay["mlp"] = tuple(self._qt(m + f"{n}_proj.weight") for n in ("gate", "up", "down"))
+        return lay
+
+    def _moe(self, l: int, router_name: str) -> "OracleLayer":
+        """The routed layer's tensors in any of the reference's three expert
+        layouts (src/model.rs:396-441)."""
+        s, p = self.spec, f"{self.spec.prefix}{l}."
+        m = p + "mlp."
+        router = self._f32(router_name).reshape(s.experts, s.hidden)
+        names = ("gate_proj", "up_proj", "down_proj")
+        experts = []
+        for e in range(s.experts):
+            trio = []
+            for w, n in enumerate(names):
+                if m + f"experts.{n}" in self.tensors:
+                    trio.append(self._qt_tuple(m + f"experts.{n}", e))
+                elif m + f"experts.{e}.{n}.weight" in self.tensors:
+                    trio.append(self._qt_tuple(m + f"experts.{e}.{n}.weight"))
+                else:
+                    trio.append(self._qt_tuple(p + f"block_sparse_moe.experts.{e}.{('w1', 'w3', 'w2')[w]}.weight"))
+            experts.append(trio)
+        shared = None
+        for stem in ("shared_experts", "shared_expert"):
+            if m + f"{stem}.gate_proj.weight" in self.tensors:
+                shared = [self._qt_tuple(m + f"{stem}.{n}.weight") for n in names]
+        return OracleLayer(s.hidden, s.experts, s.top_k, router, experts, sigmoid=s.sigmoid, norm_topk=s.norm_topk,
+                           routed_scale=s.routed_scale, n_group=s.n_group, topk_group=s.topk_group,
+                           e_bias=self._f32(m + "gate.e_score_correction_bias", True), shared=shared,
+                           shared_gate=self._f32(m + "shared_expert_gate.weight", True))
+
+    # -- the forward -----------------------------------------------------
+    def kv_dims(self):
+        s = self.spec
+        if s.mla:
+            return s.heads * (s.mla.qk_nope + s.mla.qk_rope), s.heads * s.mla.v_head
+        return s.kv_heads * s.head_dim, s.kv_heads * s.head_dim
+
+    def new_state(self, ctx: int) -> dict:
+        kd, vd = self.kv_dims()
+        return dict(pos=0, ctx=ctx, k=[np.zeros((ctx, kd), np.float32) for _ in self.layers],
+                    v=[np.zeros((ctx, vd), np.float32) for _ in self.layers])
+
+    def _attention(self, li: int, lay: dict, x: np.ndarray, st: dict) -> np.ndarray:
+        """Model::attention (src/model.rs:686-834)."""
+        s, t, base = self.spec, x.shape[0], st["pos"]
+        pos = np.arange(base, base + t, dtype=np.int32)
+        if s.mla is None:
+            qd = vd = s.head_dim
+            n_kv = s.kv_heads
+            q, k, v = matmul(lay["q"], x), matmul(lay["k"], x), matmul(lay["v"], x)
+            bufs = [q, k, v]
+            for i, b in enumerate(lay["bias"]):
+                if b is not None:
+                    flat = bufs[i].reshape(-1)
+                    flat += np.resize(b, flat.size)
+            for buf, heads, nrm in ((q, s.heads, lay["q_norm"]), (k, n_kv, lay["k_norm"])):
+                if nrm is not None:
+                    span = buf.shape[1] if nrm.size == buf.shape[1] else qd
+                    buf[:] = rmsnorm_rows(buf.reshape(-1, span), nrm, s.eps).reshape(buf.shape)
+                lib().orc_rope_rows(_p(buf), t, buf.shape[1], heads, qd, 0, qd, _p(pos), _p(self.inv), self.inv.size)
+            st["k"][li][base:base + t] = k
+            st["v"][li][base:base + t] = v
+        else:
+            m = s.mla
+            qd, vd, n_kv = m.qk_nope + m.qk_rope, m.v_head, s.heads
+            if lay["q_a"] is not None and lay["q_a_norm"] is not None:
+                q = matmul(lay["q_b"], rmsnorm_rows(matmul(lay["q_a"], x), lay["q_a_norm"], s.eps))
+            else:
+                q = matmul(lay["q_b"], x)
+            c = matmul(lay["kv_a"], x)
+            cn = rmsnorm_rows(c, lay["kv_a_norm"], s.eps, n=m.kv_lora)
+            kv = matmul(lay["kv_b"], cn).reshape(t, s.heads, m.qk_nope + m.v_head)
+            kpe = np.ascontiguousarray(c[:, m.kv_lora:])
+            lib().orc_rope_rows(_p(kpe), t, m.qk_rope, 1, 0, 0, m.qk_rope, _p(pos), _p(self.inv), self.inv.size)
+            lib().orc_rope_rows(_p(q), t, q.shape[1], s.heads, qd, m.qk_nope, m.qk_rope, _p(pos), _p(self.inv),
+                                self.inv.size)
+            kc = np.concatenate([kv[:, :, :m.qk_nope], np.broadcast_to(kpe[:, None, :], (t, s.heads, m.qk_rope))],
+                                axis=2)
+            st["k"][li][base:base + t] = kc.reshape(t, -1)
+            st["v"][li][base:base + t] = kv[:, :, m.qk_nope:].reshape(t, -1)
+        scale = np.float32(self.scale_mult / np.sqrt(np.float32(qd), dtype=np.float32))
+        out = self._attend(q, st["k"][li], st["v"][li], t, base, s.heads, n_kv, qd, vd, scale, lay["window"] or 0)
+        return matmul(lay["o"], out)
+
+    def _attend(self, q, kc, vc, t, base, heads, n_kv, qd, vd, scale, window) -> np.ndarray:
+        """The causal attention loop (src/model.rs:797-831)."""
+        q = np.ascontiguousarray(q, dtype=np.float32)
+        out = np.empty((t, heads * vd), dtype=np.float32)
+        lib().orc_attention(_p(q), _p(kc), _p(vc), t, base, heads, n_kv, qd, vd, float(scale), window, _p(out))
+        return out
+
+    def trunk(self, tokens, st: dict) -> np.ndarray:
+        """Model::trunk (src/model.rs:646-684): the residual stream [t, H]."""
+        s = self.spec
+        t = len(tokens)
+        assert t > 0 and st["pos"] + t <= st["ctx"], "context window exhausted"
+        e = self.embed
+        rb = row_bytes(e.dt, e.cols)
+        data = self.tensors["model.embed_tokens.weight"].data
+        x = np.empty((t, s.hidden), dtype=np.float32)
+        for i, tok in enumerate(tokens):
+            r = int(tok) % s.vocab
+            x[i] = dequant(e.dt, np.asarray(data[r * rb:(r + 1) * rb]), 1, e.cols)[0]
+        for li, lay in enumerate(self.layers):
+            n = rmsnorm_rows(x, lay["ln1"], s.eps)
+            x = x + self._attention(li, lay, n, st)
+            n = rmsnorm_rows(x, lay["ln2"], s.eps)
+            if "moe" in lay:
+                delta = lay["moe"].forward(n)[0]
+            else:
+                delta = mlp_forward(*lay["mlp"], n)
+            x = x + delta
+        st["pos"] += t
+        return x
+
+    def head(self, rows: np.ndarray) -> np.ndarray:
+        """Model::head (src/model.rs:636-642) of residual rows."""
+        return matmul(self.lm_head, rmsnorm_rows(rows, self.out_norm, self.spec.eps))
+
+    def forward(self, tokens, st: dict) -> np.ndarray:
+        """Model::forward: the logits of the last token."""
+        x = self.trunk(tokens, st)
+        return self.head(x[-1:])[0]
+
+    def forward_all(self, tokens, st: dict) -> np.ndarray:
+        """Model::forward_all: logits at every position."""
+        return self.head(self.trunk(tokens, st))
+
+    def generate_greedy(self, prompt, max_tokens: int, ctx: Optional[int] = None) -> list:
+        """Sampler::default (temp 0: the first index of the maximum,
+        src/sample.rs:87-95) in generate's loop (src/generate.rs:142-320)."""
+        st = self.new_state(ctx or len(prompt) + max_tokens)
+        logits = self.forward(list(prompt), st)
+        out = [int(np.argmax(logits))]
+        while len(out) < max_tokens:
+            logits = self.forward([out[-1]], st)
+            out.append(int(np.argmax(logits)))
+        return out

@@ -33,9 +33,20 @@ def record(test: str, case: str, err: float, **extra) -> None:
         pass
 
 
+PROGRESS_LOG = os.path.join(os.path.dirname(ERR_LOG), "progress.log")
+
+
 def log(msg: str) -> None:
-    print(f"[{time.strftime('%H:%M:%S')}] {msg}", flush=True)
+    """A progress line on stdout and in PROGRESS_LOG (which a captured test
+    run still shows growing while a long case runs)."""
+    line = f"[{time.strftime('%H:%M:%S')}] {msg}"
+    print(line, flush=True)
     sys.stdout.flush()
+    try:
+        with open(PROGRESS_LOG, "a") as f:
+            f.write(line + "\n")
+    except OSError:
+        pass
 
 
 def rel_err(got: np.ndarray, ref: np.ndarray) -> float:

@@ -238,3 +238,21 @@ def oracle_moe_fn(model: TinyModel, routing=None):
         return out
 
     return fn
+
+
+def host_tensors(name: str, quant_dt: Optional[int] = None):
+    """A fixture as the whole-model paths load it: (Spec, {name: HostTensor}),
+    every tensor F32 unless the pack rule (src/store.rs:418-429) stored it in
+    `quant_dt`."""
+    from moe_amd.model import HostTensor, Spec
+
+    m = TinyModel(name, quant_dt=quant_dt)
+    out = {}
+    for k, v in m.raw.items():
+        if k in m.packed:
+            dt, rows, cols, q = m.packed[k]
+            out[k] = HostTensor(dt, v.shape, np.ascontiguousarray(q).view(np.uint8).reshape(-1))
+        else:
+            out[k] = HostTensor(0, v.shape, np.ascontiguousarray(v).view(np.uint8).reshape(-1))
+    spec = Spec.derive(m.cfg, {k: t.shape for k, t in out.items()})
+    return m, spec, out

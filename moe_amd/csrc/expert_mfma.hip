@@ -45,6 +45,7 @@
 #include <hip/hip_fp16.h>
 #include <hip/hip_runtime.h>
 
+#include <cstdlib>
 #include <type_traits>
 
 #include "exact_math.h"
@@ -289,6 +290,24 @@ __device__ inline void dequant(const uint32_t *v, half8 (&bh)[2], half8 (&bl)[2]
     }
 }
 
+// Waves per SIMD of the MFMA kernels: 0 chooses per launch (below);
+// MOE_MFMA_SPLIT=1 or 2 forces one (for measurements).
+int mfma_split_forced() {
+    const char *e = getenv("MOE_MFMA_SPLIT");
+    return e && (e[0] == '1' || e[0] == '2') ? e[0] - '0' : 0;
+}
+const int g_mfma_split = mfma_split_forced();
+
+// Two waves per SIMD pay once a tile holds two or more 32-token MFMA tiles
+// (each wave of a pair then multiplies at least one): measured on MI355X,
+// -4% at 128 tokens per expert (Mixtral T=512) and -12% at 128 (Qwen3
+// T=2048) in gate/up time, +3% at 8 tokens per expert (Mixtral T=32),
+// where the second wave of each pair has no tile and only loads.
+int mfma_split_for(double tokens_per_group) {
+    if (g_mfma_split) return g_mfma_split;
+    return tokens_per_group >= 48.0 ? 2 : 1;
+}
+
 // Tile coordinates.  mode 0: routed tiles from the dispatch list; mode 1: the
 // shared expert over all T tokens.  The grid is walked in the order
 // (expert, N tile, M tile), M fastest, and each XCD (linear block id mod 8)
@@ -335,14 +354,25 @@ __device__ inline bool tile_of(const MfmaArgs &a, int mode, int gx, TileInfo &ti
     return true;
 }
 
-template <int DT, bool UP, int BM>
-__global__ __launch_bounds__(256, 1) __attribute__((amdgpu_waves_per_eu(1, 1))) void mfma_kernel(MfmaArgs a, int mode, int gx, int ksplit) {
+// SPLIT = 1: four waves, one per SIMD; wave w owns weight regions 2 w and
+// 2 w + 1 and every token tile.  SPLIT = 2: eight waves, two per SIMD; the
+// pair (w, w + 4) shares regions 2 w and 2 w + 1 (each wave loads one of
+// them) and splits the token tiles, wave w taking the first ceil(MT / 2)
+// and wave w + 4 the rest.  Both waves of a pair dequantise the same weight
+// step, which costs VALU time but no LDS traffic, and whenever one of them
+// waits for LDS, for the barrier or for its dequantisation, the other can
+// issue MFMAs.
+template <int DT, bool UP, int BM, int SPLIT>
+__global__ __launch_bounds__(256 * SPLIT, 1) __attribute__((amdgpu_waves_per_eu(SPLIT, SPLIT))) void mfma_kernel(MfmaArgs a, int mode, int gx, int ksplit) {
     using BL = BLay<DT>;
     constexpr int NS = ring_stages<DT, BM>();
     constexpr int MTMAX = BM / 32;        // 32-token MFMA tiles per block tile
+    constexpr int MWMAX = (MTMAX + SPLIT - 1) / SPLIT;  // tiles of one wave
     constexpr int AS = a_stage<BM>();     // bytes of one activation piece per stage
     constexpr int RS = 2 * AS + BL::stage;  // bytes of one ring stage
+    constexpr int NJ = 2 / SPLIT;         // weight regions one wave loads
     static_assert(NS == 3, "the step loop below assumes three stages");
+    static_assert(SPLIT == 1 || SPLIT == 2, "one or two waves per SIMD");
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
     int *src_row = reinterpret_cast<int *>(smem + NS * RS);
     int *dst_row = src_row + BM;
@@ -361,6 +391,8 @@ __global__ __launch_bounds__(256, 1) __attribute__((amdgpu_waves_per_eu(1, 1))) 
     const int nsteps = kspan / BK;
     const int tid = threadIdx.x, lane = tid & 63;
     const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int sw = wv & 3;                     // the SIMD's weight regions 2 sw, 2 sw + 1
+    const int half = SPLIT == 2 ? wv >> 2 : 0;  // which token tiles (SPLIT 2)
     const int Icol = ti.shared ? a.I_s : a.I;
     const int valid = min(BM, ti.n - ti.m0);
     const int mt = (valid + 31) / 32;
@@ -388,22 +420,30 @@ __global__ __launch_bounds__(256, 1) __attribute__((amdgpu_waves_per_eu(1, 1))) 
     const lds_p sm = (lds_p)smem;
     const int l32 = lane & 31, hf = lane >> 5;
 
-    // Activation DMA: instruction u of wave wv covers rows 8 i .. 8 i + 7,
-    // i = wv + 4 u; lane l takes row r = 8 i + l / 8 and stores slot l % 8 of
-    // that row's 128 bytes, which holds logical chunk (l % 8) ^ ((r / 2) % 8).
-    // Rows past the tile's tokens repeat token row 0 (their outputs are never
-    // stored).  The lo piece uses the same offsets in its own array.
+    // Activation DMA: the tile's rows come in groups of eight (group i =
+    // rows 8 i .. 8 i + 7, 1 KiB per piece at offset 1024 i of the stage);
+    // instruction u of wave wv loads group wv + 4 SPLIT u (modulo the tile's
+    // groups: a group loaded twice is written twice with the same bytes,
+    // before the barrier that publishes it).  Lane l takes row r = 8 i + l / 8
+    // and stores slot l % 8 of that row's 128 bytes, which holds logical
+    // chunk (l % 8) ^ ((r / 2) % 8).  Rows past the tile's tokens repeat
+    // token row 0 (their outputs are never stored).  The lo piece uses the
+    // same offsets in its own array.
     const uint32_t arow_bytes = (uint32_t)(UP ? a.H : Icol) * 2;
-    // Weight DMA: region j of wave wv holds 32 weight rows.  woff: per DMA
+    // Weight DMA: region 2 sw + j holds 32 weight rows; this wave loads the
+    // regions j of jj < NJ (SPLIT 1: both, SPLIT 2: j = half).  woff: per DMA
     // (the region's dwordx4 DMAs, then its dword DMAs) the lane's byte offset
     // in the weight matrix, without the step's K offset.
-    const uint8_t *wbase[2];
-    uint32_t woff[2][BL::inst];
+    const uint8_t *wbase[NJ];
+    uint32_t woff[NJ][BL::inst];
+    uint32_t wreg[NJ];
 #pragma unroll
-    for (int j = 0; j < 2; j++) {
+    for (int jj = 0; jj < NJ; jj++) {
+        const int j = SPLIT == 2 ? half : jj;
         const MatDev &W = (UP && j == 1) ? W1 : W0;
-        wbase[j] = W.ptr;
-        const int row0 = UP ? n0 + 32 * wv : n0 + 64 * wv + 32 * j;
+        wbase[jj] = W.ptr;
+        wreg[jj] = (uint32_t)(2 * sw + j);
+        const int row0 = UP ? n0 + 32 * sw : n0 + 64 * sw + 32 * j;
         int row = row0 + (lane & 31);
         if (row >= W.rows) row = 0;
 #pragma unroll
@@ -416,7 +456,7 @@ __global__ __launch_bounds__(256, 1) __attribute__((amdgpu_waves_per_eu(1, 1))) 
                 const int e = q >> 5;
                 off = e < BL::nd ? (uint32_t)row * W.stride + (uint32_t)(16 * BL::nx4 + 4 * e) : 0u;
             }
-            woff[j][i] = off;
+            woff[jj][i] = off;
         }
     }
     // The dequantisation's scale exponent of region j (gate, up: the two
@@ -431,24 +471,32 @@ __global__ __launch_bounds__(256, 1) __attribute__((amdgpu_waves_per_eu(1, 1))) 
     const uint32_t brow_x = 16u * l32;                 // row l32's X part within a region
     const uint32_t brow_d = BL::xbytes + 4u * l32;     // and its D part
 
-    floatx16 acc[MTMAX][2];
+    floatx16 acc[MWMAX][2];
 #pragma unroll
-    for (int t = 0; t < MTMAX; t++)
+    for (int t = 0; t < MWMAX; t++)
 #pragma unroll
         for (int j = 0; j < 2; j++) acc[t][j] = floatx16{};
 
-    auto run = [&](auto mt_c) {
+    // The step loop for a tile of MT 32-token tiles; this wave multiplies
+    // tiles T0 .. T0 + MW - 1 (MW may be 0: the wave then only loads).
+    auto run = [&](auto mt_c, auto mw_c, auto t0_c) {
         constexpr int MT = decltype(mt_c)::value;
-        constexpr int NA = 2 * MT;        // activation DMAs per wave per step (hi, then lo)
-        constexpr int NB = 2 * BL::inst;  // weight DMAs per wave per step
-        constexpr int ND = NA + NB;       // DMAs per wave per step
-        uint32_t aoffg[MT];               // activation source offsets (step 0)
+        constexpr int MW = decltype(mw_c)::value, T0 = decltype(t0_c)::value;
+        constexpr int MWR = MW > 0 ? MW : 1;  // array extent
+        constexpr int NG = 4 * MT;             // activation row groups per piece
+        constexpr int UA = (NG + 4 * SPLIT - 1) / (4 * SPLIT);  // of this wave
+        constexpr int NA = 2 * UA;             // activation DMAs per wave per step (hi, then lo)
+        constexpr int NB = NJ * BL::inst;      // weight DMAs per wave per step
+        constexpr int ND = NA + NB;            // DMAs per wave per step
+        uint32_t aoffg[UA], agrp[UA];          // source offsets (step 0) and LDS groups
 #pragma unroll
-        for (int u = 0; u < MT; u++) {
-            const int r = 8 * (wv + 4 * u) + (lane >> 3);
+        for (int u = 0; u < UA; u++) {
+            const int i = (wv + 4 * SPLIT * u) % NG;
+            const int r = 8 * i + (lane >> 3);
             const int sr = src_row[r < valid ? r : 0];
             aoffg[u] = (uint32_t)sr * arow_bytes + (uint32_t)kbeg * 2u +
                        (uint32_t)(((lane & 7) ^ ((r >> 1) & 7)) << 4);
+            agrp[u] = (uint32_t)i * 1024u;
         }
         // DMA d of step `step` into ring stage `st`: d < NA activations
         // (hi pieces, then lo), then the weight regions.  Steps past the end
@@ -458,18 +506,18 @@ __global__ __launch_bounds__(256, 1) __attribute__((amdgpu_waves_per_eu(1, 1))) 
             constexpr int d = decltype(d_c)::value;
             const int sc = step < nsteps ? step : nsteps - 1;
             if constexpr (d < NA) {
-                constexpr int p = d / MT, u = d % MT;
+                constexpr int p = d / UA, u = d % UA;
                 const uint16_t *src = p == 0 ? ahi : alo;
                 dma16(reinterpret_cast<const uint8_t *>(src) + (size_t)sc * (BK * 2), aoffg[u],
-                      lds0 + (uint32_t)st * 2 * AS + (uint32_t)p * AS + (uint32_t)(wv + 4 * u) * 1024u);
+                      lds0 + (uint32_t)st * 2 * AS + (uint32_t)p * AS + agrp[u]);
             } else {
-                constexpr int j = (d - NA) / BL::inst, i = (d - NA) % BL::inst;
-                const uint8_t *wb = wbase[j] + (size_t)(kbeg / 32 + 2 * sc) * Fmt<DT>::bytes;
-                const uint32_t lr = ldsB + (uint32_t)st * BL::stage + (uint32_t)(2 * wv + j) * BL::region;
+                constexpr int jj = (d - NA) / BL::inst, i = (d - NA) % BL::inst;
+                const uint8_t *wb = wbase[jj] + (size_t)(kbeg / 32 + 2 * sc) * Fmt<DT>::bytes;
+                const uint32_t lr = ldsB + (uint32_t)st * BL::stage + wreg[jj] * BL::region;
                 if constexpr (i < BL::ix)
-                    dma16(wb, woff[j][i], lr + 1024u * i);
+                    dma16(wb, woff[jj][i], lr + 1024u * i);
                 else
-                    dma4(wb, woff[j][i], lr + BL::xbytes + 256u * (i - BL::ix));
+                    dma4(wb, woff[jj][i], lr + BL::xbytes + 256u * (i - BL::ix));
             }
         };
         auto dma_from = [&](auto lo_c, auto hi_c, int step, int st, auto self) {
@@ -486,12 +534,12 @@ __global__ __launch_bounds__(256, 1) __attribute__((amdgpu_waves_per_eu(1, 1))) 
         // broadcasts); each lane then picks its dwords (Slots: base, or
         // base + 2 for the upper lane half).
         half8 bh[2][2][2], bl[2][2][2];  // [kb][j][m] hi and lo pieces
-        half8 ah[2][MT], al[2][MT];      // activation pieces of two groups
+        half8 ah[2][MWR], al[2][MWR];    // activation pieces of two groups
         uint32_t rowv[2][BL::rd];
         auto read_rows = [&](lds_p stage_b) {
 #pragma unroll
             for (int j = 0; j < 2; j++) {
-                const uint32_t reg = (uint32_t)(2 * wv + j) * BL::region;
+                const uint32_t reg = (uint32_t)(2 * sw + j) * BL::region;
 #pragma unroll
                 for (int x = 0; x < BL::nx4; x++) {
                     const u32x4l v =
@@ -519,52 +567,60 @@ __global__ __launch_bounds__(256, 1) __attribute__((amdgpu_waves_per_eu(1, 1))) 
         auto read_a = [&](lds_p sa, int g, int slot) {
             const lds_p p = sa + aoff[g];
 #pragma unroll
-            for (int t = 0; t < MT; t++) ah[slot][t] = lds_h8(p + 4096 * t), al[slot][t] = lds_h8(p + AS + 4096 * t);
+            for (int t = 0; t < MW; t++)
+                ah[slot][t] = lds_h8(p + 4096 * (T0 + t)), al[slot][t] = lds_h8(p + AS + 4096 * (T0 + t));
         };
         // MFMA pass q of tile i = 2 t + j for group (kb, m): q 0 = hi.lo,
         // 1 = lo.hi, 2 = hi.hi.  A group runs pass 0 over all its tiles, then
         // pass 1, then pass 2, so consecutive MFMAs never share an
-        // accumulator.
+        // accumulator (with one tile, the pair of regions still alternates).
         auto mfma = [&](int slot, int kb, int m, int q, int i) {
             const int t = i >> 1, j = i & 1;
             const half8 &A = q == 1 ? al[slot][t] : ah[slot][t];
             const half8 &B = q == 0 ? bl[kb][j][m] : bh[kb][j][m];
             acc[t][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(A, B, acc[t][j], 0, 0, 0);
         };
-        // One group's 6 MT MFMAs with DMAs [LO, HI) of step `step` spread
+        // One group's 6 MW MFMAs with DMAs [LO, HI) of step `step` spread
         // between them: a DMA that the memory pipeline cannot take yet stalls
         // this wave, not the MFMAs already queued.
         auto mfmas_dma = [&](int slot, int kb, int m, auto lo_c, auto hi_c, int step, int st) {
             constexpr int LO = decltype(lo_c)::value, HI = decltype(hi_c)::value;
-            constexpr int N = 6 * MT;
-            auto body = [&](auto i_c, auto self) {
-                constexpr int i = decltype(i_c)::value;
-                if constexpr (i < N) {
-                    mfma(slot, kb, m, i / (2 * MT), i % (2 * MT));
-                    dma_range(std::integral_constant<int, LO + i * (HI - LO) / N>{},
-                              std::integral_constant<int, LO + (i + 1) * (HI - LO) / N>{}, step, st);
-                    self(std::integral_constant<int, i + 1>{}, self);
-                }
-            };
-            body(std::integral_constant<int, 0>{}, body);
+            constexpr int N = 6 * MW;
+            if constexpr (N == 0) {
+                dma_range(lo_c, hi_c, step, st);
+            } else {
+                auto body = [&](auto i_c, auto self) {
+                    constexpr int i = decltype(i_c)::value;
+                    if constexpr (i < N) {
+                        mfma(slot, kb, m, i / (2 * MW), i % (2 * MW));
+                        dma_range(std::integral_constant<int, LO + i * (HI - LO) / N>{},
+                                  std::integral_constant<int, LO + (i + 1) * (HI - LO) / N>{}, step, st);
+                        self(std::integral_constant<int, i + 1>{}, self);
+                    }
+                };
+                body(std::integral_constant<int, 0>{}, body);
+            }
         };
         auto mfmas = [&](int slot, int kb, int m) {
 #pragma unroll
             for (int q = 0; q < 3; q++)
 #pragma unroll
-                for (int i = 0; i < 2 * MT; i++) mfma(slot, kb, m, q, i);
+                for (int i = 0; i < 2 * MW; i++) mfma(slot, kb, m, q, i);
         };
         using I0 = std::integral_constant<int, 0>;
         using I1 = std::integral_constant<int, 1>;
+        constexpr bool work = MW > 0;
 
         const lds_p smB = sm + NS * 2 * AS;
         // Prologue: steps 0 .. NS - 1 into stages 0 .. NS - 1, then wait for
         // step 0.
         for (int p = 0; p < NS; p++) dma_range(I0{}, std::integral_constant<int, ND>{}, p, p);
         wait_vm_barrier<(NS - 1) * ND>();
-        read_a(sm, 0, 0);
-        read_rows(smB);
-        dequant_raw(I0{});
+        if constexpr (work) {
+            read_a(sm, 0, 0);
+            read_rows(smB);
+            dequant_raw(I0{});
+        }
         int st = 0;
         // At the wait in group 2 of step s this wave's outstanding loads are
         // those of steps s + 1 .. s + NS - 1 (ND each, in order); leaving the
@@ -577,57 +633,79 @@ __global__ __launch_bounds__(256, 1) __attribute__((amdgpu_waves_per_eu(1, 1))) 
         for (int s = 0; s < nsteps; s++) {
             const lds_p sa = sm + st * 2 * AS;
             const int st1 = st + 1 == NS ? 0 : st + 1;
-            // g = 0 (kb 0, m 0); read group 1.
-            read_a(sa, 1, 1);
-            __builtin_amdgcn_sched_barrier(0);
-            mfmas(0, 0, 0);
-            // g = 1 (kb 0, m 1): dequantise block 1, read group 2.
-            dequant_raw(I1{});
-            read_a(sa, 2, 0);
-            mfmas(1, 0, 1);
-            __builtin_amdgcn_sched_barrier(0);
-            // g = 2 (kb 1, m 0): read group 3; then wait for this wave's
-            // loads of step s + 1 and meet the other waves.
-            read_a(sa, 3, 1);
-            mfmas(0, 1, 0);
-            __builtin_amdgcn_sched_barrier(0);
+            if constexpr (work) {
+                // g = 0 (kb 0, m 0); read group 1.
+                read_a(sa, 1, 1);
+                __builtin_amdgcn_sched_barrier(0);
+                mfmas(0, 0, 0);
+                // g = 1 (kb 0, m 1): dequantise block 1, read group 2.
+                dequant_raw(I1{});
+                read_a(sa, 2, 0);
+                mfmas(1, 0, 1);
+                __builtin_amdgcn_sched_barrier(0);
+                // g = 2 (kb 1, m 0): read group 3; then wait for this wave's
+                // loads of step s + 1 and meet the other waves.
+                read_a(sa, 3, 1);
+                mfmas(0, 1, 0);
+                __builtin_amdgcn_sched_barrier(0);
+            }
             wait_vm_barrier<WAIT>();
             __builtin_amdgcn_sched_barrier(0);
             // g = 3 (kb 1, m 1): step s + 1's group 0 and weight rows; step
             // s + NS's DMAs into this step's stage.
-            read_a(sm + st1 * 2 * AS, 0, 0);
-            read_rows(smB + st1 * BL::stage);
+            if constexpr (work) {
+                read_a(sm + st1 * 2 * AS, 0, 0);
+                read_rows(smB + st1 * BL::stage);
+            }
             __builtin_amdgcn_sched_barrier(0);
             mfmas_dma(1, 1, 1, I0{}, std::integral_constant<int, ND>{}, s + NS, st);
-            dequant_raw(I0{});
+            if constexpr (work) dequant_raw(I0{});
             __builtin_amdgcn_sched_barrier(0);
             st = st1;
         }
     };
     static_assert(MTMAX == 5 || MTMAX == 4, "one case per 32-token tile count");
+    // Tiles of this wave: SPLIT 1 all MT; SPLIT 2 the first ceil(MT / 2)
+    // (half 0) or the rest (half 1).
+    auto run_mt = [&](auto mt_c) {
+        constexpr int MT = decltype(mt_c)::value;
+        if constexpr (SPLIT == 1) {
+            run(mt_c, mt_c, std::integral_constant<int, 0>{});
+        } else {
+            constexpr int MA = (MT + 1) / 2;
+            if (half == 0)
+                run(mt_c, std::integral_constant<int, MA>{}, std::integral_constant<int, 0>{});
+            else
+                run(mt_c, std::integral_constant<int, MT - MA>{}, std::integral_constant<int, MA>{});
+        }
+    };
     switch (mt) {
-    case 1: run(std::integral_constant<int, 1>{}); break;
-    case 2: run(std::integral_constant<int, 2>{}); break;
-    case 3: run(std::integral_constant<int, 3>{}); break;
-    case 4: run(std::integral_constant<int, 4>{}); break;
+    case 1: run_mt(std::integral_constant<int, 1>{}); break;
+    case 2: run_mt(std::integral_constant<int, 2>{}); break;
+    case 3: run_mt(std::integral_constant<int, 3>{}); break;
+    case 4: run_mt(std::integral_constant<int, 4>{}); break;
     default:
-        if constexpr (MTMAX == 5) run(std::integral_constant<int, MTMAX>{});
+        if constexpr (MTMAX == 5) run_mt(std::integral_constant<int, MTMAX>{});
         break;
     }
     wait_vm<0>();
+
+    // This wave's tiles: t0 .. t0 + mw - 1.
+    const int ma = SPLIT == 2 ? (mt + 1) / 2 : mt;
+    const int t0 = half ? ma : 0, mw = half ? mt - ma : ma;
 
     // ---- epilogue: lane holds C[32 t + 8 (v / 4) + 4 hf + v % 4][column l32 of set j],
     // scaled by 2^(ex_row + wexp).
     if (UP) {
         float *hout = ti.shared ? a.hs : a.h;
-        const int col = n0 + 32 * wv + l32;
+        const int col = n0 + 32 * sw + l32;
         if (col < W0.rows) {
 #pragma unroll
-            for (int t = 0; t < MTMAX; t++) {
-                if (t >= mt) continue;
+            for (int t = 0; t < MWMAX; t++) {
+                if (t >= mw) continue;
 #pragma unroll
                 for (int v = 0; v < 16; v++) {
-                    const int r = 32 * t + 8 * (v / 4) + 4 * hf + (v % 4);
+                    const int r = 32 * (t0 + t) + 8 * (v / 4) + 4 * hf + (v % 4);
                     const int d = dst_row[r];
                     if (d < 0) continue;
                     const int e = ex_row[r];
@@ -640,14 +718,14 @@ __global__ __launch_bounds__(256, 1) __attribute__((amdgpu_waves_per_eu(1, 1))) 
         float *yout = ti.shared ? a.ys + ti.ksplit * a.yspart : a.y + ti.ksplit * a.ypart;
 #pragma unroll
         for (int j = 0; j < 2; j++) {
-            const int col = n0 + 64 * wv + 32 * j + l32;
+            const int col = n0 + 64 * sw + 32 * j + l32;
             if (col >= W0.rows) continue;
 #pragma unroll
-            for (int t = 0; t < MTMAX; t++) {
-                if (t >= mt) continue;
+            for (int t = 0; t < MWMAX; t++) {
+                if (t >= mw) continue;
 #pragma unroll
                 for (int v = 0; v < 16; v++) {
-                    const int r = 32 * t + 8 * (v / 4) + 4 * hf + (v % 4);
+                    const int r = 32 * (t0 + t) + 8 * (v / 4) + 4 * hf + (v % 4);
                     const int d = dst_row[r];
                     if (d >= 0) yout[(size_t)d * a.H + col] = ldexpf(acc[t][j][v], -(ex_row[r] + wexp0));
                 }
@@ -656,30 +734,38 @@ __global__ __launch_bounds__(256, 1) __attribute__((amdgpu_waves_per_eu(1, 1))) 
     }
 }
 
-template <int DT, bool UP, int BM>
-hipError_t launch_one(dim3 grid, const MfmaArgs &a, int mode, int ksplit, hipStream_t s) {
+template <int DT, bool UP, int BM, int SPLIT>
+hipError_t launch_split(dim3 grid, const MfmaArgs &a, int mode, int ksplit, hipStream_t s) {
     constexpr int lds = lds_bytes<DT, BM>();
-    static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void *>(&mfma_kernel<DT, UP, BM>),
-                                                       hipFuncAttributeMaxDynamicSharedMemorySize, lds);
+    static const hipError_t attr = hipFuncSetAttribute(
+        reinterpret_cast<const void *>(&mfma_kernel<DT, UP, BM, SPLIT>), hipFuncAttributeMaxDynamicSharedMemorySize,
+        lds);
     if (attr != hipSuccess) return attr;
-    hipLaunchKernelGGL((mfma_kernel<DT, UP, BM>), grid, dim3(256), lds, s, a, mode, (int)grid.x, ksplit);
+    hipLaunchKernelGGL((mfma_kernel<DT, UP, BM, SPLIT>), grid, dim3(256 * SPLIT), lds, s, a, mode, (int)grid.x,
+                       ksplit);
     return hipGetLastError();
+}
+template <int DT, bool UP, int BM>
+hipError_t launch_one(dim3 grid, const MfmaArgs &a, int mode, int ksplit, int split, hipStream_t s) {
+    return split == 2 ? launch_split<DT, UP, BM, 2>(grid, a, mode, ksplit, s)
+                      : launch_split<DT, UP, BM, 1>(grid, a, mode, ksplit, s);
 }
 
 template <bool UP>
-hipError_t launch_dt(int dt, int bm, dim3 grid, const MfmaArgs &a, int mode, int ksplit, hipStream_t s) {
+hipError_t launch_dt(int dt, int bm, dim3 grid, const MfmaArgs &a, int mode, int ksplit, int split,
+                     hipStream_t s) {
     if (bm == 160) {
         switch (dt) {
-        case MOE_DT_Q4_0: return launch_one<MOE_DT_Q4_0, UP, 160>(grid, a, mode, ksplit, s);
-        case MOE_DT_Q5_0: return launch_one<MOE_DT_Q5_0, UP, 160>(grid, a, mode, ksplit, s);
+        case MOE_DT_Q4_0: return launch_one<MOE_DT_Q4_0, UP, 160>(grid, a, mode, ksplit, split, s);
+        case MOE_DT_Q5_0: return launch_one<MOE_DT_Q5_0, UP, 160>(grid, a, mode, ksplit, split, s);
         default: return hipErrorInvalidValue;
         }
     }
     if (bm != 128) return hipErrorInvalidValue;
     switch (dt) {
-    case MOE_DT_Q8_0: return launch_one<MOE_DT_Q8_0, UP, 128>(grid, a, mode, ksplit, s);
-    case MOE_DT_Q4_0: return launch_one<MOE_DT_Q4_0, UP, 128>(grid, a, mode, ksplit, s);
-    case MOE_DT_Q5_0: return launch_one<MOE_DT_Q5_0, UP, 128>(grid, a, mode, ksplit, s);
+    case MOE_DT_Q8_0: return launch_one<MOE_DT_Q8_0, UP, 128>(grid, a, mode, ksplit, split, s);
+    case MOE_DT_Q4_0: return launch_one<MOE_DT_Q4_0, UP, 128>(grid, a, mode, ksplit, split, s);
+    case MOE_DT_Q5_0: return launch_one<MOE_DT_Q5_0, UP, 128>(grid, a, mode, ksplit, split, s);
     default: return hipErrorInvalidValue;
     }
 }
@@ -786,11 +872,14 @@ hipError_t launch_mfma(bool up, const MfmaArgs &a, int bm, const ExpertDev &e0, 
     const int cols = up ? BW / 2 : BW;
     const int ks = up ? 1 : a.ksplit;
     dim3 grid(a.max_tiles, (m.rows + cols - 1) / cols, ks);
-    hipError_t err = up ? launch_dt<true>(m.dt, bm, grid, a, 0, ks, s) : launch_dt<false>(m.dt, bm, grid, a, 0, ks, s);
+    const int sp = mfma_split_for(a.E > 0 ? (double)a.T * a.k / a.E : 0.0);
+    hipError_t err = up ? launch_dt<true>(m.dt, bm, grid, a, 0, ks, sp, s)
+                        : launch_dt<false>(m.dt, bm, grid, a, 0, ks, sp, s);
     if (err != hipSuccess || !sh) return err;
     const MatDev &ms = up ? sh->m[0] : sh->m[2];
     dim3 gs((a.T + bm - 1) / bm, (ms.rows + cols - 1) / cols, ks);
-    return up ? launch_dt<true>(ms.dt, bm, gs, a, 1, ks, s) : launch_dt<false>(ms.dt, bm, gs, a, 1, ks, s);
+    const int ss = mfma_split_for((double)a.T);
+    return up ? launch_dt<true>(ms.dt, bm, gs, a, 1, ks, ss, s) : launch_dt<false>(ms.dt, bm, gs, a, 1, ks, ss, s);
 }
 
 hipError_t launch_mfma_single(bool up, const MfmaArgs &a, int bm, const ExpertDev &ex, hipStream_t s) {
@@ -798,7 +887,8 @@ hipError_t launch_mfma_single(bool up, const MfmaArgs &a, int bm, const ExpertDe
     const int cols = up ? BW / 2 : BW;
     const int ks = up ? 1 : a.ksplit;
     dim3 gs((a.T + bm - 1) / bm, (m.rows + cols - 1) / cols, ks);
-    return up ? launch_dt<true>(m.dt, bm, gs, a, 1, ks, s) : launch_dt<false>(m.dt, bm, gs, a, 1, ks, s);
+    const int sp = mfma_split_for((double)a.T);
+    return up ? launch_dt<true>(m.dt, bm, gs, a, 1, ks, sp, s) : launch_dt<false>(m.dt, bm, gs, a, 1, ks, sp, s);
 }
 
 hipError_t launch_split_rows(const float *src, int rows, int cols, uint16_t *hi, uint16_t *lo, int32_t *ex,

@@ -567,6 +567,7 @@ int forward_on(moe_layer *L, const CallState &c, Workspace &w, const float *x, i
         m.I = L->I;
         m.I_s = L->I_s;
         m.E = L->E;
+        m.k = k;
         // Routed tiles: sum over experts of ceil(n_e / bm) <= t k / bm +
         // (experts with tokens); the shared expert's tiles follow them.
         m.max_tiles = t * k / bm + std::min(L->E, t * k) + 1;

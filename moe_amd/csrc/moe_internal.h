@@ -235,6 +235,7 @@ struct MfmaArgs {
     float *y, *ys;                // f32 [T*k, H], [T, H]
     size_t ypart, yspart;         // elements between the K parts of y, ys
     int T, H, I, I_s, E;
+    int k = 1;                    // experts per token (routed launches)
     int max_tiles;                // grid width of the routed launch: >= the routed tiles
     int shared_tiles;             // tiles of the shared expert at the end of the tile list (0 if none)
     int ksplit;                   // down projection: K parts (1, 2 or 4), part p written at y + p * ypart

@@ -50,11 +50,7 @@ __device__ inline MatDev mat_of(const MatDev *m) {
 
 // ------------------------------------------------------------- encoding
 
-// One wavefront per 64-value unit, one value per lane: lanes 0..31 form
-// block 0, 32..63 block 1.  The block's largest magnitude and the sums of
-// its codes come from shuffles inside each half; every lane then writes its
-// own three level bytes (the unit's bytes i, 64 + i and 128 + i), and lanes
-// 0 and 32 their block's s3, q01 and q2.  Same values as qact_block.
+// One wavefront per 64-value unit (qact_wave_encode).
 __global__ __launch_bounds__(256) void qenc_kernel(const float *__restrict__ src, int rows, int cols,
                                                    uint8_t *__restrict__ dst) {
     const int units = cols / 64;
@@ -64,24 +60,7 @@ __global__ __launch_bounds__(256) void qenc_kernel(const float *__restrict__ src
     for (long long w = w0; w < n; w += nw) {
         const long long r = w / units;
         const int u = (int)(w - r * units);
-        const float v = gload(src + r * cols + 64 * u + lane);
-        float amax = fmaxf(0.0f, fabsf(v));  // as the sequential fold from 0
-#pragma unroll
-        for (int m = 16; m >= 1; m >>= 1) amax = fmaxf(amax, __shfl_xor(amax, m, 64));
-        int a0, a1, a2;
-        qact_encode(v, qact_inv(amax), a0, a1, a2);
-        int q01 = 254 * a0 + a1, q2 = a2;
-#pragma unroll
-        for (int m = 16; m >= 1; m >>= 1) q01 += __shfl_xor(q01, m, 64), q2 += __shfl_xor(q2, m, 64);
-        uint8_t *unit = dst + (size_t)w * kQUnitBytes;
-        gstore(unit + lane, (uint8_t)(a0 & 0xff));
-        gstore(unit + 64 + lane, (uint8_t)(a1 & 0xff));
-        gstore(unit + 128 + lane, (uint8_t)(a2 & 0xff));
-        if ((lane & 31) == 0) {
-            gstore(reinterpret_cast<float *>(unit + 4 * kQS) + (lane >> 5), qact_s3(amax));
-            gstore(reinterpret_cast<int32_t *>(unit + 4 * kQ01) + (lane >> 5), q01);
-            gstore(reinterpret_cast<int32_t *>(unit + 4 * kQ2) + (lane >> 5), q2);
-        }
+        qact_wave_encode(gload(src + r * cols + 64 * u + lane), dst + (size_t)w * kQUnitBytes, lane);
     }
 }
 

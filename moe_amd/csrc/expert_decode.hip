@@ -15,9 +15,11 @@
 //    expert's forward at src/model.rs:925-935.  Persistent waves stream rows
 //    with several rows' weights in flight; each block first encodes x into
 //    LDS.
+//  * decode_hq_kernel: every selected expert's h (f32) to activation units,
+//    one wavefront per 64-value unit, once for all down blocks.
 //  * decode_down_kernel: a block owns ranges of output rows and one group of
-//    waves per selected expert; each lane encodes its units of the experts'
-//    h (f32) in registers, streams their down rows and combines each row in
+//    waves per selected expert; each lane loads its units of the experts'
+//    h, streams their down rows and combines each row in
 //    LDS: out = sum over the
 //    selected experts in ascending order of w * y, from +0, separate
 //    multiply and add (src/model.rs:842, 936-942); plus the shared expert
@@ -179,12 +181,30 @@ __global__ __launch_bounds__(256) void decode_up_kernel(DecodeArgs a, const floa
 
 // --------------------------------------------------------------- down
 //
+// Units of h.  Wave w of the grid encodes unit w of the list (routed task
+// t's units t * I/64 .. , then the shared expert's).  With one token each
+// selected expert has one permuted row, so task t's h is row t of a.h (the
+// dispatch kernel points the task there); the units of a task that is not
+// live encode a row nobody wrote this call and are never read.
+__global__ __launch_bounds__(256) void decode_hq_kernel(DecodeArgs a) {
+    const int ur = a.I / 64, us = a.n_shared ? a.I_s / 64 : 0;
+    const int n = a.k_bound * ur + us;
+    const int lane = threadIdx.x & 63;
+    const int w = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (w >= n) return;
+    const bool routed = w < a.k_bound * ur;
+    const int t = routed ? w / ur : a.k_bound;
+    const int u = routed ? w - t * ur : w - a.k_bound * ur;
+    const float *h = routed ? a.h + (size_t)t * a.I : a.hs;
+    qact_wave_encode(gload(h + 64 * u + lane), a.hq + ((size_t)t * a.hq_units + u) * kQUnitBytes, lane);
+}
+
 // A block owns output row ranges r = blockIdx.x, + gridDim.x, ... of `rb`
 // rows and one group of waves per task: routed task i (the i-th selected
 // expert, ascending) owns waves [i * ks_r, (i + 1) * ks_r), the shared
-// expert the ks_s waves after them.  Each lane first encodes its unit of its
-// task's h (f32) into registers; each wave then streams the task's down
-// rows of each range, NBUF - 1 ranges ahead.  Row slices leave their sums in
+// expert the ks_s waves after them.  Each lane first loads its units of its
+// task's h; each wave then streams the task's down rows of each range,
+// NBUF - 1 ranges ahead.  Row slices leave their sums in
 // LDS; after a barrier the block combines each row in the reference's
 // order.  Lanes own one unit (UPL = 1: CG lanes per row slice, 64 / CG slices
 // per wave, or ks = 4 waves of 64 lanes for rows wider than 128 units) or
@@ -306,24 +326,16 @@ __global__ __launch_bounds__(NTHR) void decode_down_kernel(DecodeArgs a, int rb,
         down_lane<DT_S>(tasks, a.k_bound, wv, ks_r, ks_s, rb, L);
     else
         down_lane<DT_R>(tasks, a.k_bound, wv, ks_r, ks_s, rb, L);
-    // The lane encodes its units of its task's h (f32, from the gate/up
-    // kernel) itself, before its weights stream.
-    // With one unit per lane its 64 values load first, then the first
-    // ranges' weights, and the encoding runs while those are in flight
-    // (loads retire in order, so waiting for h does not wait for them).
+    // The lane's units of its task's h (encoded by decode_hq_kernel) load
+    // first, then the first ranges' weights (loads retire in order, so
+    // waiting for the units does not wait for the weights).  Unconditional:
+    // lanes without a unit read task 0's first unit.
     uint32_t xa[UPL][kQUnitDw];
-    const float *hv = tasks[L.task].h;
     const int u0 = L.kw * 64 + (threadIdx.x & 63) % L.cg;
-    float hraw[64];
-    if constexpr (UPL == 1) {
-        // Unconditional (lanes without a unit read task 0's first), so that
-        // the encoding below waits for these loads only.
-        qact_unit_load((L.active && L.live[0]) ? hv + (size_t)u0 * 64 : tasks[0].h, hraw);
-    } else if (L.active) {
+    const uint8_t *ub = a.hq + (size_t)L.task * a.hq_units * kQUnitBytes;
 #pragma unroll
-        for (int j = 0; j < UPL; j++)
-            if (L.live[j]) qact_unit_from_f32(hv + (size_t)(u0 + 64 * j) * 64, xa[j]);
-    }
+    for (int j = 0; j < UPL; j++)
+        qact_unit_gload((L.active && L.live[j]) ? ub + (size_t)(u0 + 64 * j) * kQUnitBytes : a.hq, xa[j]);
     uint32_t w[NBUF][RS][UPL][DW];
     auto load = [&](int it, uint32_t (&buf)[RS][UPL][DW]) {
         const int range = blockIdx.x + it * gridDim.x;
@@ -334,11 +346,6 @@ __global__ __launch_bounds__(NTHR) void decode_down_kernel(DecodeArgs a, int rb,
     };
 #pragma unroll
     for (int b = 0; b + 1 < NBUF; b++) load(b, w[b]);
-    // Keep every prologue load ahead of the encoding (the scheduler would
-    // otherwise sink some of them below it, where they wait for it).
-    __builtin_amdgcn_sched_barrier(0);
-    if constexpr (UPL == 1)
-        if (L.active && L.live[0]) qact_unit_encode(hraw, xa[0]);
 
     // Selected experts (live routed tasks come first).
     int nh = 0;
@@ -490,6 +497,16 @@ hipError_t launch_decode_up(const DecodeArgs &a, const float *x, int dt_routed, 
     sh.k_bound = 0;
     sh.tasks = a.tasks + a.k_bound;  // the shared expert's entry
     return go(dt_shared, sh, a.I_s / slices, 1);
+}
+
+hipError_t launch_decode_encode(const DecodeArgs &a, hipStream_t s) {
+    if (!a.hq || a.I % 64 || (a.n_shared && a.I_s % 64) || a.I / 64 > a.hq_units ||
+        (a.n_shared && a.I_s / 64 > a.hq_units))
+        return hipErrorInvalidValue;
+    const int n = a.k_bound * (a.I / 64) + (a.n_shared ? a.I_s / 64 : 0);
+    if (n == 0) return hipSuccess;
+    hipLaunchKernelGGL(decode_hq_kernel, dim3((n + 3) / 4), dim3(256), 0, s, a);
+    return hipGetLastError();
 }
 
 hipError_t launch_decode_down(const DecodeArgs &a, int dt_routed, int dt_shared, hipStream_t s) {

@@ -25,7 +25,9 @@
 //                putting the row's largest |v| in [2^14, 2^15): 22
 //                significant bits (the dropped lo.lo term and the rounding
 //                of lo are ~2^-22 of a product);
-// the epilogue multiplies by 2^-(ex + wexp), which is exact.
+// the epilogue multiplies by 2^-(ex + wexp), which is exact.  SwiGLU's
+// sigmoid uses the hardware exp (v_exp_f32, about 1 ulp), as the other
+// fast paths do; only routing needs glibc's expf bit for bit.
 //
 // Operands reach LDS by DMA (global_load_lds), never through VGPRs:
 //   activations  16-byte chunks of each token row, for hi and lo alike; the
@@ -48,7 +50,6 @@
 #include <cstdlib>
 #include <type_traits>
 
-#include "exact_math.h"
 #include "gmem.h"
 #include "moe_internal.h"
 
@@ -710,7 +711,7 @@ __global__ __launch_bounds__(256 * SPLIT, 1) __attribute__((amdgpu_waves_per_eu(
                     if (d < 0) continue;
                     const int e = ex_row[r];
                     const float g = ldexpf(acc[t][0][v], -(e + wexp0)), u = ldexpf(acc[t][1][v], -(e + wexp1));
-                    hout[(size_t)d * Icol + col] = (g / (1.0f + expf_exact(-g))) * u;
+                    hout[(size_t)d * Icol + col] = (g / (1.0f + __expf(-g))) * u;
                 }
             }
         }

@@ -269,6 +269,7 @@ size_t ws_layout(const moe_layer *L, int max_t, int k, Workspace *w, char *base)
         {(void **)&x.xq, Tb * (H / 64) * kQUnitBytes},
         {(void **)&x.hq, Tb * k * (I / 64) * kQUnitBytes},
         {(void **)&x.hsq, Tb * (Is / 64) * kQUnitBytes},
+        {(void **)&x.dq, L->decode_ok ? (size_t)(k + 1) * (std::max(I, Is) / 64) * kQUnitBytes : 0},
         {(void **)&x.h, T * k * I * 4},
         {(void **)&x.hs, T * Is * 4},
         {(void **)&x.y, y_rows * H * 4},
@@ -454,7 +455,7 @@ int forward_on(moe_layer *L, const CallState &c, Workspace &w, const float *x, i
     if (path == kDecode) {
         const int dt_r = L->experts_host[0].m[0].dt;
         const int dt_s = L->has_shared ? L->experts_host[L->E].m[0].dt : dt_r;
-        if (t != 1 || !decode_fits(L->I, L->I_s, k, L->has_shared, dt_r, dt_s)) path = kGemv;
+        if (t != 1 || !L->decode_ok || !decode_fits(L->I, L->I_s, k, L->has_shared, dt_r, dt_s)) path = kGemv;
     }
     if (path == kMfma && !mfma_fits(t, k, L->H, L->I, L->has_shared ? L->I_s : 0)) path = kGemv;
     const int bm = path == kMfma ? L->mfma_bm : path == kBatch ? batch_tile_tokens(L->H, t, k, L->E) : 0;
@@ -480,10 +481,17 @@ int forward_on(moe_layer *L, const CallState &c, Workspace &w, const float *x, i
         d.E = L->E;
         d.k_bound = k;
         d.n_shared = L->has_shared ? 1 : 0;
+        d.hq = w.dq;
+        d.hq_units = std::max(L->I, L->has_shared ? L->I_s : 0) / 64;
         const int dt_r = e0.m[0].dt, dt_s = sh ? sh->m[0].dt : dt_r;
         rc = stage(L, c.profile, 3, s, [&] {
             e = launch_decode_up(d, x, dt_r, dt_s, s);
             return e == hipSuccess ? MOE_OK : hip_fail(e, "one-token gate/up kernel");
+        });
+        if (rc) return rc;
+        rc = stage(L, c.profile, 6, s, [&] {
+            e = launch_decode_encode(d, s);
+            return e == hipSuccess ? MOE_OK : hip_fail(e, "one-token encoding of h");
         });
         if (rc) return rc;
         return stage(L, c.profile, 4, s, [&] {

@@ -103,6 +103,7 @@ struct Workspace {
     uint8_t *xq = nullptr;        // [batch_t, H/64] activation units (few-tokens path)
     uint8_t *hq = nullptr;        // [batch_t * k, I/64] units of h
     uint8_t *hsq = nullptr;       // [batch_t, I_s/64] units of hs
+    uint8_t *dq = nullptr;        // [k + 1, max(I, I_s)/64] units of the one-token path's h rows
     int batch_t = 0;              // tokens the unit buffers have room for
     float *h = nullptr;           // [T*k, I] routed SwiGLU activations (f32)
     float *hs = nullptr;          // [T, I_s] shared-expert activations
@@ -206,6 +207,8 @@ struct DecodeArgs {
     int H, I, I_s, E;
     int k_bound;                  // routed tasks launched (>= hits[0])
     int n_shared;                 // 1 if the shared expert is part of the launch
+    uint8_t *hq;                  // activation units of h: task t's unit u at (t * hq_units + u) * kQUnitBytes
+    int hq_units;                 // unit slots per task (max(I, I_s) / 64)
 };
 // Whether the one-token kernels take these widths and formats, and whether
 // a down-projection block holds k routed experts (and the shared one).
@@ -213,7 +216,9 @@ constexpr int kDecodeMaxWaves = 16;  // waves of a down-projection block
 bool decode_supported(int H, int I, int I_s, int dt_routed, int dt_shared);
 bool decode_fits(int I, int I_s, int k, int has_shared, int dt_routed, int dt_shared);
 hipError_t launch_decode_up(const DecodeArgs &a, const float *x, int dt_routed, int dt_shared, hipStream_t s);
-// The down projection and combine; every lane encodes its own units of h.
+// Every live task's h (f32) to activation units at a.hq, one wavefront per unit.
+hipError_t launch_decode_encode(const DecodeArgs &a, hipStream_t s);
+// The down projection and combine over the units of h.
 hipError_t launch_decode_down(const DecodeArgs &a, int dt_routed, int dt_shared, hipStream_t s);
 
 // Prefill-path grouped GEMMs on MFMA in f32 precision: activations and the

@@ -76,45 +76,21 @@ __device__ inline QBlock qact_block(const float (&v)[32]) {
     return q;
 }
 
-// A whole unit in registers, laid out as in memory: the same bits
-// qact_block_put stores.  Loading (64 values, 16-byte aligned, global
-// memory) and encoding are separate so a caller can issue other loads in
-// between.
-typedef float qa_f32x4 __attribute__((ext_vector_type(4)));
-__device__ inline void qact_unit_load(const float *v, float (&f)[64]) {
-    // Global loads (not flat ones, which LDS waits would also wait for).
-    typedef const __attribute__((address_space(1))) qa_f32x4 *g4p;
-    const g4p s4 = (g4p)v;
+typedef uint32_t qa_u32x4 __attribute__((ext_vector_type(4)));
+
+// A unit from global memory (16-byte aligned) into registers.
+__device__ inline void qact_unit_gload(const uint8_t *unit, uint32_t (&x)[kQUnitDw]) {
+    typedef const __attribute__((address_space(1))) qa_u32x4 *g4p;
+    const g4p p = (g4p)unit;
 #pragma unroll
-    for (int i = 0; i < 16; i++) {
-        const qa_f32x4 t = s4[i];
-        f[4 * i] = t.x, f[4 * i + 1] = t.y, f[4 * i + 2] = t.z, f[4 * i + 3] = t.w;
+    for (int i = 0; i < kQUnitDw / 4; i++) {
+        const qa_u32x4 t = p[i];
+        x[4 * i] = t.x, x[4 * i + 1] = t.y, x[4 * i + 2] = t.z, x[4 * i + 3] = t.w;
     }
-}
-__device__ inline void qact_unit_encode(const float (&f)[64], uint32_t (&x)[kQUnitDw]) {
-#pragma unroll
-    for (int b = 0; b < 2; b++) {
-        float v[32];
-#pragma unroll
-        for (int i = 0; i < 32; i++) v[i] = f[32 * b + i];
-        const QBlock q = qact_block(v);
-#pragma unroll
-        for (int d = 0; d < 8; d++) x[8 * b + d] = q.w0[d], x[kQA1 + 8 * b + d] = q.w1[d], x[kQA2 + 8 * b + d] = q.w2[d];
-        x[kQS + b] = __float_as_uint(q.s3);
-        x[kQ01 + b] = (uint32_t)q.q01;
-        x[kQ2 + b] = (uint32_t)q.q2;
-    }
-    x[54] = 0u, x[55] = 0u;
-}
-__device__ inline void qact_unit_from_f32(const float *v, uint32_t (&x)[kQUnitDw]) {
-    float f[64];
-    qact_unit_load(v, f);
-    qact_unit_encode(f, x);
 }
 
 // Store an encoded block into a unit (16-byte aligned) through pointers of
 // address space AS (1: global, 3: LDS).
-typedef uint32_t qa_u32x4 __attribute__((ext_vector_type(4)));
 template <int AS>
 __device__ inline void qact_block_put(const QBlock &q, uint8_t *unit, int half) {
     typedef __attribute__((address_space(AS))) qa_u32x4 *v4p;
@@ -130,6 +106,35 @@ __device__ inline void qact_block_put(const QBlock &q, uint8_t *unit, int half) 
     ((fp)(unit + 4 * kQS))[half] = q.s3;
     ((ip)(unit + 4 * kQ01))[half] = q.q01;
     ((ip)(unit + 4 * kQ2))[half] = q.q2;
+}
+
+// One wavefront encodes one unit, one value per lane: lanes 0..31 form
+// block 0, 32..63 block 1.  The block's largest magnitude and the sums of
+// its codes come from shuffles inside each half; every lane writes its own
+// three level bytes (the unit's bytes i, 64 + i and 128 + i), and lanes 0
+// and 32 their block's s3, q01 and q2.  Same bits as qact_block: the
+// maximum and the integer sums do not depend on the order they are taken
+// in.
+__device__ inline void qact_wave_encode(float v, uint8_t *unit, int lane) {
+    float amax = fmaxf(0.0f, fabsf(v));  // as the sequential fold from 0
+#pragma unroll
+    for (int m = 16; m >= 1; m >>= 1) amax = fmaxf(amax, __shfl_xor(amax, m, 64));
+    int a0, a1, a2;
+    qact_encode(v, qact_inv(amax), a0, a1, a2);
+    int q01 = 254 * a0 + a1, q2 = a2;
+#pragma unroll
+    for (int m = 16; m >= 1; m >>= 1) q01 += __shfl_xor(q01, m, 64), q2 += __shfl_xor(q2, m, 64);
+    typedef __attribute__((address_space(1))) uint8_t *g8;
+    typedef __attribute__((address_space(1))) float *gf;
+    typedef __attribute__((address_space(1))) int32_t *gi;
+    ((g8)unit)[lane] = (uint8_t)(a0 & 0xff);
+    ((g8)unit)[64 + lane] = (uint8_t)(a1 & 0xff);
+    ((g8)unit)[128 + lane] = (uint8_t)(a2 & 0xff);
+    if ((lane & 31) == 0) {
+        ((gf)(unit + 4 * kQS))[lane >> 5] = qact_s3(amax);
+        ((gi)(unit + 4 * kQ01))[lane >> 5] = q01;
+        ((gi)(unit + 4 * kQ2))[lane >> 5] = q2;
+    }
 }
 
 }  // namespace moe

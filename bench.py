@@ -227,6 +227,69 @@ def summarize_trace(trace_dir: str, out_md: str, title: str, command: str) -> in
     return 0
 
 
+COUNTER_PASSES = [
+    "GRBM_GUI_ACTIVE SQ_BUSY_CYCLES SQ_VALU_MFMA_BUSY_CYCLES SQ_INSTS_MFMA SQ_WAVE_CYCLES SQ_WAIT_INST_ANY "
+    "SQ_INSTS_VALU SQ_INSTS_LDS",
+    "SQ_ACTIVE_INST_VALU SQ_ACTIVE_INST_LDS SQ_ACTIVE_INST_ANY SQ_WAIT_ANY SQ_INST_CYCLES_SALU SQ_INSTS_SALU "
+    "SQ_WAVES SQ_LDS_BANK_CONFLICT",
+]
+COUNTER_BENCH = "bench.py --no-cpu --steps 3 --warmup 1 --tokens 512 --batch-tokens 0 --copies 2"
+
+
+def summarize_counters(dirs: list, out_md: str) -> int:
+    """The MFMA kernels' counters at T=512 from rocprofv3 --pmc passes (one
+    directory per COUNTER_PASSES entry, each holding bench_counter_collection.csv
+    and bench_kernel_trace.csv): clock, MFMA-busy share and instruction mix
+    per launch of the gate/up and down kernels of the largest grid."""
+    import csv
+    import re
+
+    agg, dur, grids = {}, {}, {}
+    for d in dirs:
+        for r in csv.DictReader(open(os.path.join(d, "bench_counter_collection.csv"))):
+            m = re.search(r"::(\w+_kernel(<[^>]*>)?)", r["Kernel_Name"])
+            if not m or not m.group(1).startswith("mfma_kernel"):
+                continue
+            key = (m.group(1), int(r["Grid_Size"]))
+            agg.setdefault(key, {}).setdefault(r["Counter_Name"], {})[r["Dispatch_Id"]] = float(r["Counter_Value"])
+        for r in csv.DictReader(open(os.path.join(d, "bench_kernel_trace.csv"))):
+            m = re.search(r"::(\w+_kernel(<[^>]*>)?)", r["Kernel_Name"])
+            if not m or not m.group(1).startswith("mfma_kernel"):
+                continue
+            grid = int(r["Grid_Size_X"]) * int(r["Grid_Size_Y"]) * int(r["Grid_Size_Z"])
+            dur.setdefault((m.group(1), grid), []).append((int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3)
+    rows = []
+    for name in sorted({k[0] for k in agg}):
+        key = max((k for k in agg if k[0] == name), key=lambda k: k[1])
+        c = {n: sum(v.values()) / len(v) for n, v in agg[key].items()}
+        ds = dur.get(key) or [float("nan")]
+        rows.append((key, c, sum(ds) / len(ds)))
+    simds = 1024
+    lines = [f"# MFMA expert kernels (Mixtral shape, Q4_0, T=512): clock, MFMA busy, instruction mix", "",
+             "Counter passes (from the repo root on the GPU box; at most 8 SQ counters per pass):", ""]
+    for i, p in enumerate(COUNTER_PASSES):
+        lines.append(f"    cd /tmp && export TMPDIR=/tmp && rocprofv3 --kernel-trace --pmc {p} --output-format csv "
+                     f"-d $REPO/gpurun_out/mfma_pmc{i + 1} -o bench -- python3 $REPO/{COUNTER_BENCH}")
+    lines += ["", "then `python bench.py --summarize-counters gpurun_out/mfma_pmc1 gpurun_out/mfma_pmc2 OUT`.",
+              "Counters are summed over the device per dispatch and averaged over dispatches; GRBM_GUI_ACTIVE "
+              "sums the 8 XCDs, SQ_VALU_MFMA_BUSY_CYCLES the 1024 SIMDs.  Launches under counter collection are "
+              "serialised, so durations run a little long; the ratios are what the text uses.", "",
+              "| kernel | grid | duration µs | clock GHz | MFMA insts | busy cycles / MFMA | MFMA busy % of cycles "
+              "| VALU per MFMA | LDS insts | SALU insts | LDS bank conflicts |",
+              "|---|---|---|---|---|---|---|---|---|---|---|"]
+    for (name, grid), c, d in rows:
+        cyc = c.get("GRBM_GUI_ACTIVE", 0.0) / 8
+        mf, bz = c.get("SQ_INSTS_MFMA", 0.0), c.get("SQ_VALU_MFMA_BUSY_CYCLES", 0.0)
+        lines.append(f"| `{name}` | {grid} | {d:.1f} | {cyc / d / 1e3:.2f} | {mf:.3g} | {bz / mf if mf else 0:.1f} | "
+                     f"{100 * bz / simds / cyc if cyc else 0:.1f} | "
+                     f"{(c.get('SQ_INSTS_VALU', 0.0) - mf) / mf if mf else 0:.2f} | {c.get('SQ_INSTS_LDS', 0):.3g} | "
+                     f"{c.get('SQ_INSTS_SALU', 0):.3g} | {c.get('SQ_LDS_BANK_CONFLICT', 0):.3g} |")
+    with open(out_md, "w") as f:
+        f.write("\n".join(lines) + "\n")
+    print(json.dumps(dict(written=out_md, kernels=len(rows))))
+    return 0
+
+
 def traffic_of(kernel_prefix: str):
     """HBM bytes per launch of the kernel whose name starts with
     kernel_prefix, from the committed counter summary (None if absent).  The
@@ -258,6 +321,9 @@ def main() -> int:
                     help="write the HBM traffic summary from two rocprofv3 counter passes and exit")
     ap.add_argument("--summarize-trace", nargs=2, metavar=("TRACE_DIR", "OUT_MD"),
                     help="write a markdown table of kernel durations from a rocprofv3 kernel trace and exit")
+    ap.add_argument("--summarize-counters", nargs="+", metavar="DIR",
+                    help="write the MFMA kernels' counter summary from the rocprofv3 passes of COUNTER_PASSES "
+                         "(directories, then the output markdown path) and exit")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="only copy MIB MiB device-to-device 5 times (a plain copy kernel of known size, the "
                          "reference point for the FETCH_SIZE / WRITE_SIZE counters) and exit")
@@ -270,6 +336,8 @@ def main() -> int:
         return copy_calibration(args.copy_calibration)
     if args.summarize_pmc:
         return summarize_pmc(args.summarize_pmc[0], args.summarize_pmc[1], TRAFFIC_FILE)
+    if args.summarize_counters:
+        return summarize_counters(args.summarize_counters[:-1], args.summarize_counters[-1])
     if args.summarize_trace:
         return summarize_trace(args.summarize_trace[0], args.summarize_trace[1],
                                "Mixtral-8x7B-shape routed layer (Q4_0, top-2), T=1, T=32 and T=512: kernel durations",

@@ -312,7 +312,8 @@ int moe_mla_kv_store(const float *kv, const float *c, int64_t c_stride, int32_t 
 /* Causal attention (src/model.rs:790-831): row r of q (heads x qd values,
  * q_stride apart) belongs to sequence seq[r] at position pos[r] and attends
  * to cache positions [lo, pos[r]] of that sequence (lo = pos + 1 - window
- * for window > 0, else 0), head h reading kv head h / (heads / n_kv).
+ * for window > 0, else 0), head h reading kv head h / (heads / n_kv) when
+ * heads / n_kv > 1, else kv head min(h, n_kv - 1).
  * Cache layout: [sequence][ctx][n_kv * qd] keys, [sequence][ctx][n_kv * vd]
  * values.  out row r: heads x vd values.  max_pos bounds every pos[r]. */
 int moe_attention(const float *q, int64_t q_stride, int32_t rows, int32_t heads, int32_t n_kv, int32_t qd,

@@ -203,12 +203,16 @@ size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
 
 // Whether the few-tokens kernels beat MFMA tiles.  Their cost is the
 // weight bytes of every tile (an expert's weights are read once per tile of
-// nt tokens, at about twice the MFMA kernels' rate); measured on MI355X they
-// win while the hit experts average at most 1.5 tiles' worth of tokens.
+// nt tokens).  Measured on MI355X against the three-pass MFMA kernels: with
+// two-token tiles they win while the hit experts average at most 4 tokens
+// (Qwen3 T=64: 0.275 against 0.306 ms; Mixtral T=16 even; V2-Lite T=64 at
+// 6 tokens loses, 0.426 against 0.390), with one-token tiles (rows wider
+// than 4096) at most 1.5 (DeepSeek-V3 T=32: 1.11 against 1.31 ms; T=64 at
+// 2 tokens loses, 2.09 against 1.55).
 bool batch_pays(int t, int k, int E, int nt) {
     if (t < 2 || t > kBatchMaxT) return false;
     const long long rows = (long long)t * k, hit = std::min<long long>(E, rows);
-    return 2 * rows <= 3LL * nt * hit;
+    return nt >= 2 ? rows <= 4 * hit : 2 * rows <= 3 * hit;
 }
 
 // Byte layout of a workspace for up to max_t tokens of k experts each.

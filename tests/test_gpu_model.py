@@ -14,19 +14,11 @@ import time
 import numpy as np
 import pytest
 
-from gpu_util import TOL, log, record, rel_err
+from gpu_util import MODEL_TOL, TOL, log, record, rel_err
 from tiny_model import host_tensors
 
 pytestmark = pytest.mark.gpu
 
-# Bar of whole-model logits: max |gpu - oracle| / max |oracle| over a call's
-# logits.  Every operation is f32 (the projections and routed layers within
-# TOL of the oracle's products, the norms, rope and attention in f32 with
-# their own summation order); the differences compound over the layers.
-# Measured on MI355X: 1e-7 .. 1e-6 on the GQA fixtures and config 1, 3e-7 ..
-# 1.7e-5 on the mla fixture, whose logits move 4.8e-6 when one norm weight
-# moves by one ulp on the CPU path (the GQA fixtures move 2.2e-7).
-MODEL_TOL = 5e-5
 
 
 @pytest.fixture(scope="module")

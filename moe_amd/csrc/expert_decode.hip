@@ -301,6 +301,7 @@ __device__ inline void down_combine(const DecodeArgs &a, const DecodeTask *tasks
             if (a.has_gate) v = v * tasks[a.k_bound].w;
             out = out + v;
         }
+        if (a.addend) out = out + gload(a.addend + j);
         gstore(a.out + j, out);
         if (a.residual) gstore(a.residual + j, gload(a.residual + j) + out);
     }
@@ -449,21 +450,25 @@ int down_rs(int dt_r, int dt_s, int upl, bool big_block) {
 
 }  // namespace
 
+bool decode_shared_apart(int I, int I_s, int dt_routed, int dt_shared) {
+    // One down launch holds both formats only as Q4_0 + Q5_0 (the kernel's
+    // two-format instance), and one number of units per lane.
+    const bool fmt = dt_shared == dt_routed || (dt_routed == MOE_DT_Q4_0 && dt_shared == MOE_DT_Q5_0);
+    return !fmt || upl_of(I / 64) != upl_of(I_s / 64);
+}
+
 bool decode_supported(int H, int I, int I_s, int dt_routed, int dt_shared) {
     auto width = [](int cols) { return cols > 0 && cols % 64 == 0 && cols / 64 <= 256; };
     if (!width(H) || H / 64 > 128 || !width(I) || !qfmt(dt_routed)) return false;
-    if (I_s > 0) {
-        if (!width(I_s) || !qfmt(dt_shared)) return false;
-        // One down launch: both formats in one kernel, and the same units per lane.
-        const bool fmt = dt_shared == dt_routed || (dt_routed == MOE_DT_Q4_0 && dt_shared == MOE_DT_Q5_0);
-        if (!fmt || upl_of(I / 64) != upl_of(I_s / 64)) return false;
-    }
+    if (I_s > 0 && (!width(I_s) || !qfmt(dt_shared))) return false;
     return true;
 }
 
 bool decode_fits(int I, int I_s, int k, int has_shared, int dt_routed, int dt_shared) {
-    const int waves = k * down_ks(I / 64) + (has_shared ? down_ks(I_s / 64) : 0);
+    const bool apart = has_shared && decode_shared_apart(I, I_s, dt_routed, dt_shared);
+    const int waves = k * down_ks(I / 64) + (has_shared && !apart ? down_ks(I_s / 64) : 0);
     if (waves > kDecodeMaxWaves) return false;
+    if (apart) return down_ks(I_s / 64) <= kDecodeMaxWaves;
     if (!has_shared) return true;
     // Every task's row slices must split a range evenly.
     const int lo = std::min(down_slices(I / 64), down_slices(I_s / 64));
@@ -510,6 +515,26 @@ hipError_t launch_decode_encode(const DecodeArgs &a, hipStream_t s) {
 }
 
 hipError_t launch_decode_down(const DecodeArgs &a, int dt_routed, int dt_shared, hipStream_t s) {
+    if (a.n_shared && decode_shared_apart(a.I, a.I_s, dt_routed, dt_shared)) {
+        // The shared expert alone first, its gated output into a.ys; then
+        // the routed experts, adding it after their sum (the order of the
+        // one-launch combine).
+        if (!a.ys) return hipErrorInvalidValue;
+        DecodeArgs sh = a;
+        sh.k_bound = 0;
+        sh.tasks = a.tasks + a.k_bound;
+        sh.hq = a.hq + (size_t)a.k_bound * a.hq_units * kQUnitBytes;
+        sh.I = a.I_s;
+        sh.out = a.ys;
+        sh.residual = nullptr;
+        sh.addend = nullptr;
+        hipError_t e = launch_decode_down(sh, dt_shared, dt_shared, s);
+        if (e != hipSuccess) return e;
+        DecodeArgs rt = a;
+        rt.n_shared = 0;
+        rt.addend = a.ys;
+        return launch_decode_down(rt, dt_routed, dt_routed, s);
+    }
     const int ur = a.I / 64, us = a.n_shared ? a.I_s / 64 : ur;
     const int upl = upl_of(ur);
     const int ks_r = down_ks(ur), ks_s = a.n_shared ? down_ks(us) : 1;

@@ -487,6 +487,7 @@ int forward_on(moe_layer *L, const CallState &c, Workspace &w, const float *x, i
         d.n_shared = L->has_shared ? 1 : 0;
         d.hq = w.dq;
         d.hq_units = std::max(L->I, L->has_shared ? L->I_s : 0) / 64;
+        d.ys = w.ys;  // the shared expert's output when its down launch is separate
         const int dt_r = e0.m[0].dt, dt_s = sh ? sh->m[0].dt : dt_r;
         rc = stage(L, c.profile, 3, s, [&] {
             e = launch_decode_up(d, x, dt_r, dt_s, s);

@@ -209,6 +209,8 @@ struct DecodeArgs {
     int n_shared;                 // 1 if the shared expert is part of the launch
     uint8_t *hq;                  // activation units of h: task t's unit u at (t * hq_units + u) * kQUnitBytes
     int hq_units;                 // unit slots per task (max(I, I_s) / 64)
+    const float *addend;          // [H] added to out after the routed sum (the shared expert's gated output
+                                  // when it needs a down launch of its own), or null
 };
 // Whether the one-token kernels take these widths and formats, and whether
 // a down-projection block holds k routed experts (and the shared one).
@@ -220,6 +222,9 @@ hipError_t launch_decode_up(const DecodeArgs &a, const float *x, int dt_routed, 
 hipError_t launch_decode_encode(const DecodeArgs &a, hipStream_t s);
 // The down projection and combine over the units of h.
 hipError_t launch_decode_down(const DecodeArgs &a, int dt_routed, int dt_shared, hipStream_t s);
+// Whether the shared expert's down projection runs as a launch of its own
+// (its format, or its units per lane, differ from the routed experts').
+bool decode_shared_apart(int I, int I_s, int dt_routed, int dt_shared);
 
 // Prefill-path grouped GEMMs on MFMA in f32 precision: activations and the
 // dequantised weights are each split into two f16 pieces (hi + lo, exact for

@@ -123,9 +123,10 @@ LAYER_CASES = [
     ("mixtral", 32, 3), ("v2_lite", 32, 3), ("deepseek_v3", 64, 3),
     # MFMA with 128-token tiles (Q8_0) across tile boundaries, GEMV at many tokens
     ("qwen3", 300, 3), ("tiny_mixtral", 257, 3), ("qwen3", 128, 2),
-    # Qwen2-MoE: the shared expert's sigmoid gate on every path (decode takes
-    # the GEMV here: its 5632-wide shared rows need two units per lane)
-    ("qwen2_moe", 1, None), ("qwen2_moe", 1, 2), ("qwen2_moe", 6, 5), ("qwen2_moe", 64, None),
+    # Qwen2-MoE: the shared expert's sigmoid gate on every path (one token:
+    # its 5632-wide shared rows need two units per lane, the routed 1408-wide
+    # rows one, so the shared down projection runs as a launch of its own)
+    ("qwen2_moe", 1, None), ("qwen2_moe", 1, 4), ("qwen2_moe", 1, 2), ("qwen2_moe", 6, 5), ("qwen2_moe", 64, None),
     ("qwen2_moe", 64, 3), ("qwen2_moe", 17, 2), ("qwen2_moe", 512, None),
 ]
 

@@ -773,47 +773,75 @@ hipError_t launch_dt(int dt, int bm, dim3 grid, const MfmaArgs &a, int mode, int
 
 // ---- activation pieces ------------------------------------------------------
 // One block per row: the row's largest magnitude (a max over the block),
-// then every value's scaled hi and lo pieces, four values per thread step.
+// then every value's scaled hi and lo pieces.  Rows of up to 16384 values
+// stay in registers between the two (one read of the row); wider rows are
+// read twice.
 typedef float f32x4 __attribute__((ext_vector_type(4)));
-__global__ __launch_bounds__(256) void split_rows_kernel(const float *__restrict__ src, int cols,
-                                                         uint16_t *__restrict__ hi, uint16_t *__restrict__ lo,
-                                                         int32_t *__restrict__ ex) {
-    __shared__ float part[4];
-    const size_t row = blockIdx.x;
-    const f32x4 *s4 = reinterpret_cast<const f32x4 *>(src + row * cols);
-    const int n4 = cols / 4;
-    float m = 0.0f;
-    for (int i = threadIdx.x; i < n4; i += 256) {
-        const f32x4 v = gload(s4 + i);
-        m = fmaxf(m, fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
-    }
-#pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
-    if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = m;
-    __syncthreads();
-    m = fmaxf(fmaxf(part[0], part[1]), fmaxf(part[2], part[3]));
+typedef uint16_t u16x4 __attribute__((ext_vector_type(4)));
+constexpr int kSplitCached4 = 16;  // float4 per thread kept in registers
+
+__device__ inline int split_exponent(float m) {
     int e = 0;
     if (m > 0.0f && m <= 3.402823466e38f) {
         int fe;
         (void)frexpf(m, &fe);  // m in [2^(fe-1), 2^fe)
         e = 15 - fe;
     }
-    if (threadIdx.x == 0) ex[row] = e;
-    typedef uint16_t u16x4 __attribute__((ext_vector_type(4)));
+    return e;
+}
+__device__ inline void split_store(const f32x4 &v, int e, u16x4 *h4, u16x4 *l4) {
+    u16x4 ho, lw;
+#pragma unroll
+    for (int c = 0; c < 4; c++) {
+        const float x = ldexpf(v[c], e);
+        const __half h = __float2half_rn(x);
+        ho[c] = __half_as_ushort(h);
+        lw[c] = __half_as_ushort(__float2half_rn(x - __half2float(h)));
+    }
+    gstore(h4, ho);
+    gstore(l4, lw);
+}
+__device__ inline float block_max256(float m, float *part) {
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
+    if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = m;
+    __syncthreads();
+    return fmaxf(fmaxf(part[0], part[1]), fmaxf(part[2], part[3]));
+}
+template <bool CACHED>
+__global__ __launch_bounds__(256) void split_rows_kernel(const float *__restrict__ src, int cols,
+                                                         uint16_t *__restrict__ hi, uint16_t *__restrict__ lo,
+                                                         int32_t *__restrict__ ex) {
+    __shared__ float part[4];
+    const size_t row = blockIdx.x;
+    const f32x4 *s4 = reinterpret_cast<const f32x4 *>(src + row * cols);
     u16x4 *h4 = reinterpret_cast<u16x4 *>(hi + row * cols);
     u16x4 *l4 = reinterpret_cast<u16x4 *>(lo + row * cols);
-    for (int i = threadIdx.x; i < n4; i += 256) {
-        const f32x4 v = gload(s4 + i);
-        u16x4 ho, lw;
+    const int n4 = cols / 4;
+    float m = 0.0f;
+    if constexpr (CACHED) {
+        f32x4 v[kSplitCached4];
 #pragma unroll
-        for (int c = 0; c < 4; c++) {
-            const float x = ldexpf(v[c], e);
-            const __half h = __float2half_rn(x);
-            ho[c] = __half_as_ushort(h);
-            lw[c] = __half_as_ushort(__float2half_rn(x - __half2float(h)));
+        for (int u = 0; u < kSplitCached4; u++) {
+            const int i = threadIdx.x + 256 * u;
+            v[u] = i < n4 ? gload(s4 + i) : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+            m = fmaxf(m, fmaxf(fmaxf(fabsf(v[u].x), fabsf(v[u].y)), fmaxf(fabsf(v[u].z), fabsf(v[u].w))));
         }
-        gstore(h4 + i, ho);
-        gstore(l4 + i, lw);
+        const int e = split_exponent(block_max256(m, part));
+        if (threadIdx.x == 0) ex[row] = e;
+#pragma unroll
+        for (int u = 0; u < kSplitCached4; u++) {
+            const int i = threadIdx.x + 256 * u;
+            if (i < n4) split_store(v[u], e, h4 + i, l4 + i);
+        }
+    } else {
+        for (int i = threadIdx.x; i < n4; i += 256) {
+            const f32x4 v = gload(s4 + i);
+            m = fmaxf(m, fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
+        }
+        const int e = split_exponent(block_max256(m, part));
+        if (threadIdx.x == 0) ex[row] = e;
+        for (int i = threadIdx.x; i < n4; i += 256) split_store(gload(s4 + i), e, h4 + i, l4 + i);
     }
 }
 
@@ -896,7 +924,10 @@ hipError_t launch_split_rows(const float *src, int rows, int cols, uint16_t *hi,
                              hipStream_t s) {
     if (rows <= 0) return hipSuccess;
     if (cols % 4 != 0) return hipErrorInvalidValue;
-    hipLaunchKernelGGL(split_rows_kernel, dim3(rows), dim3(256), 0, s, src, cols, hi, lo, ex);
+    if (cols / 4 <= 256 * kSplitCached4)
+        hipLaunchKernelGGL(split_rows_kernel<true>, dim3(rows), dim3(256), 0, s, src, cols, hi, lo, ex);
+    else
+        hipLaunchKernelGGL(split_rows_kernel<false>, dim3(rows), dim3(256), 0, s, src, cols, hi, lo, ex);
     return hipGetLastError();
 }
 

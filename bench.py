@@ -138,6 +138,51 @@ def cpu_baseline(host, t_decode: int, t_prefill: int, runs: int = 5):
     return res[t_decode], res[t_prefill], cores
 
 
+def hbm_ceiling(mib: int) -> int:
+    """The HBM read rate of a plain streaming kernel (moe_debug_stream_read)
+    over `mib` MiB, with plain and with nontemporal loads, at 1, 2, 4 and 8
+    blocks per CU: the ceilings the weight-streaming kernels are compared
+    with beside the 8 TB/s datasheet peak."""
+    import ctypes as C
+
+    import torch
+
+    from moe_amd import _lib as L
+
+    dev = torch.device("cuda:0")
+    buf = torch.ones(mib << 20, dtype=torch.uint8, device=dev)
+    cus = torch.cuda.get_device_properties(dev).multi_processor_count
+    stream = torch.cuda.current_stream().cuda_stream
+    rows = []
+    for nt in (0, 1):
+        for per_cu in (1, 2, 4, 8):
+            blocks = cus * per_cu
+            out = torch.empty(blocks, dtype=torch.int32, device=dev)
+
+            def go():
+                L.check(L.lib().moe_debug_stream_read(C.c_void_p(buf.data_ptr()), buf.numel(),
+                                                      C.c_void_p(out.data_ptr()), blocks, nt, C.c_void_p(stream)),
+                        "moe_debug_stream_read")
+
+            for _ in range(3):
+                go()
+            t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            n = 10
+            t0.record()
+            for _ in range(n):
+                go()
+            t1.record()
+            torch.cuda.synchronize()
+            ms = t0.elapsed_time(t1) / n
+            rows.append(dict(nontemporal=nt, blocks_per_cu=per_cu, ms=round(ms, 4),
+                             gb_s=round(buf.numel() / (ms * 1e-3) / 1e9, 1)))
+    best = {nt: max(r["gb_s"] for r in rows if r["nontemporal"] == nt) for nt in (0, 1)}
+    print(json.dumps(dict(hbm_read_ceiling_gb_s=best[0], hbm_read_ceiling_nontemporal_gb_s=best[1],
+                          bytes=buf.numel(), frac_of_8tb=round(best[0] / HBM_PEAK_GBS, 4),
+                          frac_of_8tb_nontemporal=round(best[1] / HBM_PEAK_GBS, 4), runs=rows)), flush=True)
+    return 0
+
+
 def copy_calibration(mib: int) -> int:
     """Five device-to-device copies of `mib` MiB: each reads and writes exactly
     mib * 1024 KiB, so a counter run over them gives the factor between the
@@ -325,6 +370,8 @@ def main() -> int:
     ap.add_argument("--summarize-counters", nargs="+", metavar="DIR",
                     help="write the MFMA kernels' counter summary from the rocprofv3 passes of COUNTER_PASSES "
                          "(directories, then the output markdown path) and exit")
+    ap.add_argument("--hbm-ceiling", type=int, default=0, metavar="MIB",
+                    help="only time a plain streaming read of MIB MiB (moe_debug_stream_read) and exit")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="only copy MIB MiB device-to-device 5 times (a plain copy kernel of known size, the "
                          "reference point for the FETCH_SIZE / WRITE_SIZE counters) and exit")
@@ -335,6 +382,8 @@ def main() -> int:
         return 2
     if args.copy_calibration:
         return copy_calibration(args.copy_calibration)
+    if args.hbm_ceiling:
+        return hbm_ceiling(args.hbm_ceiling)
     if args.summarize_pmc:
         return summarize_pmc(args.summarize_pmc[0], args.summarize_pmc[1], TRAFFIC_FILE)
     if args.summarize_counters:

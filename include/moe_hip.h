@@ -244,6 +244,15 @@ const char *moe_last_error(void);
  * device f32 [n].  No counterpart in the reference. */
 int moe_debug_expf(const float *x, float *y, uint64_t n, void *stream);
 
+/* Diagnostics: read `bytes` (a multiple of 16, 16-byte aligned device
+ * memory) once with a grid-stride 16-byte-load kernel of `blocks` blocks
+ * (eight loads in flight per thread; nontemporal != 0: nontemporal loads),
+ * writing one xor-fold per block to out[blocks]: the HBM read rate the
+ * weight-streaming kernels are measured against.  No counterpart in the
+ * reference. */
+int moe_debug_stream_read(const void *src, uint64_t bytes, uint32_t *out, int32_t blocks, int32_t nontemporal,
+                          void *stream);
+
 /* ------------------------------------------------ the model around the layer
  * The rest of the reference's forward (src/model.rs:646-834) as device
  * operations, so that a whole decoder runs with its routed layers on the

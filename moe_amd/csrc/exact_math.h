@@ -97,4 +97,45 @@ MOE_HD inline float expf_exact(float x) {
     return (float)y;
 }
 
+#if defined(__HIPCC__)
+// expf_exact with its table spread over a wavefront: lane l holds entry
+// l % 32 (exp2_lane_entry, loaded once), and each lane fetches the entry it
+// needs from that lane instead of from memory.  Every lane of the wavefront
+// must call it together.
+__device__ inline uint64_t exp2_lane_entry() { return kExp2TabDev[threadIdx.x & 31]; }
+
+__device__ inline float expf_exact_w(float x, uint64_t lane_entry) {
+    const double kShift = 0x1.8p+52;
+    const double kInvLn2N = 0x1.71547652b82fep+0 * 32;
+    const double kC0 = 0x1.c6af84b912394p-5 / 32 / 32 / 32;
+    const double kC1 = 0x1.ebfce50fac4f3p-3 / 32 / 32;
+    const double kC2 = 0x1.62e42ff0c52d6p-1 / 32;
+    double xd = (double)x;
+    double kd = fma_d(kInvLn2N, xd, kShift);
+    uint64_t ki = d2u(kd);
+    const int src = (int)(ki % 32);
+    const uint32_t lo = (uint32_t)__shfl((int)(uint32_t)lane_entry, src, 64);
+    const uint32_t hi = (uint32_t)__shfl((int)(uint32_t)(lane_entry >> 32), src, 64);
+    uint32_t ux = f2u(x);
+    uint32_t abstop = (ux >> 20) & 0x7ff;
+    if (abstop >= 0x42b) {  // |x| >= 88, inf or nan
+        if (ux == 0xff800000u) return 0.0f;                 // -inf
+        if (abstop >= 0x7f8) return x + x;                  // nan or +inf
+        if (x > 0x1.62e42ep6f) return u2f(0x7f800000u);     // overflow -> +inf
+        if (x < -0x1.9fe368p6f) return 0.0f;                // underflow -> +0
+    }
+    kd -= kShift;
+    double r = fma_d(kInvLn2N, xd, -kd);
+    uint64_t t = ((uint64_t)hi << 32) | lo;
+    t += ki << 47;
+    double s = u2d(t);
+    double z = fma_d(kC0, r, kC1);
+    double r2 = r * r;
+    double y = fma_d(kC2, r, 1.0);
+    y = fma_d(z, r2, y);
+    y = y * s;
+    return (float)y;
+}
+#endif
+
 }  // namespace moe

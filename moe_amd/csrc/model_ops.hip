@@ -26,6 +26,7 @@
 #include <cstdint>
 
 #include "exact_math.h"
+#include "gmem.h"
 #include "moe_internal.h"
 
 namespace moe {
@@ -240,6 +241,42 @@ __global__ void add_kernel(float *__restrict__ dst, const float *__restrict__ sr
         dst[i] += src[i];
 }
 
+// Diagnostics: the HBM read ceiling.  Grid-stride 16-byte loads, eight in
+// flight per thread, folded into one word per block so nothing is elided;
+// NT = true marks the loads nontemporal (streamed past the caches).
+typedef uint32_t sr_u32x4 __attribute__((ext_vector_type(4)));
+template <bool NT>
+__global__ __launch_bounds__(256) void stream_read_kernel(const sr_u32x4 *__restrict__ src, size_t n16,
+                                                          uint32_t *__restrict__ out) {
+    constexpr int U = 8;
+    const size_t stride = (size_t)gridDim.x * 256;
+    uint32_t acc = 0;
+    size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+    for (; i + (U - 1) * stride < n16; i += U * stride) {
+        sr_u32x4 v[U];
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            const sr_u32x4 *p = src + i + u * stride;
+            if constexpr (NT)
+                v[u] = __builtin_nontemporal_load((const __attribute__((address_space(1))) sr_u32x4 *)p);
+            else
+                v[u] = gload(p);
+        }
+#pragma unroll
+        for (int u = 0; u < U; u++) acc ^= v[u].x ^ v[u].y ^ v[u].z ^ v[u].w;
+    }
+    for (; i < n16; i += stride) {
+        const sr_u32x4 v = gload(src + i);
+        acc ^= v.x ^ v.y ^ v.z ^ v.w;
+    }
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) acc ^= (uint32_t)__shfl_xor((int)acc, o, 64);
+    __shared__ uint32_t part[4];
+    if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = acc;
+    __syncthreads();
+    if (threadIdx.x == 0) out[blockIdx.x] = part[0] ^ part[1] ^ part[2] ^ part[3];
+}
+
 int launch_rc(const char *what) {
     const hipError_t e = hipGetLastError();
     return e == hipSuccess ? MOE_OK : fail(MOE_EHIP, "%s: %s", what, hipGetErrorString(e));
@@ -342,6 +379,21 @@ int moe_attention(const float *q, int64_t q_stride, int32_t rows, int32_t heads,
     hipLaunchKernelGGL(attention_kernel, dim3((unsigned)rows * heads), dim3(64), lds, (hipStream_t)stream, q,
                        q_stride, heads, n_kv, qd, vd, scale, kcache, vcache, ctx, seq, pos, window, out, out_stride);
     return launch_rc("attention kernel");
+}
+
+int moe_debug_stream_read(const void *src, uint64_t bytes, uint32_t *out, int32_t blocks, int32_t nontemporal,
+                          void *stream) {
+    if (!src || !out || blocks <= 0 || bytes % 16 || ((uintptr_t)src & 15))
+        return fail(MOE_EINVAL, "moe_debug_stream_read: bad argument");
+    if (bytes == 0) return MOE_OK;
+    const sr_u32x4 *s4 = static_cast<const sr_u32x4 *>(src);
+    if (nontemporal)
+        hipLaunchKernelGGL(stream_read_kernel<true>, dim3(blocks), dim3(256), 0, (hipStream_t)stream, s4,
+                           (size_t)(bytes / 16), out);
+    else
+        hipLaunchKernelGGL(stream_read_kernel<false>, dim3(blocks), dim3(256), 0, (hipStream_t)stream, s4,
+                           (size_t)(bytes / 16), out);
+    return launch_rc("stream-read kernel");
 }
 
 int moe_argmax(const float *x, int32_t rows, int32_t n, int32_t *out, void *stream) {

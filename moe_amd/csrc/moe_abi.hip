@@ -410,7 +410,7 @@ int route_and_dispatch(moe_layer *L, const CallState &c, Workspace &w, const flo
             return hip_fail(e, "logits copy");
         return MOE_OK;
     };
-    if (t == 1 && route_one_ok(L->H)) {
+    if (t == 1 && route_one_ok(L->H, L->E)) {
         // One token: router, gating and dispatch in a single launch.
         int rc = stage(L, c.profile, 0, s, [&] {
             e = launch_route_one(L->router, x, n_rows, L->E, L->H, p.temp, w.logits, p, a, w.route_count, s);

@@ -158,7 +158,7 @@ hipError_t launch_dispatch(const DispatchArgs &a, int32_t *chunk_scratch, hipStr
 
 // Router + gating + dispatch of one token in one launch (n_rows blocks; the
 // last to finish gates and dispatches).  `counter` is zero between calls.
-bool route_one_ok(int H);
+bool route_one_ok(int H, int E);
 hipError_t launch_route_one(const float *W, const float *x, int n_rows, int E, int H, float temp, float *logits,
                             const GateParams &p, const DispatchArgs &d, unsigned *counter, hipStream_t s);
 

@@ -314,6 +314,7 @@ struct GateScratch {
     int32_t key[64];            // rank keys (EPL == 1)
     int32_t bypos[kMaxTopK + 1];  // key at each sorted position <= k (EPL == 1)
     float bcast;
+    float shg;                  // the shared expert's sigmoid gate (has_shared_gate)
 };
 
 // Orders this wavefront's LDS writes before its later LDS reads (the
@@ -324,30 +325,55 @@ __device__ inline void wave_sync() {
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
 }
 
+// The inputs of gate_token that are fixed for the layer, fetched by the
+// wavefront ahead of the logits: expf_exact's table (one entry per lane,
+// expf_exact_w) and the score-correction biases of the lane's experts.
+template <int EPL>
+struct GateConst {
+    uint64_t tab;
+    float bias[EPL];
+};
+
+template <int EPL>
+__device__ inline GateConst<EPL> gate_const(const GateParams &p) {
+    GateConst<EPL> G;
+    const int lane = threadIdx.x & 63;
+    G.tab = exp2_lane_entry();
+#pragma unroll
+    for (int i = 0; i < EPL; i++) {
+        const int e = lane * EPL + i;
+        G.bias[i] = (p.e_bias && e < p.n_experts) ? p.e_bias[e] : 0.0f;
+    }
+    return G;
+}
+
 // Gating for token t by one wavefront, experts e = lane*EPL + i.  Restates
 // src/model.rs:855-897: gate, rank = score + bias, prune_groups, disabled,
 // stable descending sort truncated to k (ties: lower index first), forced
 // experts, weights = max(score, 0), renormalise, scale.  `lg` is the token's
 // logits row (temperature already applied; entry E is the shared-expert gate
-// logit when the layer has one).
-template <int EPL>
-__device__ void gate_token(const float *__restrict__ lg, int t, const GateParams &p, GateScratch<EPL> &S,
-                           int32_t *__restrict__ sel, float *__restrict__ wsel, float *__restrict__ shgate,
-                           unsigned long long *__restrict__ stats) {
+// logit when the layer has one).  Every lane of the wavefront calls it
+// together.  STORE = false leaves the selection (S.idx, S.w) and the shared
+// gate (S.shg) in LDS only.
+template <int EPL, bool STORE = true>
+__device__ void gate_token(const float *__restrict__ lg, int t, const GateParams &p, const GateConst<EPL> &G,
+                           GateScratch<EPL> &S, int32_t *__restrict__ sel, float *__restrict__ wsel,
+                           float *__restrict__ shgate, unsigned long long *__restrict__ stats) {
     const int lane = threadIdx.x & 63;
     const int E = p.n_experts;
     float sc[EPL], rank[EPL], bias[EPL];
 #pragma unroll
-    for (int i = 0; i < EPL; i++) {  // logits and biases requested together
+    for (int i = 0; i < EPL; i++) {  // the logits and the shared gate's logit requested together
         const int e = lane * EPL + i;
         sc[i] = e < E ? lg[e] : 0.0f;
-        bias[i] = (p.e_bias && e < E) ? p.e_bias[e] : 0.0f;
+        bias[i] = G.bias[i];
     }
+    const float lg_shared = (p.has_shared_gate && lane == 0) ? lg[E] : 0.0f;
     if (p.sigmoid) {
 #pragma unroll
         for (int i = 0; i < EPL; i++) {
             float nv = -sc[i];
-            float den = 1.0f + expf_exact(nv);
+            float den = 1.0f + expf_exact_w(nv, G.tab);
             sc[i] = 1.0f / den;
         }
     } else {
@@ -358,7 +384,7 @@ __device__ void gate_token(const float *__restrict__ lg, int t, const GateParams
         m = wave_max_rs(m);
 #pragma unroll
         for (int i = 0; i < EPL; i++) {
-            sc[i] = expf_exact(sc[i] - m);
+            sc[i] = expf_exact_w(sc[i] - m, G.tab);
             if (lane * EPL + i < E) S.sc[lane * EPL + i] = sc[i];
         }
         wave_sync();
@@ -611,15 +637,19 @@ __device__ void gate_token(const float *__restrict__ lg, int t, const GateParams
         float wv = vj;
         if (p.norm_topk) wv = wv / z;
         wv = wv * p.routed_scale;
-        sel[(size_t)t * k + lane] = ij;
-        wsel[(size_t)t * k + lane] = wv;
+        if (STORE) {
+            sel[(size_t)t * k + lane] = ij;
+            wsel[(size_t)t * k + lane] = wv;
+        }
         S.w[lane] = wv;
     }
+    const float sh_exp = expf_exact_w(-lg_shared, G.tab);  // every lane; lane 0's is the gate's
     if (lane == 0) {
         if (p.has_shared_gate) {
-            float nv = -lg[E];
-            float den = 1.0f + expf_exact(nv);
-            shgate[t] = 1.0f / den;
+            float den = 1.0f + sh_exp;
+            const float g = 1.0f / den;
+            S.shg = g;
+            if (STORE) shgate[t] = g;
         }
         if (tie && stats) atomicAdd(stats + 3, 1ull);
     }
@@ -635,7 +665,8 @@ __global__ __launch_bounds__(256) void gating_kernel(const float *__restrict__ l
     const int w = threadIdx.x >> 6;
     const int t = blockIdx.x * 4 + w;
     if (t >= T) return;
-    gate_token<EPL>(logits + (size_t)t * ld, t, p, S[w], sel, wsel, shgate, stats);
+    const GateConst<EPL> G = gate_const<EPL>(p);
+    gate_token<EPL>(logits + (size_t)t * ld, t, p, G, S[w], sel, wsel, shgate, stats);
 }
 
 // ---------------------------------------------------------------- dispatch
@@ -893,79 +924,128 @@ __global__ __launch_bounds__(kDispatchThreads) void dispatch_place_kernel(Dispat
     dispatch_place(a, blockIdx.x * kDispatchThreads, run, bm, wb);
 }
 
+// The previous call's hit list (DispatchArgs::prev) as a wavefront holds
+// it: n and entries 1 + lane + 64 m.
+struct PrevLanes {
+    uint32_t n;
+    uint32_t v[kMaxExperts / 64];
+};
+
+__device__ inline PrevLanes prev_lanes(const DispatchArgs &a) {
+    PrevLanes P;
+    const int lane = threadIdx.x & 63;
+    P.n = a.prev ? a.prev[0] : 0u;
+#pragma unroll
+    for (int m = 0; m < kMaxExperts / 64; m++) {
+        const int j = lane + 64 * m;
+        P.v[m] = (a.prev && j < a.E) ? a.prev[1 + j] : 0xffffffffu;
+    }
+    return P;
+}
+
+// An expert's entry of the one-token task table, without its h row and
+// weight: what the table holds for it.
+__device__ inline DecodeTask task_entry(const ExpertDev &xe) {
+    DecodeTask dt{};
+    dt.g = xe.m[0].ptr, dt.u = xe.m[1].ptr, dt.d = xe.m[2].ptr;
+    dt.gs = xe.m[0].stride, dt.us = xe.m[1].stride, dt.ds = xe.m[2].stride;
+    dt.dcols = xe.m[2].cols;
+    return dt;
+}
+
 // The dispatch of a single token by one wavefront: the same outputs as
-// dispatch_block for T = 1.  idx/w are the token's k selections (distinct
-// experts) in slot order; `bits` is LDS scratch for an E-bit set.
-__device__ void dispatch_one(const DispatchArgs &a, const int *idx, const float *w, unsigned long long *bits) {
+// dispatch_block for T = 1, plus the token's selection (sel, wsel) and
+// shared gate, which the one-token kernel's gating leaves in LDS.  idx/w
+// are the token's k selections (distinct experts) in slot order, `shg` the
+// shared expert's gate (has_gate), `bits` LDS scratch for two E-bit sets.
+// Its inputs come from LDS and registers, fetched before the kernel's
+// acquire: `tasks` [E + 1] the experts' task_entry (a.dtasks only),
+// `bytes` [E] a.expert_bytes, `P` the previous hits.  It only stores.
+__device__ void dispatch_one(const DispatchArgs &a, const int *idx, const float *w, float shg, bool has_gate,
+                             unsigned long long *bits, const DecodeTask *tasks, const unsigned long long *bytes_of,
+                             const PrevLanes &P) {
     const int lane = threadIdx.x & 63;
     const int E = a.E, k = a.k;
     const int nw = (E + 63) / 64;
-    if (lane < nw) bits[lane] = 0ull;
-    wave_sync();
-    if (lane < k) atomicOr(&bits[idx[lane] >> 6], 1ull << (idx[lane] & 63));
-    wave_sync();
-    // Selected experts before e (ascending): its permuted row, and hit slot.
-    auto below = [&](int e) {
-        int n = 0;
-        for (int q = 0; q < (e >> 6); q++) n += __popcll(bits[q]);
-        const unsigned long long m = (e & 63) ? ((1ull << (e & 63)) - 1) : 0ull;
-        return n + __popcll(bits[e >> 6] & m);
+    unsigned long long *pbits = bits + kMaxExperts / 64;
+    constexpr int PM = kMaxExperts / 64;
+
+    const bool pick = lane < k;
+    const int e = pick ? idx[lane] : 0;
+    const float we = pick ? w[lane] : 0.0f;
+    const unsigned long long eb = pick ? bytes_of[e] : 0ull;
+    const bool task = pick && a.dtasks != nullptr;
+    const bool stask = lane == 0 && a.dtasks != nullptr && a.has_shared;
+    const uint32_t n_prev = P.n;
+    // Task q of the table: expert x's entry with its h row and weight.
+    auto put_task = [&](int q, int x, float *h, float wt) {
+        const DecodeTask &src = tasks[x];
+        DecodeTask dt;
+        dt.g = src.g, dt.u = src.u, dt.d = src.d;
+        dt.h = h;
+        dt.gs = src.gs, dt.us = src.us, dt.ds = src.ds;
+        dt.dcols = src.dcols;
+        dt.w = wt;
+        dt.live = 1;
+        dt._pad[0] = dt._pad[1] = 0;
+        a.dtasks[q] = dt;
     };
-    int nsel = 0;
-    for (int q = 0; q < nw; q++) nsel += __popcll(bits[q]);
-    unsigned long long bytes = 0, reused = 0;
-    for (int e = lane; e < E; e += 64) {
-        const int c = (int)((bits[e >> 6] >> (e & 63)) & 1ull);
-        const int o = below(e);
-        a.counts[e] = c;
-        a.offsets[e] = o;
-        if (c) {
-            a.hits[1 + o] = e;
-            if (a.hits_out) a.hits_out[1 + o] = (uint32_t)e;
-            bytes += a.expert_bytes[e];
-            if (a.prev) {
-                bool in_prev = false;
-                for (uint32_t j = 0; j < a.prev[0]; j++) in_prev |= a.prev[1 + j] == (uint32_t)e;
-                reused += in_prev ? 1ull : 0ull;
-            }
-            if (a.bm > 0) {
-                a.tiles[4 * o] = e;
-                a.tiles[4 * o + 1] = 0;
-                a.tiles[4 * o + 2] = o;
-                a.tiles[4 * o + 3] = 1;
-            }
-            if (a.dtasks && o < a.dk_bound) {
-                DecodeTask d{};
-                const ExpertDev &x = a.experts[e];
-                d.g = x.m[0].ptr, d.u = x.m[1].ptr, d.d = x.m[2].ptr;
-                d.gs = x.m[0].stride, d.us = x.m[1].stride, d.ds = x.m[2].stride;
-                d.dcols = x.m[2].cols;
-                d.h = a.h + (size_t)o * a.I;
-                for (int s = 0; s < k; s++)
-                    if (idx[s] == e) d.w = w[s];
-                d.live = 1;
-                a.dtasks[o] = d;
-            }
-        }
+
+    // The selected set and the previous call's set, as bits in LDS.
+    if (lane < nw) bits[lane] = pbits[lane] = 0ull;
+    wave_sync();
+    if (pick) atomicOr(&bits[e >> 6], 1ull << (e & 63));
+#pragma unroll
+    for (int m = 0; m < PM; m++) {
+        const int j = lane + 64 * m;
+        if (j < E && (uint32_t)j < n_prev && P.v[m] < (uint32_t)E) atomicOr(&pbits[P.v[m] >> 6], 1ull << (P.v[m] & 63));
     }
-    if (lane < k) {
-        const int e = idx[lane], o = below(e);
+    wave_sync();
+    // Selected experts before x (ascending): its permuted row, and hit slot.
+    auto below = [&](int x) {
+        int n = 0;
+        for (int q = 0; q < (x >> 6); q++) n += __popcll(bits[q]);
+        const unsigned long long msk = (x & 63) ? ((1ull << (x & 63)) - 1) : 0ull;
+        return n + __popcll(bits[x >> 6] & msk);
+    };
+    int nsel = 0, reused = 0;
+    for (int q = 0; q < nw; q++) {
+        nsel += __popcll(bits[q]);
+        reused += __popcll(bits[q] & pbits[q]);
+    }
+
+    // Stores.
+    for (int x = lane; x < E; x += 64) {
+        a.counts[x] = (int)((bits[x >> 6] >> (x & 63)) & 1ull);
+        a.offsets[x] = below(x);
+    }
+    if (pick) {
+        const int o = below(e);
+        a.hits[1 + o] = e;
+        if (a.hits_out) a.hits_out[1 + o] = (uint32_t)e;
+        if (a.bm > 0) {
+            a.tiles[4 * o] = e;
+            a.tiles[4 * o + 1] = 0;
+            a.tiles[4 * o + 2] = o;
+            a.tiles[4 * o + 3] = 1;
+        }
+        if (task && o < a.dk_bound) put_task(o, e, a.h + (size_t)o * a.I, we);
         a.perm_tok[o] = 0;
-        a.perm_w[o] = w[lane];
+        a.perm_w[o] = we;
         a.pos[lane] = o;
+        const_cast<int32_t *>(a.sel)[lane] = e;
+        const_cast<float *>(a.wsel)[lane] = we;
         if (a.routes) {
             a.routes[lane].expert = (uint32_t)e;
-            a.routes[lane].weight = w[lane];
+            a.routes[lane].weight = we;
         }
     }
     if (a.dtasks)
         for (int t = nsel + lane; t < a.dk_bound; t += 64) a.dtasks[t] = DecodeTask{};
-    // Wave sums of the byte and reuse counts.
+    // Wave sum of the byte count.
+    unsigned long long bytes = eb;
 #pragma unroll
-    for (int m = 32; m >= 1; m >>= 1) {
-        bytes += __shfl_xor(bytes, m, 64);
-        reused += __shfl_xor(reused, m, 64);
-    }
+    for (int m = 32; m >= 1; m >>= 1) bytes += __shfl_xor(bytes, m, 64);
     if (lane == 0) {
         a.offsets[E] = nsel;
         a.offsets[E + 1] = nsel + (a.has_shared ? 1 : 0);
@@ -983,66 +1063,165 @@ __device__ void dispatch_one(const DispatchArgs &a, const int *idx, const float 
             }
             a.ntiles[0] = nt;
         }
-        a.stats[0] += (unsigned long long)k;
-        a.stats[1] += reused;
-        a.stats[2] += bytes;
-        if (a.dtasks && a.has_shared) {
-            DecodeTask d{};
-            const ExpertDev &x = a.experts[E];
-            d.g = x.m[0].ptr, d.u = x.m[1].ptr, d.d = x.m[2].ptr;
-            d.gs = x.m[0].stride, d.us = x.m[1].stride, d.ds = x.m[2].stride;
-            d.dcols = x.m[2].cols;
-            d.h = a.hs;
-            d.w = a.shgate ? a.shgate[0] : 1.0f;
-            d.live = 1;
-            a.dtasks[a.dk_bound] = d;
-        }
+        if (has_gate && a.shgate_out) a.shgate_out[0] = shg;
+        atomicAdd(a.stats + 0, (unsigned long long)k);
+        atomicAdd(a.stats + 1, (unsigned long long)reused);
+        atomicAdd(a.stats + 2, bytes);
+        if (stask) put_task(a.dk_bound, E, a.hs, a.shgate ? shg : 1.0f);
     }
 }
 
 // ------------------------------------------------------------ one token
 //
 // Router, gating and dispatch of a single token in one launch.  Block r
-// computes logit r (dot_avx2's 16 lane chains over the staged row, as in
-// router_lds_kernel); the last block to finish, counted with one device
-// atomic after a release fence, gates the token and dispatches it.  The
-// counter is returned to zero by that block, and no block waits on another.
+// computes logit r: dot_avx2's 16 lane chains (chain j sums elements j,
+// j + 16, ... with fma, in order), then its lane reduction and scalar tail.
+// The block stages its router row and x into LDS transposed: chain j's
+// elements contiguous in row j, rows one_pitch(H) floats apart (= 4 mod 64,
+// so the 16 chains' 16-byte reads, and the staging writes, fall in distinct
+// banks); the elements past the last full 16 follow both arrays as they
+// are.  Each chain then reads four steps per LDS access, one batch ahead.
+// The last block to finish, counted with one device atomic after a release
+// fence, gates the token and dispatches it.  The counter is returned to zero
+// by that block, and no block waits on another.
+//
+// The acquire that follows the count invalidates the caches, so every load
+// after it comes from memory, one dependent round trip at a time.  Every
+// block therefore fetches what the gating and dispatch read besides the
+// logits before its count, together with its operands: wave 0 the gating
+// constants and the previous hits (registers), thread e expert e's task
+// entry and byte count (LDS, after the operands).
+__host__ __device__ inline int one_pitch(int H) {
+    const int n16 = H >> 4;
+    return n16 <= 4 ? 4 : 4 + 64 * ((n16 - 4 + 63) / 64);
+}
+inline size_t one_lds_bytes(int H, int E, bool tasks) {
+    return ((size_t)32 * one_pitch(H) + 32) * sizeof(float) + (tasks ? (size_t)(E + 1) * sizeof(DecodeTask) : 0) +
+           (size_t)E * sizeof(unsigned long long);
+}
+
+// Element i of an operand into the transposed layout.
+__device__ inline void one_put(float *t, float *tail, int P, int n16, int i, float v) {
+    if (i < 16 * n16)
+        t[(i & 15) * P + (i >> 4)] = v;
+    else
+        tail[i - 16 * n16] = v;
+}
+
 template <int EPL>
 __global__ __launch_bounds__(kDispatchThreads) __attribute__((amdgpu_waves_per_eu(1, 2))) void route_one_kernel(const float *__restrict__ W,
                                                                      const float *__restrict__ x, int n_rows, int E,
                                                                      int H, float temp, float *__restrict__ logits,
                                                                      GateParams p, DispatchArgs d,
                                                                      unsigned *__restrict__ counter) {
-    extern __shared__ float lds[];  // router row r, then x
+    // [16][P] row, [16][P] x, 16 + 16 tail, [E + 1] task entries (d.dtasks), [E] byte counts
+    extern __shared__ __align__(16) float lds[];
     __shared__ GateScratch<EPL> S;
     __shared__ int s_last;
     const int r = blockIdx.x;
+    const int n16 = H >> 4, P = one_pitch(H);
+    float *ta = lds, *tb = lds + 16 * P, *tail_a = lds + 32 * P, *tail_b = tail_a + 16;
+    DecodeTask *ltask = reinterpret_cast<DecodeTask *>(lds + 32 * P + 32);
+    unsigned long long *lbytes = reinterpret_cast<unsigned long long *>(d.dtasks ? ltask + E + 1 : ltask);
+    const float *wr = W + (size_t)r * H;
+    const int tid = threadIdx.x, nt = blockDim.x;
+    // The layer's constants for the last block (requested before the
+    // operands, stored after them).
+    GateConst<EPL> G{};
+    PrevLanes Pv{};
+    if (tid < 64) {
+        G = gate_const<EPL>(p);
+        Pv = prev_lanes(d);
+    }
+    auto has_task = [&](int e) { return d.dtasks != nullptr && (e < E || (e == E && d.has_shared)); };
+    DecodeTask te{};
+    unsigned long long tbytes = 0;
+    if (tid < E) tbytes = d.expert_bytes[tid];
+    if (has_task(tid)) te = task_entry(d.experts[tid]);
     if ((H & 3) == 0 && ((uintptr_t)W & 15) == 0 && ((uintptr_t)x & 15) == 0) {
-        stage2_to_lds<4>(W + (size_t)r * H, lds, H, x, lds + H, H, H >> 2, H >> 2);
+        // Four float4 of each operand in flight per thread before its stores;
+        // indices past the end re-read the last vector and store nothing.
+        const float4 *a4 = reinterpret_cast<const float4 *>(wr), *b4 = reinterpret_cast<const float4 *>(x);
+        const int n4 = H >> 2;
+        for (int base = 0; base < n4; base += 4 * nt) {
+            float4 va[4], vb[4];
+#pragma unroll
+            for (int u = 0; u < 4; u++) {
+                const int i = base + u * nt + tid, ic = i < n4 ? i : n4 - 1;
+                va[u] = a4[ic];
+                vb[u] = b4[ic];
+            }
+#pragma unroll
+            for (int u = 0; u < 4; u++) {
+                const int i = base + u * nt + tid;
+                if (i < n4) {
+                    one_put(ta, tail_a, P, n16, 4 * i, va[u].x);
+                    one_put(ta, tail_a, P, n16, 4 * i + 1, va[u].y);
+                    one_put(ta, tail_a, P, n16, 4 * i + 2, va[u].z);
+                    one_put(ta, tail_a, P, n16, 4 * i + 3, va[u].w);
+                    one_put(tb, tail_b, P, n16, 4 * i, vb[u].x);
+                    one_put(tb, tail_b, P, n16, 4 * i + 1, vb[u].y);
+                    one_put(tb, tail_b, P, n16, 4 * i + 2, vb[u].z);
+                    one_put(tb, tail_b, P, n16, 4 * i + 3, vb[u].w);
+                }
+            }
+        }
     } else {
-        stage_to_lds(W + (size_t)r * H, lds, H);
-        stage_to_lds(x, lds + H, H);
+        for (int i = tid; i < H; i += nt) {
+            const float va = wr[i], vb = x[i];
+            one_put(ta, tail_a, P, n16, i, va);
+            one_put(tb, tail_b, P, n16, i, vb);
+        }
+    }
+    if (tid < E) lbytes[tid] = tbytes;
+    if (has_task(tid)) ltask[tid] = te;
+    for (int e = tid + nt; e <= E; e += nt) {  // E + 1 > blockDim.x
+        if (e < E) lbytes[e] = d.expert_bytes[e];
+        if (has_task(e)) ltask[e] = task_entry(d.experts[e]);
     }
     __syncthreads();
     if (threadIdx.x < 16) {
         const int j = threadIdx.x;
-        const float *a = lds, *b = lds + H;
-        const int n16 = H / 16;
+        const float4 *pa = reinterpret_cast<const float4 *>(ta + j * P);
+        const float4 *pb = reinterpret_cast<const float4 *>(tb + j * P);
+        const int nq = n16 >> 2;  // full quads of steps
         float acc = 0.0f;
-        int c = 0;
-        // Sixteen steps of the chain per batch, their LDS reads issued first.
-        for (; c + 16 <= n16; c += 16) {
-            float av[16], bv[16];
+        if (nq > 0) {
+            // Batches of four quads; the next batch's reads are issued before
+            // this batch's fmas.  Reads past the last quad re-read it.
+            float4 a0[4], b0[4], a1[4], b1[4];
+            auto ld = [&](int q, float4(&av)[4], float4(&bv)[4]) {
 #pragma unroll
-            for (int u = 0; u < 16; u++) av[u] = a[16 * (c + u) + j], bv[u] = b[16 * (c + u) + j];
+                for (int u = 0; u < 4; u++) {
+                    const int qi = q + u < nq ? q + u : nq - 1;
+                    av[u] = pa[qi];
+                    bv[u] = pb[qi];
+                }
+            };
+            auto mac = [&](int q, const float4(&av)[4], const float4(&bv)[4]) {
 #pragma unroll
-            for (int u = 0; u < 16; u++) acc = fmaf(av[u], bv[u], acc);
+                for (int u = 0; u < 4; u++)
+                    if (q + u < nq) {
+                        acc = fmaf(av[u].x, bv[u].x, acc);
+                        acc = fmaf(av[u].y, bv[u].y, acc);
+                        acc = fmaf(av[u].z, bv[u].z, acc);
+                        acc = fmaf(av[u].w, bv[u].w, acc);
+                    }
+            };
+            ld(0, a0, b0);
+            for (int q = 0; q < nq; q += 8) {
+                ld(q + 4, a1, b1);
+                mac(q, a0, b0);
+                ld(q + 8, a0, b0);
+                mac(q + 4, a1, b1);
+            }
         }
-        for (; c < n16; c++) acc = fmaf(a[16 * c + j], b[16 * c + j], acc);
-        if ((H % 16) >= 8 && j < 8) acc = fmaf(a[16 * n16 + j], b[16 * n16 + j], acc);
+        for (int c = 4 * nq; c < n16; c++) acc = fmaf(ta[j * P + c], tb[j * P + c], acc);
+        const int rem = H - 16 * n16;
+        if (rem >= 8 && j < 8) acc = fmaf(tail_a[j], tail_b[j], acc);
         float v = reduce16_avx2(acc);
         if (j == 0) {
-            v = dot_tail(v, a, b, 16 * n16 + ((H % 16) >= 8 ? 8 : 0), H);
+            v = dot_tail(v, tail_a, tail_b, rem >= 8 ? 8 : 0, rem);
             if (temp > 0.0f && r < E) v = v / temp;
             logits[r] = v;
         }
@@ -1057,12 +1236,12 @@ __global__ __launch_bounds__(kDispatchThreads) __attribute__((amdgpu_waves_per_e
     }
     __syncthreads();
     if (!s_last || threadIdx.x >= 64) return;
-    // The last block's first wavefront gates and dispatches the token.
-    __shared__ unsigned long long bits[kMaxExperts / 64];
-    gate_token<EPL>(logits, 0, p, S, const_cast<int32_t *>(d.sel), const_cast<float *>(d.wsel), d.shgate_out,
-                    d.stats);
+    // The last block's first wavefront gates and dispatches the token; the
+    // selection's stores wait for the dispatch's loads (dispatch_one).
+    __shared__ unsigned long long bits[2 * (kMaxExperts / 64)];
+    gate_token<EPL, false>(logits, 0, p, G, S, nullptr, nullptr, nullptr, d.stats);
     wave_sync();
-    dispatch_one(d, S.idx, S.w, bits);
+    dispatch_one(d, S.idx, S.w, S.shg, p.has_shared_gate != 0, bits, ltask, lbytes, Pv);
     if (threadIdx.x == 0) *counter = 0u;
 }
 
@@ -1140,13 +1319,22 @@ hipError_t launch_gating(const float *logits, int ld, int T, const GateParams &p
     return hipGetLastError();
 }
 
-bool route_one_ok(int H) { return H > 0 && (size_t)2 * H * 4 <= 64 * 1024; }
+// The transposed operands and the prefetched tables take one_lds_bytes:
+// 76 KiB at H = 7168, E = 256.  Up to 64 KiB needs no attribute; beyond,
+// the launch raises the kernel's limit (the block's static LDS is under
+// 16 KiB of the CU's 160 KiB).
+bool route_one_ok(int H, int E) { return H > 0 && E > 0 && one_lds_bytes(H, E, true) <= 144 * 1024; }
 
 hipError_t launch_route_one(const float *W, const float *x, int n_rows, int E, int H, float temp, float *logits,
                             const GateParams &p, const DispatchArgs &d, unsigned *counter, hipStream_t s) {
-    const size_t lds = (size_t)2 * H * 4;
+    if (!route_one_ok(H, E)) return hipErrorInvalidValue;
+    const size_t lds = one_lds_bytes(H, E, d.dtasks != nullptr);
     auto go = [&](auto kern) {
-        (void)hipFuncSetAttribute((const void *)kern, hipFuncAttributeMaxDynamicSharedMemorySize, 64 * 1024);
+        if (lds > 64 * 1024) {
+            const hipError_t e =
+                hipFuncSetAttribute((const void *)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+            if (e != hipSuccess) return e;
+        }
         hipLaunchKernelGGL(kern, dim3(n_rows), dim3(kDispatchThreads), lds, s, W, x, n_rows, E, H, temp, logits, p,
                            d, counter);
         return hipGetLastError();

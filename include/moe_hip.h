@@ -244,6 +244,13 @@ const char *moe_last_error(void);
  * device f32 [n].  No counterpart in the reference. */
 int moe_debug_expf(const float *x, float *y, uint64_t n, void *stream);
 
+/* Diagnostics: which one-token gate/up kernel the forward uses, for every
+ * layer of the process: 0 the automatic choice, 1 the strided kernel with
+ * its separate encoding of h, 2 the unit-aligned kernel that encodes h
+ * itself.  Returns the previous choice (>= 0) or MOE_EINVAL.  Both give the
+ * same bits.  No counterpart in the reference. */
+int moe_debug_decode_kernel(int32_t choice);
+
 /* Diagnostics: read `bytes` (a multiple of 16, 16-byte aligned device
  * memory) once with a grid-stride 16-byte-load kernel of `blocks` blocks
  * (eight loads in flight per thread; nontemporal != 0: nontemporal loads),

@@ -15,8 +15,12 @@
 //    expert's forward at src/model.rs:925-935.  Persistent waves stream rows
 //    with several rows' weights in flight; each block first encodes x into
 //    LDS.
-//  * decode_hq_kernel: every selected expert's h (f32) to activation units,
-//    one wavefront per 64-value unit, once for all down blocks.
+//  * decode_up_unit_kernel: the same rows, one block per 64-row unit of h,
+//    which the block encodes into activation units itself; used while the
+//    units fit one round of resident blocks.
+//  * decode_hq_kernel: otherwise, every selected expert's h (f32) to
+//    activation units, one wavefront per 64-value unit, once for all down
+//    blocks.
 //  * decode_down_kernel: a block owns ranges of output rows and one group of
 //    waves per selected expert; each lane loads its units of the experts'
 //    h, streams their down rows and combines each row in
@@ -34,6 +38,7 @@
 #include <hip/hip_fp16.h>
 #include <hip/hip_runtime.h>
 
+#include <atomic>
 #include <mutex>
 #include <vector>
 
@@ -177,6 +182,93 @@ __global__ __launch_bounds__(256) void decode_up_kernel(DecodeArgs a, const floa
             s += nw;
         }
     }
+}
+
+// Unit-aligned gate/up: block b computes the 64 rows of h that form unit b
+// of the activation-unit list (routed task t's units, t ascending, then
+// the shared expert's), its four waves taking the unit's steps w, w + 4,
+// ... with NBUF - 1 steps in flight.  Each row's h goes to LDS; after a
+// barrier the first wave encodes the unit (qact_wave_encode) where the down
+// kernel reads it, so no encoding launch follows.  A block of a task
+// without an expert does nothing.
+template <int DT, int UPL, int NBUF>
+__global__ __launch_bounds__(256) void decode_up_unit_kernel(DecodeArgs a, const float *__restrict__ x) {
+    extern __shared__ __align__(16) uint8_t xs[];  // x as units
+    __shared__ DecodeTask task;
+    __shared__ float hrow[64];
+    constexpr int DW = WUnit<DT>::dw, UB = WUnit<DT>::bytes;
+    const int units = a.H / 64, cg = lanes_for(units), slices = 64 / cg;
+    const int lane = threadIdx.x & 63, slot = lane / cg, c = lane % cg;
+    const bool tail = c == cg - 1;
+    bool live[UPL];
+#pragma unroll
+    for (int j = 0; j < UPL; j++) live[j] = c + 64 * j < units;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int upr = a.I / 64;
+    const int b = blockIdx.x;
+    const bool routed = b < a.k_bound * upr;
+    const int t = routed ? b / upr : a.k_bound;
+    const int u = routed ? b - t * upr : b - a.k_bound * upr;
+    const int n_steps = 64 / slices;
+
+    const int n_xb = a.H / 32;
+    float xv[32];
+    if ((int)threadIdx.x < n_xb) load32(x + (size_t)threadIdx.x * 32, xv);
+    if (threadIdx.x == 0) task = a.tasks[t];
+    __syncthreads();
+    if (!task.live) return;  // the whole block
+
+    // Step j of the unit: rows 64 u + j * slices + slot of the task; steps
+    // past the unit re-read its last one and are not computed.
+    const int cl = c < units ? c : units - 1;
+    auto step = [&](int j) {
+        UpStep st;
+        st.ok = j < n_steps;
+        const int r = 64 * u + (st.ok ? j : n_steps - 1) * slices + slot;
+        st.g = task.g + (size_t)r * task.gs + (size_t)cl * UB;
+        st.u = task.u + (size_t)r * task.us + (size_t)cl * UB;
+        st.h = nullptr;
+        return st;
+    };
+    uint32_t w[NBUF][2][UPL][DW];
+    UpStep st[NBUF];
+    int sj[NBUF];
+#pragma unroll
+    for (int k = 0; k + 1 < NBUF; k++) {
+        sj[k] = wave + 4 * k;
+        st[k] = step(sj[k]);
+        up_load<DT, UPL, DW>(st[k], live, w[k]);
+    }
+    if ((int)threadIdx.x < n_xb)
+        qact_block_put<3>(qact_block(xv), xs + (size_t)(threadIdx.x >> 1) * kQUnitBytes, threadIdx.x & 1);
+    __syncthreads();
+    uint32_t xa[UPL][kQUnitDw];
+#pragma unroll
+    for (int j = 0; j < UPL; j++)
+        if (live[j]) load_qunit<3>(xs + (size_t)(c + 64 * j) * kQUnitBytes, xa[j]);
+
+    for (bool more = sj[0] < n_steps; more;) {
+#pragma unroll
+        for (int k = 0; k < NBUF; k++) {
+            const int nk = (k + NBUF - 1) % NBUF;
+            sj[nk] = sj[(k + NBUF - 2) % NBUF] + 4;
+            st[nk] = step(sj[nk]);
+            up_load<DT, UPL, DW>(st[nk], live, w[nk]);
+            if (!st[k].ok) {
+                more = false;
+                break;
+            }
+            float g = 0.0f, uu = 0.0f;
+#pragma unroll
+            for (int j = 0; j < UPL; j++)
+                if (live[j]) g += qdot<DT, DW>(w[k][0][j], xa[j]), uu += qdot<DT, DW>(w[k][1][j], xa[j]);
+            g = slice_sum(g, cg);
+            uu = slice_sum(uu, cg);
+            if (tail) hrow[sj[k] * slices + slot] = silu_mul(g, uu);
+        }
+    }
+    __syncthreads();
+    if (wave == 0) qact_wave_encode(hrow[lane], a.hq + ((size_t)t * a.hq_units + u) * kQUnitBytes, lane);
 }
 
 // --------------------------------------------------------------- down
@@ -438,12 +530,14 @@ hipError_t up_go(const DecodeArgs &a, const float *x, int n_steps, int spr, hipS
     return hipGetLastError();
 }
 
-// Rows per lane slice of the down kernel for a format pair: what fits the
-// register budget beside the activations, NBUF buffers deep.
+// Rows per lane slice of the down kernel for a format pair: at most 2 (more
+// rows per range leave a block fewer ranges to pipeline: Mixtral's down
+// kernel took 22.2 µs at 4 rows and 20.0 at 2), and what fits the register
+// budget beside the activations, NBUF buffers deep.
 int down_rs(int dt_r, int dt_s, int upl, bool big_block) {
     const int dw = std::max(dw_of(dt_r), dw_of(dt_s));
     const int budget = big_block ? 60 : 140;  // registers for the weight ring
-    int rs = 4;
+    int rs = 2;
     while (rs > 1 && kDownBuffers * rs * upl * dw > budget) rs /= 2;
     return rs;
 }
@@ -476,9 +570,75 @@ bool decode_fits(int I, int I_s, int k, int has_shared, int dt_routed, int dt_sh
     return hi / lo <= down_rs(dt_routed, dt_shared, upl_of(I / 64), waves > 8);
 }
 
-hipError_t launch_decode_up(const DecodeArgs &a, const float *x, int dt_routed, int dt_shared, hipStream_t s) {
+template <int DT, int UPL>
+hipError_t up_unit_go(const DecodeArgs &a, const float *x, int n_units, hipStream_t s) {
+    auto k = decode_up_unit_kernel<DT, UPL, kUpBuffers>;
+    const size_t lds = (size_t)(a.H / 64) * kQUnitBytes;
+    (void)occupancy((const void *)k, 256, lds);  // lifts the LDS limit
+    hipLaunchKernelGGL(k, dim3(n_units), dim3(256), lds, s, a, x);
+    return hipGetLastError();
+}
+
+// Which one-token gate/up kernel runs: 0 by decode_unit_pays, 1 the strided
+// kernel (and the encoding launch), 2 the unit-aligned kernel.  Set by
+// moe_debug_decode_kernel, or at load by MOE_DECODE_UNIT=0 / 1.
+static int decode_unit_from_env() {
+    const char *e = getenv("MOE_DECODE_UNIT");
+    return e && (e[0] == '0' || e[0] == '1') ? 1 + (e[0] - '0') : 0;
+}
+static std::atomic<int> g_decode_unit{decode_unit_from_env()};
+
+int set_decode_kernel(int choice) { return g_decode_unit.exchange(choice); }
+
+// The unit-aligned kernel runs one block per unit of h and saves the
+// encoding launch: it pays while the units fit one round of resident
+// blocks (two per CU at one unit per lane, one at two).  Measured on
+// MI355X, one token: Mixtral (448 units) 60.3 -> 58.6 µs, Qwen3 (96) 34.7 ->
+// 32.0, V2-Lite (176) 38.8 -> 34.9, Qwen2-MoE (176) 46.5 -> 42.2; DeepSeek-V3
+// (288 units at one block per CU, two rounds) 90.5 -> 107.
+static bool decode_unit_pays(int n_units, int upl, int cus) { return n_units <= cus * (upl == 1 ? 2 : 1); }
+
+hipError_t launch_decode_up(const DecodeArgs &a, const float *x, int dt_routed, int dt_shared, bool &encoded,
+                            hipStream_t s) {
     const int units = a.H / 64, upl = upl_of(units);
     const int slices = 64 / lanes_for_host(units);
+    encoded = false;
+    const int n_units = a.k_bound * (a.I / 64) + (a.n_shared ? a.I_s / 64 : 0);
+    const int forced = g_decode_unit.load();
+    const bool unit = forced ? forced == 2 : decode_unit_pays(n_units, upl, cus_of_current_device());
+    if (unit && a.hq && a.I % 64 == 0 && (!a.n_shared || a.I_s % 64 == 0) && a.I / 64 <= a.hq_units &&
+        (!a.n_shared || a.I_s / 64 <= a.hq_units)) {
+        auto ugo = [&](int dt, const DecodeArgs &d, int nu) -> hipError_t {
+            switch (dt * 4 + upl) {
+            case MOE_DT_Q4_0 * 4 + 1: return up_unit_go<MOE_DT_Q4_0, 1>(d, x, nu, s);
+            case MOE_DT_Q4_0 * 4 + 2: return up_unit_go<MOE_DT_Q4_0, 2>(d, x, nu, s);
+            case MOE_DT_Q5_0 * 4 + 1: return up_unit_go<MOE_DT_Q5_0, 1>(d, x, nu, s);
+            case MOE_DT_Q5_0 * 4 + 2: return up_unit_go<MOE_DT_Q5_0, 2>(d, x, nu, s);
+            case MOE_DT_Q8_0 * 4 + 1: return up_unit_go<MOE_DT_Q8_0, 1>(d, x, nu, s);
+            case MOE_DT_Q8_0 * 4 + 2: return up_unit_go<MOE_DT_Q8_0, 2>(d, x, nu, s);
+            default: return hipErrorInvalidValue;
+            }
+        };
+        hipError_t e;
+        if (!a.n_shared || dt_shared == dt_routed) {
+            e = ugo(dt_routed, a, n_units);
+        } else {
+            DecodeArgs r = a;
+            r.n_shared = 0;
+            e = ugo(dt_routed, r, a.k_bound * (a.I / 64));
+            if (e == hipSuccess) {
+                // The shared expert's units: task 0 of its own table, its
+                // units after the routed tasks' in hq.
+                DecodeArgs sh = a;
+                sh.k_bound = 0;
+                sh.tasks = a.tasks + a.k_bound;
+                sh.hq = a.hq + (size_t)a.k_bound * a.hq_units * kQUnitBytes;
+                e = ugo(dt_shared, sh, a.I_s / 64);
+            }
+        }
+        encoded = e == hipSuccess;
+        return e;
+    }
     auto go = [&](int dt, const DecodeArgs &d, int n_steps, int spr) -> hipError_t {
         switch (dt * 4 + upl) {
         case MOE_DT_Q4_0 * 4 + 1: return up_go<MOE_DT_Q4_0, 1>(d, x, n_steps, spr, s);

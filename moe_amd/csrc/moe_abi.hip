@@ -489,16 +489,19 @@ int forward_on(moe_layer *L, const CallState &c, Workspace &w, const float *x, i
         d.hq_units = std::max(L->I, L->has_shared ? L->I_s : 0) / 64;
         d.ys = w.ys;  // the shared expert's output when its down launch is separate
         const int dt_r = e0.m[0].dt, dt_s = sh ? sh->m[0].dt : dt_r;
+        bool encoded = false;
         rc = stage(L, c.profile, 3, s, [&] {
-            e = launch_decode_up(d, x, dt_r, dt_s, s);
+            e = launch_decode_up(d, x, dt_r, dt_s, encoded, s);
             return e == hipSuccess ? MOE_OK : hip_fail(e, "one-token gate/up kernel");
         });
         if (rc) return rc;
-        rc = stage(L, c.profile, 6, s, [&] {
-            e = launch_decode_encode(d, s);
-            return e == hipSuccess ? MOE_OK : hip_fail(e, "one-token encoding of h");
-        });
-        if (rc) return rc;
+        if (!encoded) {
+            rc = stage(L, c.profile, 6, s, [&] {
+                e = launch_decode_encode(d, s);
+                return e == hipSuccess ? MOE_OK : hip_fail(e, "one-token encoding of h");
+            });
+            if (rc) return rc;
+        }
         return stage(L, c.profile, 4, s, [&] {
             e = launch_decode_down(d, dt_r, dt_s, s);
             return e == hipSuccess ? MOE_OK : hip_fail(e, "one-token down kernel");
@@ -1073,6 +1076,11 @@ int moe_layer_route(moe_layer *L, const float *x, int32_t t, moe_route *routes, 
     int rc = stream_ws(L, s, t, c.k, w);
     if (rc) return rc;
     return route_and_dispatch(L, c, w, x, t, 0, false, routes, nullptr, nullptr, nullptr, logits, s);
+}
+
+int moe_debug_decode_kernel(int32_t choice) {
+    if (choice < 0 || choice > 2) return fail(MOE_EINVAL, "moe_debug_decode_kernel: choice %d (0, 1 or 2)", choice);
+    return set_decode_kernel(choice);
 }
 
 int moe_layer_forward(moe_layer *L, const float *x, int32_t t, float *out, float *residual, moe_route *routes,

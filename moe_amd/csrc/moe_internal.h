@@ -217,9 +217,15 @@ struct DecodeArgs {
 constexpr int kDecodeMaxWaves = 16;  // waves of a down-projection block
 bool decode_supported(int H, int I, int I_s, int dt_routed, int dt_shared);
 bool decode_fits(int I, int I_s, int k, int has_shared, int dt_routed, int dt_shared);
-hipError_t launch_decode_up(const DecodeArgs &a, const float *x, int dt_routed, int dt_shared, hipStream_t s);
+// `encoded`: the launch also encoded h into a.hq (the unit-aligned kernel),
+// so launch_decode_encode is not needed.
+hipError_t launch_decode_up(const DecodeArgs &a, const float *x, int dt_routed, int dt_shared, bool &encoded,
+                            hipStream_t s);
 // Every live task's h (f32) to activation units at a.hq, one wavefront per unit.
 hipError_t launch_decode_encode(const DecodeArgs &a, hipStream_t s);
+// The one-token gate/up kernel choice (moe_debug_decode_kernel); returns
+// the previous one.
+int set_decode_kernel(int choice);
 // The down projection and combine over the units of h.
 hipError_t launch_decode_down(const DecodeArgs &a, int dt_routed, int dt_shared, hipStream_t s);
 // Whether the shared expert's down projection runs as a launch of its own

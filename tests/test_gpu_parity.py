@@ -207,6 +207,51 @@ def test_decode_repeated_calls(ctx, oracle, name, scale):
     record("decode", f"{name} {scale or 'full size'} x3", worst)
 
 
+@pytest.mark.parametrize("name,scale", [
+    ("tiny_mixtral", {}),
+    ("mixtral", {}),
+    ("qwen3", {}),
+    ("v2_lite", {}),                              # two shared experts: their units after the routed ones
+    ("deepseek_v3", {}),                          # two units per lane; Q5_0 shared expert: its own launch
+    ("qwen2_moe", {}),                            # the shared expert's sigmoid gate
+])
+def test_decode_up_kernels_agree(ctx, oracle, name, scale):
+    """The two one-token gate/up kernels, the strided one (with its separate
+    encoding of h) and the unit-aligned one (one block per unit of h, which
+    it encodes itself), give the same output bits, within TOL of the CPU
+    path, on the same token."""
+    from moe_amd import _lib as L
+    from moe_amd import synth
+
+    host, gl, ol = layer_pair(ctx, oracle, name, **scale)
+    x = synth.activations(SEED + 7, 1, host.shape.hidden)
+    out, sel, w, hits, stats = ol.forward(x)
+    got = {}
+    prev = L.lib().moe_debug_decode_kernel(1)
+    assert prev >= 0
+    try:
+        for choice in (1, 2):
+            assert L.lib().moe_debug_decode_kernel(choice) >= 0
+            got[choice] = run_gpu(gl, x, mode=4)
+    finally:
+        L.lib().moe_debug_decode_kernel(prev)
+        gl.set_mode(0)
+    for choice, g in got.items():
+        assert_routing_equal(g, sel, w, f"{name} kernel {choice}")
+        err = rel_err(g["out"], out)
+        assert err <= TOL, f"{name} kernel {choice}: max rel err {err:.3e}"
+    assert np.array_equal(got[1]["out"].view(np.uint32), got[2]["out"].view(np.uint32)), \
+        f"{name}: strided and unit-aligned gate/up kernels differ"
+    log(f"{name}: one-token gate/up kernels agree bit for bit, max rel err {rel_err(got[2]['out'], out):.2e}")
+
+
+def test_decode_kernel_choice_rejects_bad_values(ctx):
+    from moe_amd import _lib as L
+
+    assert L.lib().moe_debug_decode_kernel(3) == L.MOE_EINVAL
+    assert L.lib().moe_debug_decode_kernel(-1) == L.MOE_EINVAL
+
+
 @pytest.mark.parametrize("kind", ["disabled", "forced", "top1", "topE", "forced2"])
 def test_decode_interventions(ctx, oracle, kind):
     """Interventions change k and the hit list at T = 1; the one-token

@@ -183,6 +183,48 @@ def hbm_ceiling(mib: int) -> int:
     return 0
 
 
+def grid_barrier_cost() -> int:
+    """The cost of a grid-wide barrier (moe_debug_grid_barrier): cooperative
+    launches of one block per CU and of two, with 1 and with 101 barriers
+    each; per barrier = the difference / 100.  Beside them, an ordinary
+    launch of a small kernel on the same stream for the launch cost."""
+    import ctypes as C
+
+    import torch
+
+    from moe_amd import _lib as L
+
+    dev = torch.device("cuda:0")
+    cus = torch.cuda.get_device_properties(dev).multi_processor_count
+    state = torch.zeros(4, dtype=torch.int32, device=dev)
+    stream = torch.cuda.current_stream().cuda_stream
+
+    def per_launch(fn, reps=20):
+        for _ in range(3):
+            fn()
+        t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        t0.record()
+        for _ in range(reps):
+            fn()
+        t1.record()
+        torch.cuda.synchronize()
+        return t0.elapsed_time(t1) / reps * 1e3
+
+    rows = []
+    for blocks in (cus, 2 * cus):
+        us = {}
+        for nb in (1, 101):
+            us[nb] = per_launch(lambda: L.check(L.lib().moe_debug_grid_barrier(
+                blocks, nb, C.c_void_p(state.data_ptr()), C.c_void_p(stream)), "moe_debug_grid_barrier"))
+        rows.append(dict(blocks=blocks, us_1_barrier=round(us[1], 2), us_101_barriers=round(us[101], 2),
+                         us_per_barrier=round((us[101] - us[1]) / 100, 2)))
+    x = torch.ones(1 << 16, dtype=torch.float32, device=dev)
+    plain = per_launch(lambda: x.add_(0.0), reps=200)
+    err = int(state[2].item())
+    print(json.dumps(dict(grid_barrier=rows, plain_launch_us=round(plain, 2), bound_hit=err)), flush=True)
+    return 0 if err == 0 else 1
+
+
 def copy_calibration(mib: int) -> int:
     """Five device-to-device copies of `mib` MiB: each reads and writes exactly
     mib * 1024 KiB, so a counter run over them gives the factor between the
@@ -370,6 +412,8 @@ def main() -> int:
     ap.add_argument("--summarize-counters", nargs="+", metavar="DIR",
                     help="write the MFMA kernels' counter summary from the rocprofv3 passes of COUNTER_PASSES "
                          "(directories, then the output markdown path) and exit")
+    ap.add_argument("--grid-barrier", action="store_true",
+                    help="time grid-wide barriers in cooperative launches and exit")
     ap.add_argument("--hbm-ceiling", type=int, default=0, metavar="MIB",
                     help="only time a plain streaming read of MIB MiB (moe_debug_stream_read) and exit")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
@@ -384,6 +428,8 @@ def main() -> int:
         return copy_calibration(args.copy_calibration)
     if args.hbm_ceiling:
         return hbm_ceiling(args.hbm_ceiling)
+    if args.grid_barrier:
+        return grid_barrier_cost()
     if args.summarize_pmc:
         return summarize_pmc(args.summarize_pmc[0], args.summarize_pmc[1], TRAFFIC_FILE)
     if args.summarize_counters:

@@ -251,6 +251,14 @@ int moe_debug_expf(const float *x, float *y, uint64_t n, void *stream);
  * same bits.  No counterpart in the reference. */
 int moe_debug_decode_kernel(int32_t choice);
 
+/* Diagnostics: one cooperative launch of `blocks` blocks of 512 threads
+ * (all resident: more is MOE_EINVAL) that pass `barriers` grid-wide
+ * barriers (a device atomic per block on a counter, a polled generation
+ * word; each poll bounded, state[2] set if a bound was hit).  `state`:
+ * device u32[4], zero before the first call, left consistent for the next.
+ * No counterpart in the reference. */
+int moe_debug_grid_barrier(int32_t blocks, int32_t barriers, uint32_t *state, void *stream);
+
 /* Diagnostics: read `bytes` (a multiple of 16, 16-byte aligned device
  * memory) once with a grid-stride 16-byte-load kernel of `blocks` blocks
  * (eight loads in flight per thread; nontemporal != 0: nontemporal loads),

@@ -277,6 +277,42 @@ __global__ __launch_bounds__(256) void stream_read_kernel(const sr_u32x4 *__rest
     if (threadIdx.x == 0) out[blockIdx.x] = part[0] ^ part[1] ^ part[2] ^ part[3];
 }
 
+// Diagnostics: the cost of a grid-wide barrier.  `barriers` barriers of
+// every block of a cooperative launch: a release fence, one device atomic
+// per block on a shared counter, the last arrival resets it and advances a
+// generation word that the others poll.  The poll is bounded (2^20 reads;
+// state[2] = 1 records that a bound was hit), so no wave can spin forever.
+struct GridBarrier {
+    unsigned count, gen, err, pad;
+};
+
+__global__ __launch_bounds__(512) void grid_barrier_kernel(GridBarrier *b, int barriers) {
+    __shared__ unsigned s_gen;
+    if (threadIdx.x == 0) s_gen = __hip_atomic_load(&b->gen, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __syncthreads();
+    unsigned g = s_gen;
+    for (int i = 0; i < barriers; i++) {
+        __syncthreads();
+        if (threadIdx.x == 0) {
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+            const unsigned old = __hip_atomic_fetch_add(&b->count, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            if (old == gridDim.x - 1) {
+                __hip_atomic_store(&b->count, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                __hip_atomic_store(&b->gen, g + 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
+            } else {
+                for (unsigned n = 0; __hip_atomic_load(&b->gen, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == g; n++)
+                    if (n > (1u << 20)) {
+                        __hip_atomic_store(&b->err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                        break;
+                    }
+            }
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+        }
+        g++;
+        __syncthreads();
+    }
+}
+
 int launch_rc(const char *what) {
     const hipError_t e = hipGetLastError();
     return e == hipSuccess ? MOE_OK : fail(MOE_EHIP, "%s: %s", what, hipGetErrorString(e));
@@ -394,6 +430,24 @@ int moe_debug_stream_read(const void *src, uint64_t bytes, uint32_t *out, int32_
         hipLaunchKernelGGL(stream_read_kernel<false>, dim3(blocks), dim3(256), 0, (hipStream_t)stream, s4,
                            (size_t)(bytes / 16), out);
     return launch_rc("stream-read kernel");
+}
+
+int moe_debug_grid_barrier(int32_t blocks, int32_t barriers, uint32_t *state, void *stream) {
+    if (blocks <= 0 || barriers < 0 || !state) return fail(MOE_EINVAL, "moe_debug_grid_barrier: bad argument");
+    int dev = 0, cus = 0, per_cu = 0;
+    if (hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+        hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, (const void *)grid_barrier_kernel, 512, 0) !=
+            hipSuccess)
+        return fail(MOE_EHIP, "moe_debug_grid_barrier: device query failed");
+    if (blocks > cus * per_cu)
+        return fail(MOE_EINVAL, "moe_debug_grid_barrier: %d blocks cannot all be resident (%d per CU, %d CUs)", blocks,
+                    per_cu, cus);
+    GridBarrier *b = reinterpret_cast<GridBarrier *>(state);
+    void *args[] = {&b, &barriers};
+    const hipError_t e = hipLaunchCooperativeKernel((const void *)grid_barrier_kernel, dim3(blocks), dim3(512), args, 0,
+                                                    (hipStream_t)stream);
+    return e == hipSuccess ? MOE_OK : fail(MOE_EHIP, "grid-barrier kernel: %s", hipGetErrorString(e));
 }
 
 int moe_argmax(const float *x, int32_t rows, int32_t n, int32_t *out, void *stream) {

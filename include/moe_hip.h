@@ -251,6 +251,14 @@ int moe_debug_expf(const float *x, float *y, uint64_t n, void *stream);
  * same bits.  No counterpart in the reference. */
 int moe_debug_decode_kernel(int32_t choice);
 
+/* Diagnostics: which MFMA kernels the fast paths use, for every layer and
+ * projection of the process: 0 the two-pass kernels (weight codes times
+ * the activations' two f16 pieces, the block scale applied to each block's
+ * f32 sum), 1 the three-pass kernels (both operands in two f16 pieces).
+ * Returns the previous choice (>= 0) or MOE_EINVAL.  No counterpart in the
+ * reference. */
+int moe_debug_mfma_kernel(int32_t choice);
+
 /* Diagnostics: one cooperative launch of `blocks` blocks of 512 threads
  * (all resident: more is MOE_EINVAL) that pass `barriers` grid-wide
  * barriers (a device atomic per block on a counter, a polled generation

@@ -7,15 +7,21 @@
 //          epilogue forms h = silu(G) * U in f32 (src/model.rs:31-33).
 //   down : 256 rows of W_down, K = I (optionally split into 2 or 4 K parts,
 //          each written to its own part of y); output y in f32.
-// Four waves, one per SIMD.  Wave w owns every token row of the tile and 64
-// weight rows, so each weight value is dequantised exactly once per tile, in
-// the registers of the wave that multiplies it, and the BM x 64 f32
-// accumulators live in the wave's AGPRs (V_MFMA_F32_32X32X16_F16).
+// Four waves, one per SIMD (or eight, two per SIMD: SPLIT below).  Wave w
+// owns every token row of the tile and 64 weight rows, so each weight value
+// is decoded once per tile (per wave of a pair), in the registers of the
+// wave that multiplies it, and the f32 accumulators of its tiles live in
+// registers (V_MFMA_F32_32X32X16_F16).
 //
 // Precision.  The reference multiplies f32 activations by exactly
-// dequantised f32 weights d q (src/quant.rs:482-506).  Here both operands
-// are carried as two f16 pieces and three MFMAs accumulate
-// hi.hi + hi.lo + lo.hi in f32:
+// dequantised f32 weights d q (src/quant.rs:482-506).  The default
+// (two-pass) kernels carry the activations as two f16 pieces (below) and
+// the weights as their codes q, exact in f16: per 32-value block, four
+// MFMAs accumulate (hi + lo) q of both 16-value halves in f32 from zero,
+// and the block's d (f32) adds that sum into the tile with one fma; the
+// products are exact, so the activations' 22 bits bound the error.  The
+// three-pass kernels (kept for measurement) carry both operands as two f16
+// pieces and three MFMAs accumulate hi.hi + hi.lo + lo.hi in f32:
 //   weights      d q has at most 18 significant bits (11 of d, 7 of q), so
 //                hi = f16(d q) and lo = d q - hi (one fma, exact) hold it
 //                exactly; d is first multiplied by 2^wexp (exact), the
@@ -25,7 +31,8 @@
 //                putting the row's largest |v| in [2^14, 2^15): 22
 //                significant bits (the dropped lo.lo term and the rounding
 //                of lo are ~2^-22 of a product);
-// the epilogue multiplies by 2^-(ex + wexp), which is exact.  SwiGLU's
+// the epilogue multiplies by 2^-(ex + wexp) (two-pass: 2^-ex), which is
+// exact.  SwiGLU's
 // sigmoid uses the hardware exp (v_exp_f32, about 1 ulp), as the other
 // fast paths do; only routing needs glibc's expf bit for bit.
 //
@@ -47,6 +54,7 @@
 #include <hip/hip_fp16.h>
 #include <hip/hip_runtime.h>
 
+#include <atomic>
 #include <cstdlib>
 #include <type_traits>
 
@@ -291,6 +299,54 @@ __device__ inline void dequant(const uint32_t *v, half8 (&bh)[2], half8 (&bl)[2]
     }
 }
 
+// The codes of block kb as f16 (exact: |q| <= 128) for the two-pass
+// kernels, and the block's scale d: the MFMAs multiply the activations'
+// pieces by q, and d multiplies the block's f32 sums afterwards.
+__device__ inline void codesq4(uint32_t v, __half2 off2, uint32_t &q01, uint32_t &q23) {
+    q01 = h2_bits(__hsub2(as_h2(perm(0x64646464u, v, 0x04010400u)), off2));
+    q23 = h2_bits(__hsub2(as_h2(perm(0x64646464u, v, 0x04030402u)), off2));
+}
+template <int DT, int KB>
+__device__ inline void decode_codes(const uint32_t *v, half8 (&bq)[2], float &d, int h) {
+    const uint32_t s = KB == 0 ? (v[0] & 0xffffu) : (v[0] >> 16);
+    d = __half2float(__ushort_as_half((unsigned short)s));
+    uint32_t o[4];
+    if constexpr (DT == MOE_DT_Q4_0) {
+        const __half2 off2 = __floats2half2_rn(1032.0f, 1032.0f);
+        const uint32_t w0 = KB == 0 ? alignb(v[2], v[1], 2) : v[1];
+        const uint32_t w1 = KB == 0 ? alignb(v[3], v[2], 2) : v[2];
+        codesq4(w0 & 0x0f0f0f0fu, off2, o[0], o[1]);
+        codesq4(w1 & 0x0f0f0f0fu, off2, o[2], o[3]);
+        bq[0] = pack8(o);
+        codesq4((w0 >> 4) & 0x0f0f0f0fu, off2, o[0], o[1]);
+        codesq4((w1 >> 4) & 0x0f0f0f0fu, off2, o[2], o[3]);
+        bq[1] = pack8(o);
+    } else if constexpr (DT == MOE_DT_Q5_0) {
+        const __half2 off2 = __floats2half2_rn(1040.0f, 1040.0f);
+        const uint32_t qh = KB == 0 ? alignb(v[1], v[0], 2) : v[1];
+        const uint32_t w0 = KB == 0 ? alignb(v[3], v[2], 2) : v[2];
+        const uint32_t w1 = KB == 0 ? alignb(v[4], v[3], 2) : v[3];
+        const uint32_t hb = qh >> (8 * h);
+        codesq4((w0 & 0x0f0f0f0fu) | spread4(hb & 0xfu), off2, o[0], o[1]);
+        codesq4((w1 & 0x0f0f0f0fu) | spread4((hb >> 4) & 0xfu), off2, o[2], o[3]);
+        bq[0] = pack8(o);
+        codesq4(((w0 >> 4) & 0x0f0f0f0fu) | spread4((hb >> 16) & 0xfu), off2, o[0], o[1]);
+        codesq4(((w1 >> 4) & 0x0f0f0f0fu) | spread4((hb >> 20) & 0xfu), off2, o[2], o[3]);
+        bq[1] = pack8(o);
+    } else {
+        const __half2 off2 = __floats2half2_rn(1152.0f, 1152.0f);
+#pragma unroll
+        for (int m = 0; m < 2; m++) {
+            const uint32_t *c = v + 1 + (KB == 0 ? 3 : 2) * m;
+            const uint32_t w0 = KB == 0 ? alignb(c[1], c[0], 2) : c[0];
+            const uint32_t w1 = KB == 0 ? alignb(c[2], c[1], 2) : c[1];
+            codesq4(w0 ^ 0x80808080u, off2, o[0], o[1]);
+            codesq4(w1 ^ 0x80808080u, off2, o[2], o[3]);
+            bq[m] = pack8(o);
+        }
+    }
+}
+
 // Waves per SIMD of the MFMA kernels: 0 chooses per launch (below);
 // MOE_MFMA_SPLIT=1 or 2 forces one (for measurements).
 int mfma_split_forced() {
@@ -299,12 +355,26 @@ int mfma_split_forced() {
 }
 const int g_mfma_split = mfma_split_forced();
 
-// Two waves per SIMD pay once a tile holds two or more 32-token MFMA tiles
-// (each wave of a pair then multiplies at least one): measured on MI355X,
-// -4% at 128 tokens per expert (Mixtral T=512) and -12% at 128 (Qwen3
-// T=2048) in gate/up time, +3% at 8 tokens per expert (Mixtral T=32),
-// where the second wave of each pair has no tile and only loads.
+// Three-pass kernels: two waves per SIMD pay once a tile holds two or more
+// 32-token MFMA tiles (each wave of a pair then multiplies at least one):
+// measured on MI355X, -4% at 128 tokens per expert (Mixtral T=512) and -12%
+// at 128 (Qwen3 T=2048) in gate/up time, +3% at 8 tokens per expert
+// (Mixtral T=32), where the second wave of each pair has no tile and only
+// loads.
+// The two-pass kernels (launch split 3) run by default: measured on MI355X
+// against the three-pass ones, Mixtral T=512 1.106 -> 0.947 ms per layer
+// (gate/up 713 -> 612 µs, down 341 -> 282), Qwen3 T=2048 0.784 -> 0.724,
+// Mixtral T=32 0.404 -> 0.389, Qwen3 T=128 and V2-Lite T=256 within 1.5%.
+// MOE_MFMA_Q2=0 at load, or moe_debug_mfma_kernel(1), selects the
+// three-pass kernels (for measurements and tests).
+int mfma_q2_off() {
+    const char *e = getenv("MOE_MFMA_Q2");
+    return e && e[0] == '0';
+}
+std::atomic<int> g_mfma_q2_off{mfma_q2_off()};
+
 int mfma_split_for(double tokens_per_group) {
+    if (!g_mfma_q2_off.load()) return 3;
     if (g_mfma_split) return g_mfma_split;
     return tokens_per_group >= 48.0 ? 2 : 1;
 }
@@ -363,7 +433,15 @@ __device__ inline bool tile_of(const MfmaArgs &a, int mode, int gx, TileInfo &ti
 // step, which costs VALU time but no LDS traffic, and whenever one of them
 // waits for LDS, for the barrier or for its dequantisation, the other can
 // issue MFMAs.
-template <int DT, bool UP, int BM, int SPLIT>
+//
+// Q2 (two passes; SPLIT = 2 only): the weights enter the MFMAs as their
+// codes q (exact in f16) and each product is (hi + lo) q in two MFMAs; the
+// four MFMAs of a 32-value block accumulate the block's sum P from zero,
+// and the block's scale d then adds it into the tile: acc = fma(d, P, acc),
+// in f32.  Against the three passes of d q split into pieces this drops a
+// third of the MFMAs and most of the dequantisation; it adds 16 fmas per
+// lane per tile and block.  The ring, DMAs, waits and epilogue are shared.
+template <int DT, bool UP, int BM, int SPLIT, bool Q2>
 __global__ __launch_bounds__(256 * SPLIT, 1) __attribute__((amdgpu_waves_per_eu(SPLIT, SPLIT))) void mfma_kernel(MfmaArgs a, int mode, int gx, int ksplit) {
     using BL = BLay<DT>;
     constexpr int NS = ring_stages<DT, BM>();
@@ -374,6 +452,7 @@ __global__ __launch_bounds__(256 * SPLIT, 1) __attribute__((amdgpu_waves_per_eu(
     constexpr int NJ = 2 / SPLIT;         // weight regions one wave loads
     static_assert(NS == 3, "the step loop below assumes three stages");
     static_assert(SPLIT == 1 || SPLIT == 2, "one or two waves per SIMD");
+    static_assert(!Q2 || SPLIT == 2, "two-pass tiles keep their sums in VGPRs: two waves per SIMD");
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
     int *src_row = reinterpret_cast<int *>(smem + NS * RS);
     int *dst_row = src_row + BM;
@@ -397,7 +476,7 @@ __global__ __launch_bounds__(256 * SPLIT, 1) __attribute__((amdgpu_waves_per_eu(
     const int Icol = ti.shared ? a.I_s : a.I;
     const int valid = min(BM, ti.n - ti.m0);
     const int mt = (valid + 31) / 32;
-    const int wexp0 = W0.wexp, wexp1 = W1.wexp;
+    const int wexp0 = Q2 ? 0 : W0.wexp, wexp1 = Q2 ? 0 : W1.wexp;
 
     // Activation pieces and their row exponents.
     const uint16_t *ahi = UP ? a.xhi : (ti.shared ? a.hshi : a.hhi);
@@ -613,56 +692,157 @@ __global__ __launch_bounds__(256 * SPLIT, 1) __attribute__((amdgpu_waves_per_eu(
         constexpr bool work = MW > 0;
 
         const lds_p smB = sm + NS * 2 * AS;
-        // Prologue: steps 0 .. NS - 1 into stages 0 .. NS - 1, then wait for
-        // step 0.
-        for (int p = 0; p < NS; p++) dma_range(I0{}, std::integral_constant<int, ND>{}, p, p);
-        wait_vm_barrier<(NS - 1) * ND>();
-        if constexpr (work) {
-            read_a(sm, 0, 0);
-            read_rows(smB);
-            dequant_raw(I0{});
-        }
-        int st = 0;
-        // At the wait in group 2 of step s this wave's outstanding loads are
-        // those of steps s + 1 .. s + NS - 1 (ND each, in order); leaving the
-        // newest (NS - 2) ND outstanding completes step s + 1.  After the
-        // barrier that follows, no wave reads stage s again (its last reads,
-        // group 3's activations, come before the barrier), so group 3 sends
-        // step s + NS's loads into it.
         constexpr int WAIT = (NS - 2) * ND;
         static_assert(NS * ND < 64, "vmcnt range");
-        for (int s = 0; s < nsteps; s++) {
-            const lds_p sa = sm + st * 2 * AS;
-            const int st1 = st + 1 == NS ? 0 : st + 1;
+        if constexpr (!Q2) {
+            // Prologue: steps 0 .. NS - 1 into stages 0 .. NS - 1, then wait for
+            // step 0.
+            for (int p = 0; p < NS; p++) dma_range(I0{}, std::integral_constant<int, ND>{}, p, p);
+            wait_vm_barrier<(NS - 1) * ND>();
             if constexpr (work) {
-                // g = 0 (kb 0, m 0); read group 1.
-                read_a(sa, 1, 1);
+                read_a(sm, 0, 0);
+                read_rows(smB);
+                dequant_raw(I0{});
+            }
+            int st = 0;
+            // At the wait in group 2 of step s this wave's outstanding loads are
+            // those of steps s + 1 .. s + NS - 1 (ND each, in order); leaving the
+            // newest (NS - 2) ND outstanding completes step s + 1.  After the
+            // barrier that follows, no wave reads stage s again (its last reads,
+            // group 3's activations, come before the barrier), so group 3 sends
+            // step s + NS's loads into it.
+            for (int s = 0; s < nsteps; s++) {
+                const lds_p sa = sm + st * 2 * AS;
+                const int st1 = st + 1 == NS ? 0 : st + 1;
+                if constexpr (work) {
+                    // g = 0 (kb 0, m 0); read group 1.
+                    read_a(sa, 1, 1);
+                    __builtin_amdgcn_sched_barrier(0);
+                    mfmas(0, 0, 0);
+                    // g = 1 (kb 0, m 1): dequantise block 1, read group 2.
+                    dequant_raw(I1{});
+                    read_a(sa, 2, 0);
+                    mfmas(1, 0, 1);
+                    __builtin_amdgcn_sched_barrier(0);
+                    // g = 2 (kb 1, m 0): read group 3; then wait for this wave's
+                    // loads of step s + 1 and meet the other waves.
+                    read_a(sa, 3, 1);
+                    mfmas(0, 1, 0);
+                    __builtin_amdgcn_sched_barrier(0);
+                }
+                wait_vm_barrier<WAIT>();
                 __builtin_amdgcn_sched_barrier(0);
-                mfmas(0, 0, 0);
-                // g = 1 (kb 0, m 1): dequantise block 1, read group 2.
-                dequant_raw(I1{});
-                read_a(sa, 2, 0);
-                mfmas(1, 0, 1);
+                // g = 3 (kb 1, m 1): step s + 1's group 0 and weight rows; step
+                // s + NS's DMAs into this step's stage.
+                if constexpr (work) {
+                    read_a(sm + st1 * 2 * AS, 0, 0);
+                    read_rows(smB + st1 * BL::stage);
+                }
                 __builtin_amdgcn_sched_barrier(0);
-                // g = 2 (kb 1, m 0): read group 3; then wait for this wave's
+                mfmas_dma(1, 1, 1, I0{}, std::integral_constant<int, ND>{}, s + NS, st);
+                if constexpr (work) dequant_raw(I0{});
+                __builtin_amdgcn_sched_barrier(0);
+                st = st1;
+            }
+        } else {
+            // Two passes.  Unit u (< 2 MW) of a step is tile T0 + u % MW of
+            // block u / MW: its activations (hi and lo of both 16-value
+            // groups) sit in buffer u % 2, read one unit ahead.
+            half8 bq[2][2][2];  // [kb][j][m] codes
+            float dq[2][2];     // [kb][j] scale of the lane's row
+            half8 A[2][4];      // hi m0, lo m0, hi m1, lo m1
+            const floatx16 zero = {};
+            auto decode = [&](auto kb_c) {
+                constexpr int kb = decltype(kb_c)::value;
+#pragma unroll
+                for (int j = 0; j < 2; j++) {
+                    uint32_t v[7];
+#pragma unroll
+                    for (int k = 0; k < SL::n[kb]; k++) {
+                        const int b = SL::base[kb][k];
+                        v[k] = SL::hm[kb][k] ? (hf ? rowv[j][b + 2] : rowv[j][b]) : rowv[j][b];
+                    }
+                    decode_codes<DT, kb>(v, bq[kb][j], dq[kb][j], hf);
+                }
+            };
+            auto read_unit = [&](lds_p sa, int u, half8(&Ab)[4]) {
+                const int kb = u / MWR, t = u % MWR;
+                const lds_p p0 = sa + aoff[2 * kb] + 4096 * (T0 + t);
+                const lds_p p1 = sa + aoff[2 * kb + 1] + 4096 * (T0 + t);
+                Ab[0] = lds_h8(p0), Ab[1] = lds_h8(p0 + AS), Ab[2] = lds_h8(p1), Ab[3] = lds_h8(p1 + AS);
+            };
+            // Unit u's eight MFMAs (the two regions' chains alternate), with
+            // DMAs [LO, HI) of step `step` spread between them, then the
+            // block sums into the tiles.
+            auto unit = [&](auto u_c, auto lo_c, auto hi_c, int step, int stg) {
+                constexpr int u = decltype(u_c)::value, kb = u / MWR, t = u % MWR, b = u % 2;
+                constexpr int LO = decltype(lo_c)::value, HI = decltype(hi_c)::value;
+                floatx16 p[2];
+                auto mf = [&](auto i_c) {
+                    constexpr int i = decltype(i_c)::value, j = i & 1, q = i >> 1;  // q: hi m0, lo m0, hi m1, lo m1
+                    p[j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(A[b][q], bq[kb][j][q >> 1], i < 2 ? zero : p[j], 0,
+                                                                   0, 0);
+                    dma_range(std::integral_constant<int, LO + i * (HI - LO) / 8>{},
+                              std::integral_constant<int, LO + (i + 1) * (HI - LO) / 8>{}, step, stg);
+                };
+                mf(std::integral_constant<int, 0>{});
+                mf(std::integral_constant<int, 1>{});
+                mf(std::integral_constant<int, 2>{});
+                mf(std::integral_constant<int, 3>{});
+                mf(std::integral_constant<int, 4>{});
+                mf(std::integral_constant<int, 5>{});
+                mf(std::integral_constant<int, 6>{});
+                mf(std::integral_constant<int, 7>{});
+#pragma unroll
+                for (int j = 0; j < 2; j++)
+#pragma unroll
+                    for (int v = 0; v < 16; v++) acc[t][j][v] = fmaf(dq[kb][j], p[j][v], acc[t][j][v]);
+            };
+            auto units_to = [&](auto u_c, auto self, const lds_p sa) {
+                constexpr int u = decltype(u_c)::value;
+                if constexpr (u + 1 < 2 * MW) {
+                    read_unit(sa, u + 1, A[(u + 1) % 2]);
+                    if constexpr (u == 0) decode(I1{});
+                    unit(u_c, I0{}, I0{}, 0, 0);
+                    __builtin_amdgcn_sched_barrier(0);
+                    self(std::integral_constant<int, u + 1>{}, self, sa);
+                }
+            };
+
+            for (int p = 0; p < NS; p++) dma_range(I0{}, std::integral_constant<int, ND>{}, p, p);
+            wait_vm_barrier<(NS - 1) * ND>();
+            if constexpr (work) {
+                read_rows(smB);
+                decode(I0{});
+                read_unit(sm, 0, A[0]);
+            }
+            int st = 0;
+            for (int s = 0; s < nsteps; s++) {
+                const lds_p sa = sm + st * 2 * AS;
+                const int st1 = st + 1 == NS ? 0 : st + 1;
+                // Units 0 .. 2 MW - 2; the last unit's activations are read
+                // during the one before it.
+                if constexpr (work) units_to(I0{}, units_to, sa);
+                // Every read of this stage is done: wait for this wave's
                 // loads of step s + 1 and meet the other waves.
-                read_a(sa, 3, 1);
-                mfmas(0, 1, 0);
+                wait_vm_barrier<WAIT>();
                 __builtin_amdgcn_sched_barrier(0);
+                if constexpr (work) {
+                    // The next step's first unit and weight rows, then this
+                    // step's last unit with step s + NS's DMAs between its
+                    // MFMAs, then the next step's block-0 codes.
+                    read_unit(sm + st1 * 2 * AS, 0, A[0]);
+                    read_rows(smB + st1 * BL::stage);
+                    __builtin_amdgcn_sched_barrier(0);
+                    unit(std::integral_constant<int, 2 * MWR - 1>{}, I0{}, std::integral_constant<int, ND>{}, s + NS,
+                         st);
+                    decode(I0{});
+                } else {
+                    dma_range(I0{}, std::integral_constant<int, ND>{}, s + NS, st);
+                }
+                __builtin_amdgcn_sched_barrier(0);
+                st = st1;
             }
-            wait_vm_barrier<WAIT>();
-            __builtin_amdgcn_sched_barrier(0);
-            // g = 3 (kb 1, m 1): step s + 1's group 0 and weight rows; step
-            // s + NS's DMAs into this step's stage.
-            if constexpr (work) {
-                read_a(sm + st1 * 2 * AS, 0, 0);
-                read_rows(smB + st1 * BL::stage);
-            }
-            __builtin_amdgcn_sched_barrier(0);
-            mfmas_dma(1, 1, 1, I0{}, std::integral_constant<int, ND>{}, s + NS, st);
-            if constexpr (work) dequant_raw(I0{});
-            __builtin_amdgcn_sched_barrier(0);
-            st = st1;
         }
     };
     static_assert(MTMAX == 5 || MTMAX == 4, "one case per 32-token tile count");
@@ -735,21 +915,23 @@ __global__ __launch_bounds__(256 * SPLIT, 1) __attribute__((amdgpu_waves_per_eu(
     }
 }
 
-template <int DT, bool UP, int BM, int SPLIT>
+template <int DT, bool UP, int BM, int SPLIT, bool Q2>
 hipError_t launch_split(dim3 grid, const MfmaArgs &a, int mode, int ksplit, hipStream_t s) {
     constexpr int lds = lds_bytes<DT, BM>();
     static const hipError_t attr = hipFuncSetAttribute(
-        reinterpret_cast<const void *>(&mfma_kernel<DT, UP, BM, SPLIT>), hipFuncAttributeMaxDynamicSharedMemorySize,
-        lds);
+        reinterpret_cast<const void *>(&mfma_kernel<DT, UP, BM, SPLIT, Q2>),
+        hipFuncAttributeMaxDynamicSharedMemorySize, lds);
     if (attr != hipSuccess) return attr;
-    hipLaunchKernelGGL((mfma_kernel<DT, UP, BM, SPLIT>), grid, dim3(256 * SPLIT), lds, s, a, mode, (int)grid.x,
+    hipLaunchKernelGGL((mfma_kernel<DT, UP, BM, SPLIT, Q2>), grid, dim3(256 * SPLIT), lds, s, a, mode, (int)grid.x,
                        ksplit);
     return hipGetLastError();
 }
+// split 3: the two-pass kernel (two waves per SIMD).
 template <int DT, bool UP, int BM>
 hipError_t launch_one(dim3 grid, const MfmaArgs &a, int mode, int ksplit, int split, hipStream_t s) {
-    return split == 2 ? launch_split<DT, UP, BM, 2>(grid, a, mode, ksplit, s)
-                      : launch_split<DT, UP, BM, 1>(grid, a, mode, ksplit, s);
+    if (split == 3) return launch_split<DT, UP, BM, 2, true>(grid, a, mode, ksplit, s);
+    return split == 2 ? launch_split<DT, UP, BM, 2, false>(grid, a, mode, ksplit, s)
+                      : launch_split<DT, UP, BM, 1, false>(grid, a, mode, ksplit, s);
 }
 
 template <bool UP>
@@ -936,5 +1118,7 @@ hipError_t launch_scale_max(const ExpertDev *experts, int n, unsigned *out, hipS
     hipLaunchKernelGGL(scale_max_kernel, dim3(n, 3, 16), dim3(256), 0, s, experts, out);
     return hipGetLastError();
 }
+
+int set_mfma_kernel(int choice) { return g_mfma_q2_off.exchange(choice == 1 ? 1 : 0); }
 
 }  // namespace moe

@@ -1078,6 +1078,11 @@ int moe_layer_route(moe_layer *L, const float *x, int32_t t, moe_route *routes, 
     return route_and_dispatch(L, c, w, x, t, 0, false, routes, nullptr, nullptr, nullptr, logits, s);
 }
 
+int moe_debug_mfma_kernel(int32_t choice) {
+    if (choice < 0 || choice > 1) return fail(MOE_EINVAL, "moe_debug_mfma_kernel: choice %d (0 or 1)", choice);
+    return set_mfma_kernel(choice);
+}
+
 int moe_debug_decode_kernel(int32_t choice) {
     if (choice < 0 || choice > 2) return fail(MOE_EINVAL, "moe_debug_decode_kernel: choice %d (0, 1 or 2)", choice);
     return set_decode_kernel(choice);

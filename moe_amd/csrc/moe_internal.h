@@ -226,6 +226,9 @@ hipError_t launch_decode_encode(const DecodeArgs &a, hipStream_t s);
 // The one-token gate/up kernel choice (moe_debug_decode_kernel); returns
 // the previous one.
 int set_decode_kernel(int choice);
+// The MFMA kernels (moe_debug_mfma_kernel): 0 two-pass, 1 three-pass;
+// returns the previous one.
+int set_mfma_kernel(int choice);
 // The down projection and combine over the units of h.
 hipError_t launch_decode_down(const DecodeArgs &a, int dt_routed, int dt_shared, hipStream_t s);
 // Whether the shared expert's down projection runs as a launch of its own

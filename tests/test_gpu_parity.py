@@ -245,11 +245,37 @@ def test_decode_up_kernels_agree(ctx, oracle, name, scale):
     log(f"{name}: one-token gate/up kernels agree bit for bit, max rel err {rel_err(got[2]['out'], out):.2e}")
 
 
+@pytest.mark.parametrize("name,t", [("mixtral", 512), ("qwen3", 300), ("deepseek_v3", 64), ("qwen2_moe", 64),
+                                    ("tiny_mixtral", 257)])
+def test_mfma_three_pass_kernels(ctx, oracle, name, t):
+    """The three-pass MFMA kernels (both operands in two f16 pieces), which
+    the two-pass default replaced, still match the CPU path."""
+    from moe_amd import _lib as L
+    from moe_amd import synth
+
+    host, gl, ol = layer_pair(ctx, oracle, name)
+    x = synth.activations(SEED + 11, t, host.shape.hidden)
+    out, sel, w, hits, stats = ol.forward(x)
+    prev = L.lib().moe_debug_mfma_kernel(1)
+    assert prev >= 0
+    try:
+        g = run_gpu(gl, x, mode=3)
+    finally:
+        L.lib().moe_debug_mfma_kernel(prev)
+        gl.set_mode(0)
+    assert_routing_equal(g, sel, w, f"{name} T={t}")
+    err = rel_err(g["out"], out)
+    log(f"{name} T={t} three-pass MFMA: max rel err {err:.2e}")
+    record("layer", f"{name} T={t} three-pass MFMA", err)
+    assert err <= TOL, f"{name} T={t} three-pass: max rel err {err:.3e}"
+
+
 def test_decode_kernel_choice_rejects_bad_values(ctx):
     from moe_amd import _lib as L
 
     assert L.lib().moe_debug_decode_kernel(3) == L.MOE_EINVAL
     assert L.lib().moe_debug_decode_kernel(-1) == L.MOE_EINVAL
+    assert L.lib().moe_debug_mfma_kernel(2) == L.MOE_EINVAL
 
 
 @pytest.mark.parametrize("kind", ["disabled", "forced", "top1", "topE", "forced2"])

@@ -747,8 +747,14 @@ __global__ __launch_bounds__(256 * SPLIT, 1) __attribute__((amdgpu_waves_per_eu(
         } else {
             // Two passes.  Unit u (< 2 MW) of a step is tile T0 + u % MW of
             // block u / MW: its activations (hi and lo of both 16-value
-            // groups) sit in buffer u % 2, read one unit ahead.
-            half8 bq[2][2][2];  // [kb][j][m] codes
+            // groups) sit in buffer u % 2, read one unit ahead.  Its eight
+            // MFMAs (the two regions' chains alternating: back-to-back
+            // MFMAs on one accumulator stall) leave the block sums in
+            // ps[u % 2]; the fmas that add them into the tiles follow the
+            // next unit's MFMAs, so the matrix cores need not wait for them.
+            // One block's codes are held at a time: block 1's are decoded
+            // once block 0's last unit has issued its MFMAs.
+            half8 bq[1][2][2];  // [j][m] codes of the block in progress
             float dq[2][2];     // [kb][j] scale of the lane's row
             half8 A[2][4];      // hi m0, lo m0, hi m1, lo m1
             const floatx16 zero = {};
@@ -762,7 +768,7 @@ __global__ __launch_bounds__(256 * SPLIT, 1) __attribute__((amdgpu_waves_per_eu(
                         const int b = SL::base[kb][k];
                         v[k] = SL::hm[kb][k] ? (hf ? rowv[j][b + 2] : rowv[j][b]) : rowv[j][b];
                     }
-                    decode_codes<DT, kb>(v, bq[kb][j], dq[kb][j], hf);
+                    decode_codes<DT, kb>(v, bq[0][j], dq[kb][j], hf);
                 }
             };
             auto read_unit = [&](lds_p sa, int u, half8(&Ab)[4]) {
@@ -771,17 +777,14 @@ __global__ __launch_bounds__(256 * SPLIT, 1) __attribute__((amdgpu_waves_per_eu(
                 const lds_p p1 = sa + aoff[2 * kb + 1] + 4096 * (T0 + t);
                 Ab[0] = lds_h8(p0), Ab[1] = lds_h8(p0 + AS), Ab[2] = lds_h8(p1), Ab[3] = lds_h8(p1 + AS);
             };
-            // Unit u's eight MFMAs (the two regions' chains alternate), with
-            // DMAs [LO, HI) of step `step` spread between them, then the
-            // block sums into the tiles.
-            auto unit = [&](auto u_c, auto lo_c, auto hi_c, int step, int stg) {
-                constexpr int u = decltype(u_c)::value, kb = u / MWR, t = u % MWR, b = u % 2;
+            floatx16 ps[2][2];  // [unit parity][j]
+            auto unit_mfma = [&](auto u_c, auto lo_c, auto hi_c, int step, int stg) {
+                constexpr int u = decltype(u_c)::value, b = u % 2;
                 constexpr int LO = decltype(lo_c)::value, HI = decltype(hi_c)::value;
-                floatx16 p[2];
                 auto mf = [&](auto i_c) {
-                    constexpr int i = decltype(i_c)::value, j = i & 1, q = i >> 1;  // q: hi m0, lo m0, hi m1, lo m1
-                    p[j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(A[b][q], bq[kb][j][q >> 1], i < 2 ? zero : p[j], 0,
-                                                                   0, 0);
+                    constexpr int i = decltype(i_c)::value, j = i & 1, q = i >> 1;
+                    ps[b][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(A[b][q], bq[0][j][q >> 1], i < 2 ? zero : ps[b][j],
+                                                                      0, 0, 0);
                     dma_range(std::integral_constant<int, LO + i * (HI - LO) / 8>{},
                               std::integral_constant<int, LO + (i + 1) * (HI - LO) / 8>{}, step, stg);
                 };
@@ -793,22 +796,25 @@ __global__ __launch_bounds__(256 * SPLIT, 1) __attribute__((amdgpu_waves_per_eu(
                 mf(std::integral_constant<int, 5>{});
                 mf(std::integral_constant<int, 6>{});
                 mf(std::integral_constant<int, 7>{});
+            };
+            auto unit_fma = [&](auto u_c) {
+                constexpr int u = decltype(u_c)::value, kb = u / MWR, t = u % MWR, b = u % 2;
 #pragma unroll
                 for (int j = 0; j < 2; j++)
 #pragma unroll
-                    for (int v = 0; v < 16; v++) acc[t][j][v] = fmaf(dq[kb][j], p[j][v], acc[t][j][v]);
+                    for (int v = 0; v < 16; v++) acc[t][j][v] = fmaf(dq[kb][j], ps[b][j][v], acc[t][j][v]);
             };
             auto units_to = [&](auto u_c, auto self, const lds_p sa) {
                 constexpr int u = decltype(u_c)::value;
                 if constexpr (u + 1 < 2 * MW) {
                     read_unit(sa, u + 1, A[(u + 1) % 2]);
-                    if constexpr (u == 0) decode(I1{});
-                    unit(u_c, I0{}, I0{}, 0, 0);
+                    unit_mfma(u_c, I0{}, I0{}, 0, 0);
+                    if constexpr (u > 0) unit_fma(std::integral_constant<int, u - 1>{});
+                    if constexpr (u == MW - 1) decode(I1{});
                     __builtin_amdgcn_sched_barrier(0);
                     self(std::integral_constant<int, u + 1>{}, self, sa);
                 }
             };
-
             for (int p = 0; p < NS; p++) dma_range(I0{}, std::integral_constant<int, ND>{}, p, p);
             wait_vm_barrier<(NS - 1) * ND>();
             if constexpr (work) {
@@ -834,8 +840,10 @@ __global__ __launch_bounds__(256 * SPLIT, 1) __attribute__((amdgpu_waves_per_eu(
                     read_unit(sm + st1 * 2 * AS, 0, A[0]);
                     read_rows(smB + st1 * BL::stage);
                     __builtin_amdgcn_sched_barrier(0);
-                    unit(std::integral_constant<int, 2 * MWR - 1>{}, I0{}, std::integral_constant<int, ND>{}, s + NS,
-                         st);
+                    unit_mfma(std::integral_constant<int, 2 * MWR - 1>{}, I0{}, std::integral_constant<int, ND>{},
+                              s + NS, st);
+                    unit_fma(std::integral_constant<int, 2 * MWR - 2>{});
+                    unit_fma(std::integral_constant<int, 2 * MWR - 1>{});
                     decode(I0{});
                 } else {
                     dma_range(I0{}, std::integral_constant<int, ND>{}, s + NS, st);

@@ -313,12 +313,32 @@ __global__ __launch_bounds__(512) void grid_barrier_kernel(GridBarrier *b, int b
     }
 }
 
+// y = sum over the k parts (p ascending) of parts[p n + i]; residual[i] +=
+// y[i] when given.  The K parts of a split projection.
+__global__ __launch_bounds__(256) void sum_parts_kernel(const float *__restrict__ parts, int k, size_t n,
+                                                        float *__restrict__ y, float *__restrict__ residual) {
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x) {
+        float v = parts[i];
+        for (int p = 1; p < k; p++) v = v + parts[(size_t)p * n + i];
+        y[i] = v;
+        if (residual) residual[i] = residual[i] + v;
+    }
+}
+
 int launch_rc(const char *what) {
     const hipError_t e = hipGetLastError();
     return e == hipSuccess ? MOE_OK : fail(MOE_EHIP, "%s: %s", what, hipGetErrorString(e));
 }
 
 }  // namespace
+
+hipError_t launch_sum_parts(const float *parts, int k, size_t n, float *y, float *residual, hipStream_t s) {
+    if (n == 0) return hipSuccess;
+    if (k <= 0) return hipErrorInvalidValue;
+    const unsigned blocks = (unsigned)std::min<size_t>((n + 255) / 256, 4096);
+    hipLaunchKernelGGL(sum_parts_kernel, dim3(blocks), dim3(256), 0, s, parts, k, n, y, residual);
+    return hipGetLastError();
+}
 
 hipError_t launch_add(float *dst, const float *src, size_t n, hipStream_t s) {
     if (n == 0) return hipSuccess;

@@ -1154,17 +1154,50 @@ namespace {
 
 // Tokens up to which the GEMV beats the MFMA path for one matrix.
 constexpr int kLinearGemvMaxT = 8;
+constexpr size_t kLinearPartsMax = (size_t)32 << 20;  // bytes of K-split partial outputs
 
-size_t linear_ws_layout(const moe_linear *l, int max_t, char *base, uint16_t **hi, uint16_t **lo, int32_t **ex) {
+// K parts of one MFMA projection over t tokens.  A block walks its K range
+// one ring step at a time (~1.5 µs per 64 values at one token tile), so a
+// matrix of few 256-row tiles leaves the CUs idle and each block slow:
+// measured on MI355X, V2-Lite's 2048 -> 3072 projection at T=32 took 50 µs
+// in 12 blocks.  Split K (each part two steps or more) until the grid has
+// 256 blocks; the parts are summed in order afterwards.
+int linear_ksplit(const moe_linear *l, int t) {
+    const MatDev &m = l->host.m[2];
+    const long long blocks = (long long)((t + l->bm - 1) / l->bm) * ((m.rows + 255) / 256);
+    int ks = 1;
+    while (ks < 16 && blocks * ks < 256 && m.cols % (2 * ks * 64) == 0 && m.cols / (2 * ks) >= 128 &&
+           (size_t)2 * ks * t * m.rows * 4 <= kLinearPartsMax)
+        ks *= 2;
+    return ks;
+}
+
+// Parts buffer for any t <= max_t: ks * t * rows floats, largest at the top
+// of a run of t with the same number of token tiles.
+size_t linear_parts_bytes(const moe_linear *l, int max_t) {
+    size_t best = 0;
+    for (int top = l->bm;; top += l->bm) {
+        const int t = std::min(top, max_t);
+        const int ks = linear_ksplit(l, t);
+        if (ks > 1) best = std::max(best, (size_t)ks * t * l->host.m[2].rows * 4);
+        if (top >= max_t) break;
+    }
+    return best;
+}
+
+size_t linear_ws_layout(const moe_linear *l, int max_t, char *base, uint16_t **hi, uint16_t **lo, int32_t **ex,
+                        float **parts) {
     const size_t T = (size_t)max_t, K = (size_t)l->host.m[2].cols;
     const bool pieces = l->mfma && max_t > kLinearGemvMaxT;
     const size_t a = pieces ? align_up(T * K * 2, 256) : 0, b = pieces ? align_up(T * 4, 256) : 0;
+    const size_t c = pieces ? align_up(linear_parts_bytes(l, max_t), 256) : 0;
     if (base && pieces) {
         *hi = reinterpret_cast<uint16_t *>(base);
         *lo = reinterpret_cast<uint16_t *>(base + a);
         *ex = reinterpret_cast<int32_t *>(base + 2 * a);
+        *parts = c ? reinterpret_cast<float *>(base + 2 * a + b) : nullptr;
     }
-    return std::max<size_t>(2 * a + b, 256);
+    return std::max<size_t>(2 * a + b + c, 256);
 }
 
 }  // namespace
@@ -1227,7 +1260,7 @@ void moe_linear_destroy(moe_linear *l) {
 
 int moe_linear_workspace_size(const moe_linear *l, int32_t max_t, uint64_t *bytes) {
     if (!l || max_t <= 0 || !bytes) return fail(MOE_EINVAL, "moe_linear_workspace_size: bad argument");
-    *bytes = linear_ws_layout(l, max_t, nullptr, nullptr, nullptr, nullptr);
+    *bytes = linear_ws_layout(l, max_t, nullptr, nullptr, nullptr, nullptr, nullptr);
     return MOE_OK;
 }
 
@@ -1239,13 +1272,15 @@ int moe_linear_forward(moe_linear *l, const float *x, int32_t t, float *y, float
     const MatDev &m = l->host.m[2];
     hipError_t e = hipSuccess;
     if (l->mfma && t > kLinearGemvMaxT) {
-        const size_t need = linear_ws_layout(l, t, nullptr, nullptr, nullptr, nullptr);
+        const size_t need = linear_ws_layout(l, t, nullptr, nullptr, nullptr, nullptr, nullptr);
         if (!workspace || workspace_bytes < need || (uintptr_t)workspace % 256)
             return fail(MOE_EINVAL, "moe_linear_forward: %d tokens need a 256-byte-aligned workspace of %zu bytes", t,
                         need);
         uint16_t *hi = nullptr, *lo = nullptr;
         int32_t *ex = nullptr;
-        linear_ws_layout(l, t, static_cast<char *>(workspace), &hi, &lo, &ex);
+        float *parts = nullptr;
+        linear_ws_layout(l, t, static_cast<char *>(workspace), &hi, &lo, &ex, &parts);
+        const int ks = linear_ksplit(l, t);
         MfmaArgs a{};
         a.experts = l->dev;
         a.E = 0;
@@ -1255,12 +1290,18 @@ int moe_linear_forward(moe_linear *l, const float *x, int32_t t, float *y, float
         a.hshi = hi;
         a.hslo = lo;
         a.hsex = ex;
-        a.ys = y;
+        a.ys = ks > 1 ? parts : y;
         a.yspart = (size_t)t * m.rows;
-        a.ksplit = 1;
+        a.ksplit = ks;
         a.shared_tiles = (t + l->bm - 1) / l->bm;
         e = launch_split_rows(x, t, m.cols, hi, lo, ex, s);
         if (e == hipSuccess) e = launch_mfma_single(false, a, l->bm, l->host, s);
+        if (e == hipSuccess && ks > 1) {
+            // y = the parts summed in order; residual += y in the same pass.
+            e = launch_sum_parts(parts, ks, (size_t)t * m.rows, y, residual, s);
+            if (e != hipSuccess) return hip_fail(e, "linear K parts");
+            return MOE_OK;
+        }
     } else {
         GemvArgs a{};
         a.experts = l->dev;

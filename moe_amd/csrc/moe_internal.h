@@ -187,6 +187,9 @@ hipError_t launch_gemv_down(const GemvArgs &a, const ExpertDev &host_e0, const E
 hipError_t launch_gemv_down_single(const GemvArgs &a, const ExpertDev &ex, hipStream_t s);
 // dst[i] += src[i] for n values.
 hipError_t launch_add(float *dst, const float *src, size_t n, hipStream_t s);
+// y[i] = parts[i] + parts[n + i] + ... (k parts, in order); residual[i] +=
+// y[i] when residual is not null.
+hipError_t launch_sum_parts(const float *parts, int k, size_t n, float *y, float *residual, hipStream_t s);
 // Down projection with the combine, shared expert and residual folded in
 // (T <= kFusedMaxT): writes out (and residual) directly.
 constexpr int kFusedMaxT = 8;

@@ -24,6 +24,12 @@
  *     owns, so calls on different streams (or workspaces) share no scratch.
  *     Host threads may call concurrently; moe_layer_set_routing and
  *     moe_layer_set_mode apply to calls made after they return.
+ *   - Inside a forward call on the few-tokens or MFMA path, a layer's shared
+ *     expert runs on a stream the context owns, which waits for `stream`
+ *     (an event) before it starts, and `stream` waits for it before the
+ *     combine: the call stays ordered on `stream` as a whole.  Calls on a
+ *     stream that is being captured into a graph, and
+ *     moe_layer_forward_noalloc, keep every launch on `stream`.
  */
 #ifndef MOE_HIP_H
 #define MOE_HIP_H
@@ -113,8 +119,9 @@ typedef struct moe_route {
 
 /* ------------------------------------------------------------------ setup */
 
-/* Open a context on HIP device `device`.  Replaces Model::load's ownership of
- * the Store (src/model.rs:336-341). */
+/* Open a context on HIP device `device`, with one non-blocking stream of
+ * default priority for the layers' shared experts.  Replaces Model::load's
+ * ownership of the Store (src/model.rs:336-341). */
 int moe_ctx_create(int device, moe_ctx **out);
 void moe_ctx_destroy(moe_ctx *ctx);
 

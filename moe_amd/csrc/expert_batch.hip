@@ -408,4 +408,12 @@ hipError_t launch_batch_down(const BatchArgs &a, const ExpertDev &e0, const Expe
     return down_dt(sh->m[2].dt, a, sh->m[2].cols, a.shared_tiles, 1, s);
 }
 
+hipError_t launch_batch_up_shared(const BatchArgs &a, const ExpertDev &sh, hipStream_t s) {
+    return a.shared_tiles ? up_dt(sh.m[0].dt, a, sh.m[0].rows, a.shared_tiles, 1, s) : hipSuccess;
+}
+
+hipError_t launch_batch_down_shared(const BatchArgs &a, const ExpertDev &sh, hipStream_t s) {
+    return a.shared_tiles ? down_dt(sh.m[2].dt, a, sh.m[2].cols, a.shared_tiles, 1, s) : hipSuccess;
+}
+
 }  // namespace moe

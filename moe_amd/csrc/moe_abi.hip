@@ -82,6 +82,13 @@ struct moe_ctx {
     int device = 0;
     std::mutex mu;
     std::vector<Region> regions;
+    // The stream the shared expert's kernels run on beside the routed ones
+    // (few-tokens and MFMA paths), and the events that fork it from and
+    // join it to the caller's stream; side_mu makes each record-and-wait
+    // pair atomic between callers.  Null if they could not be created.
+    hipStream_t side = nullptr;
+    hipEvent_t ev_fork = nullptr, ev_join = nullptr;
+    std::mutex side_mu;
 };
 
 struct moe_layer {
@@ -335,6 +342,7 @@ struct CallState {
     int mode;
     int k;
     bool profile;
+    bool side = true;  // the shared expert may run on the context's side stream
     GateParams gp;
 };
 
@@ -435,6 +443,19 @@ int route_and_dispatch(moe_layer *L, const CallState &c, Workspace &w, const flo
     });
 }
 
+// The side stream waits for what stream s has queued so far (fork), or s
+// for what the side stream has (join).
+hipError_t fork_side(moe_ctx *ctx, hipStream_t s) {
+    std::lock_guard<std::mutex> g(ctx->side_mu);
+    hipError_t e = hipEventRecord(ctx->ev_fork, s);
+    return e == hipSuccess ? hipStreamWaitEvent(ctx->side, ctx->ev_fork, 0) : e;
+}
+hipError_t join_side(moe_ctx *ctx, hipStream_t s) {
+    std::lock_guard<std::mutex> g(ctx->side_mu);
+    hipError_t e = hipEventRecord(ctx->ev_join, ctx->side);
+    return e == hipSuccess ? hipStreamWaitEvent(s, ctx->ev_join, 0) : e;
+}
+
 // The routed layer on workspace w (sized for at least t tokens of c.k
 // experts).
 int forward_on(moe_layer *L, const CallState &c, Workspace &w, const float *x, int t, float *out, float *residual,
@@ -468,6 +489,21 @@ int forward_on(moe_layer *L, const CallState &c, Workspace &w, const float *x, i
 
     const ExpertDev &e0 = L->experts_host[0];
     const ExpertDev *sh = L->has_shared ? &L->experts_host[L->E] : nullptr;
+    // The shared expert on the context's side stream, forked from s after
+    // the activations are encoded and joined back before the combine
+    // (few-tokens and MFMA paths).  Not while stages are being timed on s,
+    // nor for the no-allocation entry, nor while s is being captured into a
+    // graph (the capture then holds one stream's launches only).
+    bool side = sh && c.side && !c.profile && L->ctx->side && (path == kBatch || path == kMfma);
+    if (side && s) {
+        hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+        if (hipStreamIsCapturing(s, &cs) != hipSuccess) {
+            (void)hipGetLastError();  // the launches below report their own errors
+            side = false;
+        } else if (cs != hipStreamCaptureStatusNone) {
+            side = false;
+        }
+    }
     hipError_t e = hipSuccess;
     int ksplit = 1;
     if (path == kDecode) {
@@ -541,22 +577,33 @@ int forward_on(moe_layer *L, const CallState &c, Workspace &w, const float *x, i
             return e == hipSuccess ? MOE_OK : hip_fail(e, "activation encoding");
         });
         if (rc) return rc;
+        if (side) {
+            // The shared expert (its own buffers: hs, hsq, ys) beside the
+            // routed experts; the combine waits for both.
+            e = fork_side(L->ctx, s);
+            if (e == hipSuccess) e = launch_batch_up_shared(b, *sh, L->ctx->side);
+            if (e == hipSuccess) e = launch_qenc(w.hs, t, L->I_s, w.hsq, L->ctx->side);
+            if (e == hipSuccess) e = launch_batch_down_shared(b, *sh, L->ctx->side);
+            if (e != hipSuccess) return hip_fail(e, "shared expert (few-tokens kernels)");
+        }
+        const ExpertDev *shs = side ? nullptr : sh;  // the shared expert on stream s
         rc = stage(L, c.profile, 3, s, [&] {
-            e = launch_batch_up(b, e0, sh, s);
+            e = launch_batch_up(b, e0, shs, s);
             return e == hipSuccess ? MOE_OK : hip_fail(e, "few-tokens gate/up kernel");
         });
         if (rc) return rc;
         rc = stage(L, c.profile, 6, s, [&] {
             e = launch_qenc(w.h, t * k, L->I, w.hq, s);
-            if (e == hipSuccess && sh) e = launch_qenc(w.hs, t, L->I_s, w.hsq, s);
+            if (e == hipSuccess && shs) e = launch_qenc(w.hs, t, L->I_s, w.hsq, s);
             return e == hipSuccess ? MOE_OK : hip_fail(e, "activation encoding");
         });
         if (rc) return rc;
         rc = stage(L, c.profile, 4, s, [&] {
-            e = launch_batch_down(b, e0, sh, s);
+            e = launch_batch_down(b, e0, shs, s);
             return e == hipSuccess ? MOE_OK : hip_fail(e, "few-tokens down kernel");
         });
         if (rc) return rc;
+        if (side && (e = join_side(L->ctx, s)) != hipSuccess) return hip_fail(e, "shared expert join");
     } else if (path == kMfma) {
         MfmaArgs m{};
         m.experts = L->experts_dev;
@@ -600,22 +647,31 @@ int forward_on(moe_layer *L, const CallState &c, Workspace &w, const float *x, i
             return e == hipSuccess ? MOE_OK : hip_fail(e, "activation pieces");
         });
         if (rc) return rc;
+        if (side) {
+            e = fork_side(L->ctx, s);
+            if (e == hipSuccess) e = launch_mfma_single(true, m, bm, *sh, L->ctx->side);
+            if (e == hipSuccess) e = launch_split_rows(w.hs, t, L->I_s, w.hshi, w.hslo, w.hsex, L->ctx->side);
+            if (e == hipSuccess) e = launch_mfma_single(false, m, bm, *sh, L->ctx->side);
+            if (e != hipSuccess) return hip_fail(e, "shared expert (MFMA kernels)");
+        }
+        const ExpertDev *shs = side ? nullptr : sh;
         rc = stage(L, c.profile, 3, s, [&] {
-            e = launch_mfma(true, m, bm, e0, sh, s);
+            e = launch_mfma(true, m, bm, e0, shs, s);
             return e == hipSuccess ? MOE_OK : hip_fail(e, "MFMA up kernel");
         });
         if (rc) return rc;
         rc = stage(L, c.profile, 6, s, [&] {
             e = launch_split_rows(w.h, t * k, L->I, w.hhi, w.hlo, w.hex, s);
-            if (e == hipSuccess && sh) e = launch_split_rows(w.hs, t, L->I_s, w.hshi, w.hslo, w.hsex, s);
+            if (e == hipSuccess && shs) e = launch_split_rows(w.hs, t, L->I_s, w.hshi, w.hslo, w.hsex, s);
             return e == hipSuccess ? MOE_OK : hip_fail(e, "activation pieces");
         });
         if (rc) return rc;
         rc = stage(L, c.profile, 4, s, [&] {
-            e = launch_mfma(false, m, bm, e0, sh, s);
+            e = launch_mfma(false, m, bm, e0, shs, s);
             return e == hipSuccess ? MOE_OK : hip_fail(e, "MFMA down kernel");
         });
         if (rc) return rc;
+        if (side && (e = join_side(L->ctx, s)) != hipSuccess) return hip_fail(e, "shared expert join");
     } else {
         GemvArgs a{};
         a.experts = L->experts_dev;
@@ -743,6 +799,15 @@ int moe_ctx_create(int device, moe_ctx **out) {
     if (device < 0 || device >= n) return fail(MOE_EINVAL, "device %d does not exist (%d visible)", device, n);
     auto *c = new moe_ctx();
     c->device = device;
+    {
+        DeviceGuard g(device);
+        if (hipStreamCreateWithFlags(&c->side, hipStreamNonBlocking) != hipSuccess ||
+            hipEventCreateWithFlags(&c->ev_fork, hipEventDisableTiming) != hipSuccess ||
+            hipEventCreateWithFlags(&c->ev_join, hipEventDisableTiming) != hipSuccess) {
+            (void)hipGetLastError();
+            c->side = nullptr;  // everything on the caller's stream
+        }
+    }
     *out = c;
     return MOE_OK;
 }
@@ -753,6 +818,9 @@ void moe_ctx_destroy(moe_ctx *ctx) {
     hipDeviceSynchronize();
     for (auto &r : ctx->regions)
         if (r.ptr) hipFree(r.ptr);
+    if (ctx->ev_fork) hipEventDestroy(ctx->ev_fork);
+    if (ctx->ev_join) hipEventDestroy(ctx->ev_join);
+    if (ctx->side) hipStreamDestroy(ctx->side);
     delete ctx;
 }
 
@@ -1118,6 +1186,7 @@ int moe_layer_forward_noalloc(moe_layer *L, const float *x, int32_t t, float *ou
     DeviceGuard g(L->ctx->device);
     CallState c = snapshot(L);
     c.profile = false;  // stage timing creates events; this entry point allocates nothing
+    c.side = false;     // one stream: what a caller capturing or pinning its stream expects
     const size_t need = ws_layout(L, t, c.k, nullptr, nullptr);
     if (need > kScratchBytes)
         return fail(MOE_EINVAL,

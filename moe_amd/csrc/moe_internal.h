@@ -320,6 +320,9 @@ int batch_ksplit(int I, int I_s);
 hipError_t launch_qenc(const float *src, int rows, int cols, uint8_t *dst, hipStream_t s);
 hipError_t launch_batch_up(const BatchArgs &a, const ExpertDev &e0, const ExpertDev *sh, hipStream_t s);
 hipError_t launch_batch_down(const BatchArgs &a, const ExpertDev &e0, const ExpertDev *sh, hipStream_t s);
+// The shared expert's tiles alone (what the two launchers above add for sh).
+hipError_t launch_batch_up_shared(const BatchArgs &a, const ExpertDev &sh, hipStream_t s);
+hipError_t launch_batch_down_shared(const BatchArgs &a, const ExpertDev &sh, hipStream_t s);
 
 struct CombineArgs {
     const float *y, *ys;

@@ -385,6 +385,14 @@ int mfma_split_for(double tokens_per_group) {
 // takes a contiguous range of that order: an expert's weight tile is read
 // from HBM once and met in L2 by the expert's other M tiles, and the
 // expert's activations stay in that XCD's L2 while its N tiles go by.
+//
+// A block holds a CU (its LDS ring fills it), so an XCD's range runs in
+// rounds of xcd_cus blocks, and the last round is partly filled when the
+// range is not a multiple of that.  When it would hold at most half a
+// round of tiles (single-part launches), each of those last tiles is split
+// in two blocks along its tokens: 32-token tiles [0, ceil(MT / 2)) in one
+// and the rest in the other, at the end of the XCD's range, so the last
+// round is full and each of its blocks does about half a tile's products.
 struct TileInfo {
     int g, m0, n, row0, ntile, ksplit;
     bool shared;
@@ -400,28 +408,54 @@ __device__ inline bool tile_of(const MfmaArgs &a, int mode, int gx, TileInfo &ti
     // launch walks only its own (at most gx of them, so valid <= total).
     const int valid = mode == 1 ? mt_sh * gy : (a.ntiles[0] - a.shared_tiles) * gy;
     // XCD x (= lin mod 8) takes t in [x * per, (x + 1) * per) in order.
-    int t = lin;
+    int t = lin, half = -1;
     if ((total & 7) == 0) {
         const int per = (valid + 7) >> 3;
         const int j = lin >> 3;
-        if (j >= per) return false;
-        t = (lin & 7) * per + j;
+        const int tail = gz == 1 && a.xcd_cus > 0 ? per % a.xcd_cus : 0;
+        if (tail > 0 && 2 * tail <= a.xcd_cus && 8 * (per + tail) <= total) {
+            // Blocks head .. head + tail - 1 take the first halves of the
+            // XCD's last `tail` tiles, the next `tail` blocks their second.
+            const int head = per - tail;
+            if (j >= per + tail) return false;
+            if (j < head) {
+                t = (lin & 7) * per + j;
+            } else {
+                half = j - head >= tail;
+                t = (lin & 7) * per + head + (j - head - (half ? tail : 0));
+            }
+        } else {
+            if (j >= per) return false;
+            t = (lin & 7) * per + j;
+        }
     }
     if (t >= valid) return false;
     if (mode == 1) {
         ti.ntile = t / mt_sh;
         ti.g = a.E, ti.m0 = (t % mt_sh) * BM, ti.n = a.T, ti.row0 = 0, ti.shared = true;
-        return true;
+    } else {
+        // Tiles of one group are contiguous: t / gy lies inside t's group.
+        const int ie = t / gy;
+        const int f = a.tiles[4 * ie + 2], mt = a.tiles[4 * ie + 3];
+        const int local = t - f * gy;
+        const int i = f + local % mt;
+        ti.ntile = local / mt;
+        const int g = a.tiles[4 * i];
+        if (g >= a.E) return false;
+        ti.g = g, ti.m0 = a.tiles[4 * i + 1], ti.n = a.counts[g], ti.row0 = a.offsets[g], ti.shared = false;
     }
-    // Tiles of one group are contiguous: t / gy lies inside t's group.
-    const int ie = t / gy;
-    const int f = a.tiles[4 * ie + 2], mt = a.tiles[4 * ie + 3];
-    const int local = t - f * gy;
-    const int i = f + local % mt;
-    ti.ntile = local / mt;
-    const int g = a.tiles[4 * i];
-    if (g >= a.E) return false;
-    ti.g = g, ti.m0 = a.tiles[4 * i + 1], ti.n = a.counts[g], ti.row0 = a.offsets[g], ti.shared = false;
+    if (half >= 0) {
+        // The tile's tokens [m0, end), end - m0 <= BM, in two parts.
+        const int end = min(ti.n, ti.m0 + BM);
+        const int mh = (end - ti.m0 + 63) / 64;  // ceil(MT / 2) 32-token tiles
+        if (half == 0) {
+            ti.n = min(end, ti.m0 + 32 * mh);
+        } else {
+            ti.m0 += 32 * mh;
+            ti.n = end;
+            if (ti.m0 >= end) return false;
+        }
+    }
     return true;
 }
 
@@ -1035,6 +1069,39 @@ __global__ __launch_bounds__(256) void split_rows_kernel(const float *__restrict
     }
 }
 
+// Rows of at most 64 kSplitWave4 float4s: one wavefront per row (four rows
+// per block), the row's largest |v| from lane shuffles; the same pieces and
+// exponent as split_rows_kernel.
+constexpr int kSplitWave4 = 8;
+__global__ __launch_bounds__(256) void split_rows_wave_kernel(const float *__restrict__ src, int rows, int cols,
+                                                              uint16_t *__restrict__ hi, uint16_t *__restrict__ lo,
+                                                              int32_t *__restrict__ ex) {
+    const int lane = threadIdx.x & 63;
+    const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (row >= rows) return;
+    const f32x4 *s4 = reinterpret_cast<const f32x4 *>(src + (size_t)row * cols);
+    u16x4 *h4 = reinterpret_cast<u16x4 *>(hi + (size_t)row * cols);
+    u16x4 *l4 = reinterpret_cast<u16x4 *>(lo + (size_t)row * cols);
+    const int n4 = cols / 4;
+    f32x4 v[kSplitWave4];
+    float m = 0.0f;
+#pragma unroll
+    for (int u = 0; u < kSplitWave4; u++) {
+        const int i = lane + 64 * u;
+        v[u] = i < n4 ? gload(s4 + i) : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+        m = fmaxf(m, fmaxf(fmaxf(fabsf(v[u].x), fabsf(v[u].y)), fmaxf(fabsf(v[u].z), fabsf(v[u].w))));
+    }
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
+    const int e = split_exponent(m);
+    if (lane == 0) ex[row] = e;
+#pragma unroll
+    for (int u = 0; u < kSplitWave4; u++) {
+        const int i = lane + 64 * u;
+        if (i < n4) split_store(v[u], e, h4 + i, l4 + i);
+    }
+}
+
 // ---- weight scales -------------------------------------------------------------
 // Block (g, m, z): slice z of matrix m of expert g; every 32-value block's
 // scale (the first two bytes of the block), as |d| in f16 bits.
@@ -1085,27 +1152,64 @@ int mfma_down_ksplit(int m_tiles, int n_rows, int K, int K_shared) {
     return ks;
 }
 
-hipError_t launch_mfma(bool up, const MfmaArgs &a, int bm, const ExpertDev &e0, const ExpertDev *sh,
+namespace {
+int device_cus() {
+    static int n = 0;
+    if (!n) {
+        int dev = 0, v = 0;
+        if (hipGetDevice(&dev) == hipSuccess &&
+            hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && v > 0)
+            n = v;
+        else
+            n = 256;
+    }
+    return n;
+}
+// CUs per XCD for tile_of's split of the last round, or 0 (no split) when
+// the tiles hold about one 32-token tile or less: its second halves would
+// be empty blocks.
+int split_cus(double tokens_per_tile) { return tokens_per_tile >= 48.0 ? device_cus() / 8 : 0; }
+// Grid for `tiles` tile columns of `rows` weight rows.  With the split of
+// the last round (xcd_cus > 0, one K part): room for it (half a round per
+// XCD) and a multiple of 8 blocks, so the XCD order applies; `order` makes
+// it apply where the plain grid would not be a multiple of 8 (gate/up
+// launches: an expert's activations meet every N tile in one L2).  Down
+// launches keep their plain grid's order: with many token tiles per expert
+// (skewed routing) the XCD order re-reads each tile's activations for
+// every N tile, where the plain order keeps a token tile on one XCD.
+dim3 tile_grid(int tiles, int rows, int cols, int ks, int xcd_cus, bool order) {
+    const int gy = (rows + cols - 1) / cols;
+    if (xcd_cus <= 0 || ks != 1) return dim3(tiles, gy, ks);
+    if (!order && ((long long)tiles * gy) % 8 != 0) return dim3(tiles, gy, ks);
+    const long long need = (long long)tiles * gy + 8LL * (xcd_cus / 2);
+    int gx = (int)((need + gy - 1) / gy);
+    while (((long long)gx * gy) & 7) gx++;
+    return dim3(gx, gy, ks);
+}
+}  // namespace
+
+hipError_t launch_mfma(bool up, const MfmaArgs &a0, int bm, const ExpertDev &e0, const ExpertDev *sh,
                        hipStream_t s) {
+    MfmaArgs a = a0;
+    a.xcd_cus = split_cus(a.E > 0 ? (double)a.T * a.k / a.E : 0.0);
     const MatDev &m = up ? e0.m[0] : e0.m[2];
     const int cols = up ? BW / 2 : BW;
     const int ks = up ? 1 : a.ksplit;
-    dim3 grid(a.max_tiles, (m.rows + cols - 1) / cols, ks);
+    const dim3 grid = tile_grid(a.max_tiles, m.rows, cols, ks, a.xcd_cus, up);
     const int sp = mfma_split_for(a.E > 0 ? (double)a.T * a.k / a.E : 0.0);
     hipError_t err = up ? launch_dt<true>(m.dt, bm, grid, a, 0, ks, sp, s)
                         : launch_dt<false>(m.dt, bm, grid, a, 0, ks, sp, s);
     if (err != hipSuccess || !sh) return err;
-    const MatDev &ms = up ? sh->m[0] : sh->m[2];
-    dim3 gs((a.T + bm - 1) / bm, (ms.rows + cols - 1) / cols, ks);
-    const int ss = mfma_split_for((double)a.T);
-    return up ? launch_dt<true>(ms.dt, bm, gs, a, 1, ks, ss, s) : launch_dt<false>(ms.dt, bm, gs, a, 1, ks, ss, s);
+    return launch_mfma_single(up, a, bm, *sh, s);
 }
 
-hipError_t launch_mfma_single(bool up, const MfmaArgs &a, int bm, const ExpertDev &ex, hipStream_t s) {
+hipError_t launch_mfma_single(bool up, const MfmaArgs &a0, int bm, const ExpertDev &ex, hipStream_t s) {
+    MfmaArgs a = a0;
+    a.xcd_cus = split_cus((double)(a.T < bm ? a.T : bm));
     const MatDev &m = up ? ex.m[0] : ex.m[2];
     const int cols = up ? BW / 2 : BW;
     const int ks = up ? 1 : a.ksplit;
-    dim3 gs((a.T + bm - 1) / bm, (m.rows + cols - 1) / cols, ks);
+    const dim3 gs = tile_grid((a.T + bm - 1) / bm, m.rows, cols, ks, a.xcd_cus, up);
     const int sp = mfma_split_for((double)a.T);
     return up ? launch_dt<true>(m.dt, bm, gs, a, 1, ks, sp, s) : launch_dt<false>(m.dt, bm, gs, a, 1, ks, sp, s);
 }
@@ -1114,7 +1218,9 @@ hipError_t launch_split_rows(const float *src, int rows, int cols, uint16_t *hi,
                              hipStream_t s) {
     if (rows <= 0) return hipSuccess;
     if (cols % 4 != 0) return hipErrorInvalidValue;
-    if (cols / 4 <= 256 * kSplitCached4)
+    if (cols / 4 <= 64 * kSplitWave4)
+        hipLaunchKernelGGL(split_rows_wave_kernel, dim3((rows + 3) / 4), dim3(256), 0, s, src, rows, cols, hi, lo, ex);
+    else if (cols / 4 <= 256 * kSplitCached4)
         hipLaunchKernelGGL(split_rows_kernel<true>, dim3(rows), dim3(256), 0, s, src, cols, hi, lo, ex);
     else
         hipLaunchKernelGGL(split_rows_kernel<false>, dim3(rows), dim3(256), 0, s, src, cols, hi, lo, ex);

@@ -150,7 +150,7 @@ struct DispatchArgs {
     const float *shgate;          // [1] or null
     int I, dk_bound;
 };
-// More than one chunk of tokens (T > 512): three launches (count per
+// More than 512 tokens: three launches (count per
 // chunk, scan, place per chunk) using chunk_scratch [dispatch_chunks(T) * E]
 // ints; otherwise one block.  The permuted rows are the same either way.
 int dispatch_chunks(int T);
@@ -261,6 +261,7 @@ struct MfmaArgs {
     int max_tiles;                // grid width of the routed launch: >= the routed tiles
     int shared_tiles;             // tiles of the shared expert at the end of the tile list (0 if none)
     int ksplit;                   // down projection: K parts (1, 2 or 4), part p written at y + p * ypart
+    int xcd_cus;                  // CUs per XCD (set by the launchers)
 };
 // Token tile of the MFMA kernels for a layer whose matrices have formats
 // dts[0..n): 160, or 128 when a Q8_0 matrix leaves LDS room for fewer rows.

@@ -673,6 +673,11 @@ __global__ __launch_bounds__(256) void gating_kernel(const float *__restrict__ l
 
 constexpr int kDispatchThreads = 512;
 constexpr int kDispatchWaves = kDispatchThreads / 64;
+// Tokens per chunk of the many-token dispatch (count and place kernels run
+// one block of this many threads per chunk): 128 up to kSmallChunkMaxT
+// tokens, kDispatchThreads beyond (the scan walks every chunk per expert).
+constexpr int kChunkTokens = 128;
+constexpr int kSmallChunkMaxT = 2048;
 
 // Exclusive scan of one int per thread across the block; returns the
 // exclusive prefix and writes the block total to *total.
@@ -720,18 +725,24 @@ __device__ int dispatch_tables(const DispatchArgs &a, int c, int *wave_sums, uns
         a.offsets[E + 1] = total + (a.has_shared ? T : 0);
         a.counts[E] = a.has_shared ? T : 0;
     }
+    // The previous call's hit list as a bit set, loaded in parallel.
+    __shared__ unsigned long long prev_bits[kMaxExperts / 64];
+    if (a.prev) {
+        for (int x = tid; x < kMaxExperts / 64; x += kDispatchThreads) prev_bits[x] = 0ull;
+        __syncthreads();
+        const uint32_t np = a.prev[0];
+        for (uint32_t j = tid; j < np; j += kDispatchThreads) {
+            const uint32_t v = a.prev[1 + j];
+            if (v < (uint32_t)E) atomicOr(&prev_bits[v >> 6], 1ull << (v & 63));
+        }
+    }
     int nh;
-    const int hp = block_scan_excl(c > 0 ? 1 : 0, wave_sums, &nh);
+    const int hp = block_scan_excl(c > 0 ? 1 : 0, wave_sums, &nh);  // its barrier publishes prev_bits
     if (c > 0) {
         a.hits[1 + hp] = e;
         if (a.hits_out) a.hits_out[1 + hp] = (uint32_t)e;
         atomicAdd(s_bytes, a.expert_bytes[e]);
-        if (a.prev) {
-            const uint32_t np = a.prev[0];
-            bool in_prev = false;
-            for (uint32_t j = 0; j < np; j++) in_prev |= a.prev[1 + j] == (uint32_t)e;
-            if (in_prev) atomicAdd(s_reused, (unsigned long long)c);
-        }
+        if (a.prev && ((prev_bits[e >> 6] >> (e & 63)) & 1ull)) atomicAdd(s_reused, (unsigned long long)c);
     }
     if (tid == 0) {
         a.hits[0] = nh;
@@ -793,12 +804,14 @@ __device__ int dispatch_tables(const DispatchArgs &a, int c, int *wave_sums, uns
     return o;
 }
 
-// Stable permuted rows of tokens t0 .. t0 + kDispatchThreads - 1 (one per
-// thread): within an expert, lower token first.  run[e] enters as the
-// expert's next free row and leaves advanced past these tokens.  bm and wb
-// are LDS scratch.
+// Stable permuted rows of tokens t0 .. t0 + NT - 1 (one per thread of an
+// NT-thread block): within an expert, lower token first.  run[e] enters as
+// the expert's next free row and leaves advanced past these tokens.  bm and
+// wb are LDS scratch of NT / 64 rows.
+template <int NT>
 __device__ void dispatch_place(const DispatchArgs &a, int t0, int *run, unsigned long long (*bm)[kMaxExperts],
                                int (*wb)[kMaxExperts]) {
+    constexpr int NW = NT / 64;
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
     const int E = a.E, T = a.T, k = a.k;
     const int t = t0 + tid;
@@ -807,9 +820,9 @@ __device__ void dispatch_place(const DispatchArgs &a, int t0, int *run, unsigned
     if (t < T)
         for (int s = 0; s < k; s++) atomicOr(&bm[wv][a.sel[(size_t)t * k + s]], 1ull << lane);
     __syncthreads();
-    for (int x = tid; x < E; x += kDispatchThreads) {
+    for (int x = tid; x < E; x += NT) {
         int r = run[x];
-        for (int w2 = 0; w2 < kDispatchWaves; w2++) {
+        for (int w2 = 0; w2 < NW; w2++) {
             wb[w2][x] = r;
             r += __popcll(bm[w2][x]);
         }
@@ -835,11 +848,12 @@ __device__ void dispatch_place(const DispatchArgs &a, int t0, int *run, unsigned
 }
 
 // Counts of the selections of tokens t0 .. t0 + len - 1 into cnt (LDS,
-// zeroed by the caller).
+// zeroed by the caller), by an NT-thread block.
+template <int NT>
 __device__ inline void dispatch_count(const DispatchArgs &a, int t0, int len, int *cnt) {
     const int E = a.E, k = a.k;
     const int n = len * k;
-    for (int i = threadIdx.x; i < n; i += kDispatchThreads) {
+    for (int i = threadIdx.x; i < n; i += NT) {
         const int e = a.sel[(size_t)t0 * k + i];
         if (e >= 0 && e < E) atomicAdd(&cnt[e], 1);
     }
@@ -857,7 +871,7 @@ __device__ void dispatch_block(const DispatchArgs &a) {
     for (int e = tid; e < E; e += kDispatchThreads) cnt[e] = 0;
     if (tid == 0) s_reused = 0, s_bytes = 0;
     __syncthreads();
-    dispatch_count(a, 0, T, cnt);
+    dispatch_count<kDispatchThreads>(a, 0, T, cnt);
     __syncthreads();
     const int c = tid < E ? cnt[tid] : 0;
     const int o = dispatch_tables(a, c, wave_sums, &s_reused, &s_bytes);
@@ -869,23 +883,24 @@ __device__ void dispatch_block(const DispatchArgs &a) {
         a.stats[2] += s_bytes;
     }
     // Stable positions, kDispatchThreads tokens per pass.
-    for (int t0 = 0; t0 < T; t0 += kDispatchThreads) dispatch_place(a, t0, run, bm, wb);
+    for (int t0 = 0; t0 < T; t0 += kDispatchThreads) dispatch_place<kDispatchThreads>(a, t0, run, bm, wb);
 }
 
 __global__ __launch_bounds__(kDispatchThreads) void dispatch_kernel(DispatchArgs a) { dispatch_block(a); }
 
-// Many tokens: chunks of kDispatchThreads tokens.  Pass 1 counts each
+// Many tokens: chunks of dispatch_chunk_tokens(T) tokens.  Pass 1 counts each
 // chunk's selections per expert; pass 2 (one block) sums them into the
 // tables and gives every (chunk, expert) its first row; pass 3 places each
 // chunk's tokens from there.  The rows are the same as dispatch_block's.
-__global__ __launch_bounds__(kDispatchThreads) void dispatch_count_kernel(DispatchArgs a, int32_t *chunk_cnt) {
+template <int NT>
+__global__ __launch_bounds__(NT) void dispatch_count_kernel(DispatchArgs a, int32_t *chunk_cnt) {
     __shared__ int cnt[kMaxExperts];
-    const int t0 = blockIdx.x * kDispatchThreads;
-    for (int e = threadIdx.x; e < a.E; e += kDispatchThreads) cnt[e] = 0;
+    const int t0 = blockIdx.x * NT;
+    for (int e = threadIdx.x; e < a.E; e += NT) cnt[e] = 0;
     __syncthreads();
-    dispatch_count(a, t0, min(kDispatchThreads, a.T - t0), cnt);
+    dispatch_count<NT>(a, t0, min(NT, a.T - t0), cnt);
     __syncthreads();
-    for (int e = threadIdx.x; e < a.E; e += kDispatchThreads) chunk_cnt[(size_t)blockIdx.x * a.E + e] = cnt[e];
+    for (int e = threadIdx.x; e < a.E; e += NT) chunk_cnt[(size_t)blockIdx.x * a.E + e] = cnt[e];
 }
 
 __global__ __launch_bounds__(kDispatchThreads) void dispatch_scan_kernel(DispatchArgs a, int32_t *chunk_cnt,
@@ -915,13 +930,14 @@ __global__ __launch_bounds__(kDispatchThreads) void dispatch_scan_kernel(Dispatc
     }
 }
 
-__global__ __launch_bounds__(kDispatchThreads) void dispatch_place_kernel(DispatchArgs a, const int32_t *chunk_base) {
+template <int NT>
+__global__ __launch_bounds__(NT) void dispatch_place_kernel(DispatchArgs a, const int32_t *chunk_base) {
     __shared__ int run[kMaxExperts];
-    __shared__ unsigned long long bm[kDispatchWaves][kMaxExperts];
-    __shared__ int wb[kDispatchWaves][kMaxExperts];
-    for (int e = threadIdx.x; e < a.E; e += kDispatchThreads) run[e] = chunk_base[(size_t)blockIdx.x * a.E + e];
+    __shared__ unsigned long long bm[NT / 64][kMaxExperts];
+    __shared__ int wb[NT / 64][kMaxExperts];
+    for (int e = threadIdx.x; e < a.E; e += NT) run[e] = chunk_base[(size_t)blockIdx.x * a.E + e];
     __syncthreads();
-    dispatch_place(a, blockIdx.x * kDispatchThreads, run, bm, wb);
+    dispatch_place<NT>(a, blockIdx.x * NT, run, bm, wb);
 }
 
 // The previous call's hit list (DispatchArgs::prev) as a wavefront holds
@@ -1345,7 +1361,11 @@ hipError_t launch_route_one(const float *W, const float *x, int n_rows, int E, i
     return go(route_one_kernel<8>);
 }
 
-int dispatch_chunks(int T) { return T > kDispatchThreads ? (T + kDispatchThreads - 1) / kDispatchThreads : 0; }
+int dispatch_chunk_tokens(int T) { return T <= kSmallChunkMaxT ? kChunkTokens : kDispatchThreads; }
+int dispatch_chunks(int T) {
+    const int c = dispatch_chunk_tokens(T);
+    return T > kDispatchThreads ? (T + c - 1) / c : 0;
+}
 
 hipError_t launch_dispatch(const DispatchArgs &a, int32_t *chunk_scratch, hipStream_t s) {
     const int nc = dispatch_chunks(a.T);
@@ -1353,9 +1373,17 @@ hipError_t launch_dispatch(const DispatchArgs &a, int32_t *chunk_scratch, hipStr
         hipLaunchKernelGGL(dispatch_kernel, dim3(1), dim3(kDispatchThreads), 0, s, a);
         return hipGetLastError();
     }
-    hipLaunchKernelGGL(dispatch_count_kernel, dim3(nc), dim3(kDispatchThreads), 0, s, a, chunk_scratch);
-    hipLaunchKernelGGL(dispatch_scan_kernel, dim3(1), dim3(kDispatchThreads), 0, s, a, chunk_scratch, nc);
-    hipLaunchKernelGGL(dispatch_place_kernel, dim3(nc), dim3(kDispatchThreads), 0, s, a, chunk_scratch);
+    if (dispatch_chunk_tokens(a.T) == kChunkTokens) {
+        hipLaunchKernelGGL(dispatch_count_kernel<kChunkTokens>, dim3(nc), dim3(kChunkTokens), 0, s, a, chunk_scratch);
+        hipLaunchKernelGGL(dispatch_scan_kernel, dim3(1), dim3(kDispatchThreads), 0, s, a, chunk_scratch, nc);
+        hipLaunchKernelGGL(dispatch_place_kernel<kChunkTokens>, dim3(nc), dim3(kChunkTokens), 0, s, a, chunk_scratch);
+    } else {
+        hipLaunchKernelGGL(dispatch_count_kernel<kDispatchThreads>, dim3(nc), dim3(kDispatchThreads), 0, s, a,
+                           chunk_scratch);
+        hipLaunchKernelGGL(dispatch_scan_kernel, dim3(1), dim3(kDispatchThreads), 0, s, a, chunk_scratch, nc);
+        hipLaunchKernelGGL(dispatch_place_kernel<kDispatchThreads>, dim3(nc), dim3(kDispatchThreads), 0, s, a,
+                           chunk_scratch);
+    }
     return hipGetLastError();
 }
 

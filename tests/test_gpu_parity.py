@@ -452,18 +452,20 @@ def _forward_async(gl, x, stream, workspace=None):
     return out, routes
 
 
-@pytest.mark.parametrize("use_ws", [False, True])
-def test_two_streams_one_layer(ctx, oracle, use_ws):
-    """Two streams run the same layer at once (MFMA-sized and one-token
-    calls interleaved, nothing synchronised in between): each output equals
-    the CPU path's for its own input."""
+@pytest.mark.parametrize("name,use_ws", [("qwen3", False), ("qwen3", True), ("v2_lite", False),
+                                         ("qwen2_moe", True)])
+def test_two_streams_one_layer(ctx, oracle, name, use_ws):
+    """Two streams run the same layer at once (MFMA-sized, few-tokens and
+    one-token calls interleaved, nothing synchronised in between): each
+    output equals the CPU path's for its own input.  With a shared expert
+    (v2_lite, qwen2_moe) both calls also share the context's side stream."""
     import torch
 
     from moe_amd import synth
 
-    host, gl, ol = layer_pair(ctx, oracle, "qwen3")
+    host, gl, ol = layer_pair(ctx, oracle, name)
     streams = [torch.cuda.Stream(), torch.cuda.Stream()]
-    xs = [synth.activations(SEED + 60 + i, t, host.shape.hidden) for i, t in enumerate([300, 1, 200, 1])]
+    xs = [synth.activations(SEED + 60 + i, t, host.shape.hidden) for i, t in enumerate([300, 1, 200, 24, 32, 1])]
     wss = [None, None]
     if use_ws:
         wss = [gl.new_workspace(gl.workspace_size(300)) for _ in streams]
@@ -477,7 +479,7 @@ def test_two_streams_one_layer(ctx, oracle, use_ws):
         r = routes.cpu().numpy()
         assert_routing_equal(dict(sel=r[..., 0], w=r[..., 1].view(np.float32)), sel, w, f"call {i}")
         err = rel_err(out.cpu().numpy(), ref)
-        record("streams", f"qwen3 T={x.shape[0]} stream {i % 2} ws={use_ws}", err)
+        record("streams", f"{name} T={x.shape[0]} stream {i % 2} ws={use_ws}", err)
         assert err <= TOL, f"call {i}: max rel err {err:.2e}"
 
 

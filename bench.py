@@ -225,6 +225,42 @@ def grid_barrier_cost() -> int:
     return 0 if err == 0 else 1
 
 
+def mfma_valu_issue() -> int:
+    """The issue rate of the two-pass MFMA kernels' instruction mix
+    (moe_debug_mfma_valu): one block per CU, one or two waves per SIMD, each
+    wave iterating 8 MFMAs (V_MFMA_F32_32X32X16_F16), 56 or 32 f32 fmas, or
+    both, the fmas after the MFMAs or spread between them.  Reported: ns per
+    iteration of one wave."""
+    import ctypes as C
+
+    import torch
+
+    from moe_amd import _lib as L
+
+    dev = torch.device("cuda:0")
+    cus = torch.cuda.get_device_properties(dev).multi_processor_count
+    out = torch.empty(cus * 512, dtype=torch.float32, device=dev)
+    stream = torch.cuda.current_stream().cuda_stream
+    iters = 20000
+    rows = []
+    for waves in (1, 2):
+        for mf, va, mix in ((8, 0, 0), (0, 56, 0), (8, 56, 0), (8, 56, 1), (8, 32, 1)):
+            def go(n):
+                L.check(L.lib().moe_debug_mfma_valu(mf, va, mix, waves, cus, n, C.c_void_p(out.data_ptr()),
+                                                    C.c_void_p(stream)), "moe_debug_mfma_valu")
+            go(10)
+            t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            t0.record()
+            go(iters)
+            t1.record()
+            torch.cuda.synchronize()
+            ns = t0.elapsed_time(t1) * 1e6 / iters
+            rows.append(dict(waves_per_simd=waves, mfmas=mf, fmas=va, interleaved=bool(mix),
+                             ns_per_iteration=round(ns, 2)))
+    print(json.dumps(dict(mfma_valu_issue=rows, iterations=iters, blocks=cus)), flush=True)
+    return 0
+
+
 def copy_calibration(mib: int) -> int:
     """Five device-to-device copies of `mib` MiB: each reads and writes exactly
     mib * 1024 KiB, so a counter run over them gives the factor between the
@@ -414,6 +450,8 @@ def main() -> int:
                          "(directories, then the output markdown path) and exit")
     ap.add_argument("--grid-barrier", action="store_true",
                     help="time grid-wide barriers in cooperative launches and exit")
+    ap.add_argument("--mfma-valu", action="store_true",
+                    help="time MFMA and VALU issue alone and together (moe_debug_mfma_valu) and exit")
     ap.add_argument("--hbm-ceiling", type=int, default=0, metavar="MIB",
                     help="only time a plain streaming read of MIB MiB (moe_debug_stream_read) and exit")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
@@ -430,6 +468,8 @@ def main() -> int:
         return hbm_ceiling(args.hbm_ceiling)
     if args.grid_barrier:
         return grid_barrier_cost()
+    if args.mfma_valu:
+        return mfma_valu_issue()
     if args.summarize_pmc:
         return summarize_pmc(args.summarize_pmc[0], args.summarize_pmc[1], TRAFFIC_FILE)
     if args.summarize_counters:

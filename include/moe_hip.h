@@ -274,6 +274,17 @@ int moe_debug_mfma_kernel(int32_t choice);
  * No counterpart in the reference. */
 int moe_debug_grid_barrier(int32_t blocks, int32_t barriers, uint32_t *state, void *stream);
 
+/* Diagnostics: the issue rate of the two-pass MFMA kernels' instruction
+ * mix.  `blocks` blocks of 256 * waves_per_simd (1 or 2) threads; each wave
+ * runs `iters` iterations of `mfmas` V_MFMA_F32_32X32X16_F16 (two
+ * independent chains) and `valus` f32 fmas on registers of their own, the
+ * fmas after the MFMAs (interleave 0) or spread between them (1); one
+ * float per thread into out[blocks * 256 * waves_per_simd].  Supported
+ * (mfmas, valus, interleave): (8,0,0), (0,56,0), (8,56,0), (8,56,1),
+ * (8,32,1).  No counterpart in the reference. */
+int moe_debug_mfma_valu(int32_t mfmas, int32_t valus, int32_t interleave, int32_t waves_per_simd, int32_t blocks,
+                        int32_t iters, float *out, void *stream);
+
 /* Diagnostics: read `bytes` (a multiple of 16, 16-byte aligned device
  * memory) once with a grid-stride 16-byte-load kernel of `blocks` blocks
  * (eight loads in flight per thread; nontemporal != 0: nontemporal loads),

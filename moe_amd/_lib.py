@@ -92,6 +92,8 @@ PROTOTYPES = {
     "moe_debug_decode_kernel": (C.c_int, [C.c_int32]),
     "moe_debug_mfma_kernel": (C.c_int, [C.c_int32]),
     "moe_debug_grid_barrier": (C.c_int, [C.c_int32, C.c_int32, C.c_void_p, C.c_void_p]),
+    "moe_debug_mfma_valu": (C.c_int, [C.c_int32, C.c_int32, C.c_int32, C.c_int32, C.c_int32, C.c_int32, C.c_void_p,
+                                      C.c_void_p]),
     "moe_debug_stream_read": (C.c_int, [C.c_void_p, C.c_uint64, C.c_void_p, C.c_int32, C.c_int32, C.c_void_p]),
     "moe_layer_profile": (C.c_int, [C.c_void_p, C.c_int]),
     "moe_container_open": (C.c_int, [C.c_void_p, C.c_uint64, C.POINTER(C.c_void_p)]),

@@ -313,6 +313,47 @@ __global__ __launch_bounds__(512) void grid_barrier_kernel(GridBarrier *b, int b
     }
 }
 
+// Issue-rate probe for the two-pass MFMA kernels' mix: each wave runs
+// `iters` iterations of MF V_MFMA_F32_32X32X16_F16 (two independent
+// accumulator chains) and VA f32 fmas on 32 registers of their own;
+// MIX = 0: the fmas after the iteration's MFMAs (a scheduling barrier
+// between), 1: VA / MF fmas after each MFMA.  One result per thread keeps
+// the work live.
+typedef _Float16 probe_half8 __attribute__((ext_vector_type(8)));
+typedef float probe_floatx16 __attribute__((ext_vector_type(16)));
+template <int MF, int VA, bool MIX>
+__global__ __launch_bounds__(512) void mfma_valu_probe_kernel(float *out, int iters, float s) {
+    const int lane = threadIdx.x & 63;
+    probe_half8 a, b;
+    for (int i = 0; i < 8; i++) a[i] = (_Float16)(lane * 0.001f + i), b[i] = (_Float16)(i * 0.5f);
+    probe_floatx16 c0 = {}, c1 = {};
+    float v[32];
+    for (int i = 0; i < 32; i++) v[i] = (float)(lane + i);
+    constexpr int per = MF > 0 ? VA / MF : 0;
+    for (int it = 0; it < iters; it++) {
+#pragma unroll
+        for (int m = 0; m < MF; m++) {
+            if (m & 1)
+                c1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c1, 0, 0, 0);
+            else
+                c0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c0, 0, 0, 0);
+            if constexpr (MIX) {
+#pragma unroll
+                for (int k = 0; k < per; k++) v[(m * per + k) & 31] = fmaf(v[(m * per + k) & 31], s, 1.0f);
+            }
+        }
+        if constexpr (!MIX || MF == 0) {
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int k = 0; k < VA; k++) v[k & 31] = fmaf(v[k & 31], s, 1.0f);
+        }
+    }
+    float r = 0.0f;
+    for (int i = 0; i < 16; i++) r += c0[i] + c1[i];
+    for (int i = 0; i < 32; i++) r += v[i];
+    out[(size_t)blockIdx.x * blockDim.x + threadIdx.x] = r;
+}
+
 // y = sum over the k parts (p ascending) of parts[p n + i]; residual[i] +=
 // y[i] when given.  The K parts of a split projection.
 __global__ __launch_bounds__(256) void sum_parts_kernel(const float *__restrict__ parts, int k, size_t n,
@@ -450,6 +491,27 @@ int moe_debug_stream_read(const void *src, uint64_t bytes, uint32_t *out, int32_
         hipLaunchKernelGGL(stream_read_kernel<false>, dim3(blocks), dim3(256), 0, (hipStream_t)stream, s4,
                            (size_t)(bytes / 16), out);
     return launch_rc("stream-read kernel");
+}
+
+int moe_debug_mfma_valu(int32_t mfmas, int32_t valus, int32_t interleave, int32_t waves_per_simd, int32_t blocks,
+                        int32_t iters, float *out, void *stream) {
+    if (!out || blocks <= 0 || iters < 0 || (waves_per_simd != 1 && waves_per_simd != 2))
+        return fail(MOE_EINVAL, "moe_debug_mfma_valu: bad argument");
+    const dim3 grid(blocks), block(256 * waves_per_simd);
+    hipStream_t s = (hipStream_t)stream;
+    const int key = mfmas * 10000 + valus * 10 + (interleave ? 1 : 0);
+    switch (key) {
+    case 80000: hipLaunchKernelGGL((mfma_valu_probe_kernel<8, 0, false>), grid, block, 0, s, out, iters, 0.999f); break;
+    case 560: hipLaunchKernelGGL((mfma_valu_probe_kernel<0, 56, false>), grid, block, 0, s, out, iters, 0.999f); break;
+    case 80560: hipLaunchKernelGGL((mfma_valu_probe_kernel<8, 56, false>), grid, block, 0, s, out, iters, 0.999f); break;
+    case 80561: hipLaunchKernelGGL((mfma_valu_probe_kernel<8, 56, true>), grid, block, 0, s, out, iters, 0.999f); break;
+    case 80321: hipLaunchKernelGGL((mfma_valu_probe_kernel<8, 32, true>), grid, block, 0, s, out, iters, 0.999f); break;
+    default:
+        return fail(MOE_EINVAL,
+                    "moe_debug_mfma_valu: (mfmas, valus, interleave) must be (8,0,0), (0,56,0), (8,56,0), (8,56,1) "
+                    "or (8,32,1)");
+    }
+    return launch_rc("MFMA/VALU probe kernel");
 }
 
 int moe_debug_grid_barrier(int32_t blocks, int32_t barriers, uint32_t *state, void *stream) {

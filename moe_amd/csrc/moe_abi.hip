@@ -210,16 +210,18 @@ size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
 
 // Whether the few-tokens kernels beat MFMA tiles.  Their cost is the
 // weight bytes of every tile (an expert's weights are read once per tile of
-// nt tokens).  Measured on MI355X against the three-pass MFMA kernels: with
-// two-token tiles they win while the hit experts average at most 4 tokens
-// (Qwen3 T=64: 0.275 against 0.306 ms; Mixtral T=16 even; V2-Lite T=64 at
-// 6 tokens loses, 0.426 against 0.390), with one-token tiles (rows wider
-// than 4096) at most 1.5 (DeepSeek-V3 T=32: 1.11 against 1.31 ms; T=64 at
-// 2 tokens loses, 2.09 against 1.55).
-bool batch_pays(int t, int k, int E, int nt) {
+// nt tokens).  Measured on MI355X against the two-pass MFMA kernels (ms per
+// layer, few-tokens against MFMA): with two-token tiles and rows of 2048
+// they win while the hit experts average at most 4 tokens (Qwen3 T=64 0.277
+// against 0.293; V2-Lite T=64 at 6 tokens loses, 0.405 against 0.311), with
+// rows of 4096 at most 3 (Mixtral T=8 at 2 tokens 0.275 against 0.391, T=16
+// at 4 loses, 0.457 against 0.412), with one-token tiles (rows wider than
+// 4096) at most 1.5 (DeepSeek-V3 T=32 at 1 token 1.054 against 1.116).
+bool batch_pays(int t, int k, int E, int H, int nt) {
     if (t < 2 || t > kBatchMaxT) return false;
     const long long rows = (long long)t * k, hit = std::min<long long>(E, rows);
-    return nt >= 2 ? rows <= 4 * hit : 2 * rows <= 3 * hit;
+    if (nt < 2) return 2 * rows <= 3 * hit;
+    return rows <= (H >= 4096 ? 3 : 4) * hit;
 }
 
 // Byte layout of a workspace for up to max_t tokens of k experts each.
@@ -473,7 +475,7 @@ int forward_on(moe_layer *L, const CallState &c, Workspace &w, const float *x, i
         path = L->mfma_ok ? kMfma : kGemv;
         if (t == 1 && L->decode_ok)
             path = kDecode;
-        else if (L->batch_ok && batch_pays(t, k, L->E, batch_tile_tokens(L->H, t, k, L->E)))
+        else if (L->batch_ok && batch_pays(t, k, L->E, L->H, batch_tile_tokens(L->H, t, k, L->E)))
             path = kBatch;
     }
     if (path == kBatch && (!L->batch_ok || t > w.batch_t)) path = L->mfma_ok ? kMfma : kGemv;

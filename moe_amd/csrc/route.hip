@@ -194,11 +194,10 @@ __global__ __launch_bounds__(256) void router_tiled_kernel(const float *__restri
 #pragma unroll
         for (int u = 0; u < TPT; u++) acc[i][u] = 0.0f;
     // Each thread moves 2 float4 of W (32 rows x 16 float4) and up to 2 of x
-    // (kTTv tokens) per chunk; the next chunk's loads are issued before this
-    // chunk's FMAs.
+    // (kTTv tokens) per chunk, through two register buffers: the loads of
+    // chunk c + 2 are issued before chunk c's FMAs.
     const bool vec = (H & 3) == 0;
-    float4 pw[2], px[2];
-    auto load_chunk = [&](int k0) {
+    auto load_chunk = [&](int k0, float4(&pw)[2], float4(&px)[2]) {
 #pragma unroll
         for (int u = 0; u < 2; u++) {
             const int q = tid + 256 * u, rr = q >> 4, kk = (q & 15) * 4;
@@ -217,8 +216,12 @@ __global__ __launch_bounds__(256) void router_tiled_kernel(const float *__restri
             pw[u] = w4, px[u] = x4;
         }
     };
-    if (kfull > 0) load_chunk(0);
-    for (int k0 = 0; k0 < kfull; k0 += kKC) {
+    float4 pwa[2], pxa[2], pwb[2], pxb[2];
+    if (kfull > 0) load_chunk(0, pwa, pxa);
+    if (kKC < kfull) load_chunk(kKC, pwb, pxb);
+    // Chunk k0 from register buffer (pw, px), which then takes chunk
+    // k0 + 2 kKC.
+    auto chunk = [&](int k0, float4(&pw)[2], float4(&px)[2]) {
 #pragma unroll
         for (int u = 0; u < 2; u++) {
             const int q = tid + 256 * u, rr = q >> 4, kk = (q & 15) * 4;
@@ -234,7 +237,7 @@ __global__ __launch_bounds__(256) void router_tiled_kernel(const float *__restri
             }
         }
         __syncthreads();
-        if (k0 + kKC < kfull) load_chunk(k0 + kKC);
+        if (k0 + 2 * kKC < kfull) load_chunk(k0 + 2 * kKC, pw, px);
         static_assert(kKC == 64, "four 16-value steps per chunk");
         float4 wq[8], xq[TPT];
 #pragma unroll
@@ -254,6 +257,10 @@ __global__ __launch_bounds__(256) void router_tiled_kernel(const float *__restri
             }
         }
         __syncthreads();
+    };
+    for (int k0 = 0; k0 < kfull; k0 += 2 * kKC) {
+        chunk(k0, pwa, pxa);
+        if (k0 + kKC < kfull) chunk(k0 + kKC, pwb, pxb);
     }
     const bool has8 = (H % 16) >= 8;
     const int tail = kfull + (has8 ? 8 : 0);
@@ -1296,7 +1303,7 @@ hipError_t launch_router(const float *W, const float *x, int T, int n_rows, int 
     // one block per CU ran 4.5x slower than their FMA count); ~1150 cycles
     // per 64-value K chunk at TPT = 8.
     auto tiles_of = [&](int tpt) { return (double)((n_rows + kRT - 1) / kRT) * ((T + 4 * tpt - 1) / (4 * tpt)); };
-    const int tpt = tiles_of(8) >= 3 * 256 ? 8 : tiles_of(4) >= 3 * 256 ? 4 : 2;
+    const int tpt = tiles_of(8) >= 3 * 256 ? 8 : tiles_of(4) >= 3 * 256 ? 4 : tiles_of(2) >= 3 * 256 ? 2 : 1;
     const double tiled = std::ceil(tiles_of(8) / (256.0 * 3)) * (H / 64.0) * 1150.0 / clk_us;
     if (best_rb > 0 && best <= tiled) {
         const int RB = best_rb, TB = best_tb;
@@ -1315,8 +1322,10 @@ hipError_t launch_router(const float *W, const float *x, int T, int n_rows, int 
             hipLaunchKernelGGL(router_tiled_kernel<8>, grid, dim3(256), 0, s, W, x, T, n_rows, E, H, temp, logits);
         else if (tpt == 4)
             hipLaunchKernelGGL(router_tiled_kernel<4>, grid, dim3(256), 0, s, W, x, T, n_rows, E, H, temp, logits);
-        else
+        else if (tpt == 2)
             hipLaunchKernelGGL(router_tiled_kernel<2>, grid, dim3(256), 0, s, W, x, T, n_rows, E, H, temp, logits);
+        else
+            hipLaunchKernelGGL(router_tiled_kernel<1>, grid, dim3(256), 0, s, W, x, T, n_rows, E, H, temp, logits);
     }
     return hipGetLastError();
 }

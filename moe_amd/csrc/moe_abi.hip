@@ -485,7 +485,9 @@ int forward_on(moe_layer *L, const CallState &c, Workspace &w, const float *x, i
         if (t != 1 || !L->decode_ok || !decode_fits(L->I, L->I_s, k, L->has_shared, dt_r, dt_s)) path = kGemv;
     }
     if (path == kMfma && !mfma_fits(t, k, L->H, L->I, L->has_shared ? L->I_s : 0)) path = kGemv;
-    const int bm = path == kMfma ? L->mfma_bm : path == kBatch ? batch_tile_tokens(L->H, t, k, L->E) : 0;
+    const int bm = path == kMfma    ? mfma_call_tile(L->mfma_bm, t, k, L->E)
+                   : path == kBatch ? batch_tile_tokens(L->H, t, k, L->E)
+                                    : 0;
     int rc = route_and_dispatch(L, c, w, x, t, bm, path == kDecode, routes, hits, prev, stats, nullptr, s);
     if (rc) return rc;
 

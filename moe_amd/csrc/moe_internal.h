@@ -266,6 +266,8 @@ struct MfmaArgs {
 // Token tile of the MFMA kernels for a layer whose matrices have formats
 // dts[0..n): 160, or 128 when a Q8_0 matrix leaves LDS room for fewer rows.
 int mfma_tile_m(const int *dts, int n);
+// The token tile of one routed call of t tokens, k experts each, of E.
+int mfma_call_tile(int layer_bm, int t, int k, int E);
 bool mfma_format_ok(int dt);
 bool mfma_fits(size_t t, size_t k, size_t H, size_t I, size_t I_s);
 constexpr int kMaxKSplit = 4;

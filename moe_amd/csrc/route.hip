@@ -917,17 +917,37 @@ __global__ __launch_bounds__(kDispatchThreads) void dispatch_scan_kernel(Dispatc
     const int tid = threadIdx.x;
     if (tid == 0) s_reused = 0, s_bytes = 0;
     __syncthreads();
+    // Chunk counts are read kScanBatch at a time, all in flight together
+    // (one dependent load per chunk cost a memory round trip each); the
+    // first batch stays in registers for the second pass.
+    constexpr int kScanBatch = 16;
+    int cb[kScanBatch];
     int c = 0;
     if (tid < a.E)
-        for (int ch = 0; ch < n_chunks; ch++) c += chunk_cnt[(size_t)ch * a.E + tid];
+        for (int ch0 = 0; ch0 < n_chunks; ch0 += kScanBatch) {
+            int v[kScanBatch];
+#pragma unroll
+            for (int u = 0; u < kScanBatch; u++)
+                v[u] = ch0 + u < n_chunks ? chunk_cnt[(size_t)(ch0 + u) * a.E + tid] : 0;
+#pragma unroll
+            for (int u = 0; u < kScanBatch; u++) {
+                c += v[u];
+                if (ch0 == 0) cb[u] = v[u];
+            }
+        }
     int o = dispatch_tables(a, c, wave_sums, &s_reused, &s_bytes);
     // Each chunk's first row per expert, in place of its count.
     if (tid < a.E)
-        for (int ch = 0; ch < n_chunks; ch++) {
-            int32_t *p = chunk_cnt + (size_t)ch * a.E + tid;
-            const int v = *p;
-            *p = o;
-            o += v;
+        for (int ch0 = 0; ch0 < n_chunks; ch0 += kScanBatch) {
+            int v[kScanBatch];
+#pragma unroll
+            for (int u = 0; u < kScanBatch; u++)
+                v[u] = ch0 == 0 ? cb[u] : ch0 + u < n_chunks ? chunk_cnt[(size_t)(ch0 + u) * a.E + tid] : 0;
+#pragma unroll
+            for (int u = 0; u < kScanBatch; u++) {
+                if (ch0 + u < n_chunks) chunk_cnt[(size_t)(ch0 + u) * a.E + tid] = o;
+                o += v[u];
+            }
         }
     __syncthreads();
     if (tid == 0) {

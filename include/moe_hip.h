@@ -171,7 +171,9 @@ int moe_layer_workspace_size(const moe_layer *layer, int32_t max_t, uint64_t *by
  * none fits), 1 = exact kernels
  * (bit-identical to the CPU path, slow), 2 = GEMV, 3 = MFMA, 4 = one-token
  * kernels at t = 1 and GEMV otherwise, 5 = few-tokens integer-dot kernels
- * (up to 256 tokens).  Every path computes in f32 precision: the GEMV and
+ * (up to 256 tokens), 6 = MFMA grouped GEMM with the weights streamed
+ * through a deep LDS ring (eight waves per tile, same arithmetic as 3;
+ * shapes it does not take fall back as 3 does).  Every path computes in f32 precision: the GEMV and
  * exact kernels in f32 arithmetic, the integer-dot kernels on activations
  * held as three int8 levels (2^-24 of each 32-value block's range), the
  * MFMA kernels on two-piece f16 operands (exact weights, 22-bit

@@ -35,8 +35,14 @@ HIP_FLAGS = [
 ]
 # Sources whose arithmetic must follow the reference operation by operation.
 EXACT = {"route.hip", "combine.hip", "expert_gemv.hip", "expert_decode.hip"}
+# Per-source code-generation options.  expert_stream.hip keeps its MFMA
+# accumulators in VGPRs: with the accumulators in AGPRs the register
+# allocator rotates them between registers every loop iteration (dozens of
+# v_accvgpr moves per step), in VGPRs the loop has none.
+EXTRA = {"expert_stream.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"]}
 
-SOURCES = ["route.hip", "expert_gemv.hip", "expert_decode.hip", "expert_batch.hip", "expert_mfma.hip", "combine.hip",
+SOURCES = ["route.hip", "expert_gemv.hip", "expert_decode.hip", "expert_batch.hip", "expert_mfma.hip",
+           "expert_stream.hip", "combine.hip",
            "model_ops.hip", "moe_abi.hip"]
 HOST_SOURCES = ["host_util.cpp", "container.cpp"]
 
@@ -53,6 +59,7 @@ def _compile_hip(src: str) -> Path:
     flags = list(HIP_FLAGS)
     if src in EXACT:
         flags.append("-ffp-contract=off")
+    flags += EXTRA.get(src, [])
     _run([HIPCC, *flags, "-c", str(CSRC / src), "-o", str(obj)])
     return obj
 

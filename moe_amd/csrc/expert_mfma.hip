@@ -59,12 +59,14 @@
 #include <type_traits>
 
 #include "gmem.h"
+#include "lds_dma.h"
+#include "mfma_tiles.h"
 #include "moe_internal.h"
 
 namespace moe {
 namespace {
 
-typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+using namespace lds;
 typedef float floatx16 __attribute__((ext_vector_type(16)));
 
 constexpr int BW = 256;  // weight rows per tile (up: 128 gate + 128 up rows)
@@ -75,8 +77,6 @@ constexpr int a_stage() {
     return BM * BK * 2;
 }
 
-__device__ inline uint32_t alignb(uint32_t hi, uint32_t lo, uint32_t s) { return __builtin_amdgcn_alignbyte(hi, lo, s); }
-__device__ inline uint32_t perm(uint32_t hi, uint32_t lo, uint32_t sel) { return __builtin_amdgcn_perm(hi, lo, sel); }
 __device__ inline __half2 as_h2(uint32_t v) {
     __half2 h;
     __builtin_memcpy(&h, &v, 4);
@@ -87,7 +87,6 @@ __device__ inline uint32_t h2_bits(__half2 h) {
     __builtin_memcpy(&v, &h, 4);
     return v;
 }
-__device__ inline uint32_t spread4(uint32_t h) { return ((h * 0x00204081u) & 0x01010101u) << 4; }
 
 // Codes b0..b3 (bytes of v, each < 256) minus `off2`, times `d2`: the
 // products as exact f16 pieces, hi (pairs (b0, b1), (b2, b3)) and lo.  0x64
@@ -109,47 +108,6 @@ __device__ inline half8 pack8(const uint32_t (&o)[4]) {
     return r;
 }
 
-// Bytes of one 32-value block, and dwords per weight row per K step (two
-// blocks; a row's step always starts 4-byte aligned since K % 64 == 0).
-template <int DT>
-struct Fmt;
-template <>
-struct Fmt<MOE_DT_Q4_0> {
-    static constexpr int bytes = 18, rd = 9;
-};
-template <>
-struct Fmt<MOE_DT_Q5_0> {
-    static constexpr int bytes = 22, rd = 11;
-};
-template <>
-struct Fmt<MOE_DT_Q8_0> {
-    static constexpr int bytes = 34, rd = 17;
-};
-// Weight DMA.  A row's step (rd dwords) is split into nx4 16-byte lanes
-// (dwords 0 .. 4 nx4 - 1) and nd dword lanes (the rest).  One 32-row region
-// is laid out as
-//   X part  lane q = 32 x + r  (x < nx4) at 16 q: dwords 4x .. 4x+3 of row r
-//   D part  lane q = 32 e + r  (e < nd)  at X + 4 q: dword 4 nx4 + e of row r
-// and filled by nx4 / 2 dwordx4 DMAs plus ceil(nd / 2) dword DMAs (lanes
-// past nd load row 0 into the padding at the region's end).  Dword d of row
-// r of the region therefore sits at loc(d, r) below.
-template <int DT>
-struct BLay {
-    static constexpr int rd = Fmt<DT>::rd;
-    static constexpr int nx4 = rd / 4;             // 2, 2, 4 (even)
-    static constexpr int nd = rd - 4 * nx4;        // 1, 3, 1
-    static constexpr int ix = nx4 / 2;             // dwordx4 DMAs per region
-    static constexpr int id = (nd + 1) / 2;        // dword DMAs per region
-    static constexpr int inst = ix + id;
-    static constexpr int xbytes = 512 * nx4;
-    static constexpr int region = xbytes + 256 * id;  // bytes
-    static constexpr int stage = 8 * region;
-    static_assert(nx4 % 2 == 0, "whole dwordx4 DMAs per region");
-    __device__ static constexpr uint32_t loc(int d, int r) {
-        return d < 4 * nx4 ? (uint32_t)(512 * (d >> 2) + 16 * r + 4 * (d & 3))
-                           : (uint32_t)(xbytes + 128 * (d - 4 * nx4) + 4 * r);
-    }
-};
 // Ring stages per format and token tile: as many as fit in the 160 KiB of
 // LDS beside three per-row arrays.
 template <int DT, int BM>
@@ -166,64 +124,6 @@ static_assert(ring_stages<MOE_DT_Q4_0, 160>() == 3 && ring_stages<MOE_DT_Q5_0, 1
               "three-stage ring for every instantiated format and tile");
 static_assert(ring_stages<MOE_DT_Q8_0, 160>() < 3, "Q8_0 takes 128-token tiles");
 
-// ---- LDS DMA and exact waits ------------------------------------------------
-// global_load_lds writes lane l's 16 (or 4) bytes to LDS address m0 + 16 l
-// (4 l); lanes with EXEC clear write nothing.  Addresses are an SGPR base
-// plus a 32-bit VGPR offset; the base and the LDS address are wave-uniform
-// (readfirstlane states that to the compiler, which may not prove it).
-//
-// The compiler cannot see that the assembly below is a vector memory load
-// that reads an SGPR base and M0, so it would not insert the wait states the
-// hardware needs between a VALU write of an SGPR (v_readfirstlane) and a
-// vector memory instruction reading it (5), or between an M0 write and an
-// LDS DMA (1).  The assembly therefore copies the base with s_mov_b64 (a
-// scalar read, which the hardware interlocks) into SGPRs that nothing but
-// scalar instructions ever wrote, and pads one wait state after the copy.
-__device__ inline const void *uniform_ptr(const void *p) {
-    const uint64_t v = reinterpret_cast<uint64_t>(p);
-    const uint64_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)v);
-    const uint64_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(v >> 32));
-    return reinterpret_cast<const void *>(lo | (hi << 32));
-}
-__device__ inline void dma16(const void *base, uint32_t off, uint32_t lds) {
-    uint64_t sb;
-    asm volatile(
-        "s_mov_b64 %0, %2\n\t"
-        "s_nop 0\n\t"
-        "global_load_lds_dwordx4 %1, %0"
-        : "=&s"(sb)
-        : "v"(off), "s"(uniform_ptr(base)), "{m0}"(__builtin_amdgcn_readfirstlane((int)lds))
-        : "memory");
-}
-__device__ inline void dma4(const void *base, uint32_t off, uint32_t lds) {
-    uint64_t sb;
-    asm volatile(
-        "s_mov_b64 %0, %2\n\t"
-        "s_nop 0\n\t"
-        "global_load_lds_dword %1, %0"
-        : "=&s"(sb)
-        : "v"(off), "s"(uniform_ptr(base)), "{m0}"(__builtin_amdgcn_readfirstlane((int)lds))
-        : "memory");
-}
-template <int N>
-__device__ inline void wait_vm() {
-    static_assert(N >= 0 && N < 64, "vmcnt range");
-    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
-}
-// Wait for all but the newest N of this wave's loads and for its LDS reads,
-// then meet the other waves.
-template <int N>
-__device__ inline void wait_vm_barrier() {
-    static_assert(N >= 0 && N < 64, "vmcnt range");
-    asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"(N) : "memory");
-}
-__device__ inline uint32_t lds_addr(const void *p) {
-    return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void *)p;
-}
-typedef const __attribute__((address_space(3))) uint8_t *lds_p;
-typedef uint32_t u32x4l __attribute__((ext_vector_type(4)));
-__device__ inline uint32_t lds_u32(lds_p p) { return *(const __attribute__((address_space(3))) uint32_t *)p; }
-__device__ inline half8 lds_h8(lds_p p) { return *(const __attribute__((address_space(3))) half8 *)p; }
 
 // ---- weight fragments -----------------------------------------------------
 // Lane (l32, h) of a wave reads row l32 of a 32-row region.  For K group
@@ -379,86 +279,6 @@ int mfma_split_for(double tokens_per_group) {
     return tokens_per_group >= 48.0 ? 2 : 1;
 }
 
-// Tile coordinates.  mode 0: routed tiles from the dispatch list; mode 1: the
-// shared expert over all T tokens.  The grid is walked in the order
-// (expert, N tile, M tile), M fastest, and each XCD (linear block id mod 8)
-// takes a contiguous range of that order: an expert's weight tile is read
-// from HBM once and met in L2 by the expert's other M tiles, and the
-// expert's activations stay in that XCD's L2 while its N tiles go by.
-//
-// A block holds a CU (its LDS ring fills it), so an XCD's range runs in
-// rounds of xcd_cus blocks, and the last round is partly filled when the
-// range is not a multiple of that.  When it would hold at most half a
-// round of tiles (single-part launches), each of those last tiles is split
-// in two blocks along its tokens: 32-token tiles [0, ceil(MT / 2)) in one
-// and the rest in the other, at the end of the XCD's range, so the last
-// round is full and each of its blocks does about half a tile's products.
-struct TileInfo {
-    int g, m0, n, row0, ntile, ksplit;
-    bool shared;
-};
-template <int BM>
-__device__ inline bool tile_of(const MfmaArgs &a, int mode, int gx, TileInfo &ti) {
-    const int gy = gridDim.y, gz = gridDim.z;
-    const int total = gx * gy;
-    const int lin = blockIdx.x + gx * blockIdx.y;
-    ti.ksplit = gz > 1 ? (int)blockIdx.z : 0;
-    const int mt_sh = (a.T + BM - 1) / BM;
-    // Routed tiles come first in the tile list, the shared expert's last; a
-    // launch walks only its own (at most gx of them, so valid <= total).
-    const int valid = mode == 1 ? mt_sh * gy : (a.ntiles[0] - a.shared_tiles) * gy;
-    // XCD x (= lin mod 8) takes t in [x * per, (x + 1) * per) in order.
-    int t = lin, half = -1;
-    if ((total & 7) == 0) {
-        const int per = (valid + 7) >> 3;
-        const int j = lin >> 3;
-        const int tail = gz == 1 && a.xcd_cus > 0 ? per % a.xcd_cus : 0;
-        if (tail > 0 && 2 * tail <= a.xcd_cus && 8 * (per + tail) <= total) {
-            // Blocks head .. head + tail - 1 take the first halves of the
-            // XCD's last `tail` tiles, the next `tail` blocks their second.
-            const int head = per - tail;
-            if (j >= per + tail) return false;
-            if (j < head) {
-                t = (lin & 7) * per + j;
-            } else {
-                half = j - head >= tail;
-                t = (lin & 7) * per + head + (j - head - (half ? tail : 0));
-            }
-        } else {
-            if (j >= per) return false;
-            t = (lin & 7) * per + j;
-        }
-    }
-    if (t >= valid) return false;
-    if (mode == 1) {
-        ti.ntile = t / mt_sh;
-        ti.g = a.E, ti.m0 = (t % mt_sh) * BM, ti.n = a.T, ti.row0 = 0, ti.shared = true;
-    } else {
-        // Tiles of one group are contiguous: t / gy lies inside t's group.
-        const int ie = t / gy;
-        const int f = a.tiles[4 * ie + 2], mt = a.tiles[4 * ie + 3];
-        const int local = t - f * gy;
-        const int i = f + local % mt;
-        ti.ntile = local / mt;
-        const int g = a.tiles[4 * i];
-        if (g >= a.E) return false;
-        ti.g = g, ti.m0 = a.tiles[4 * i + 1], ti.n = a.counts[g], ti.row0 = a.offsets[g], ti.shared = false;
-    }
-    if (half >= 0) {
-        // The tile's tokens [m0, end), end - m0 <= BM, in two parts.
-        const int end = min(ti.n, ti.m0 + BM);
-        const int mh = (end - ti.m0 + 63) / 64;  // ceil(MT / 2) 32-token tiles
-        if (half == 0) {
-            ti.n = min(end, ti.m0 + 32 * mh);
-        } else {
-            ti.m0 += 32 * mh;
-            ti.n = end;
-            if (ti.m0 >= end) return false;
-        }
-    }
-    return true;
-}
-
 // SPLIT = 1: four waves, one per SIMD; wave w owns weight regions 2 w and
 // 2 w + 1 and every token tile.  SPLIT = 2: eight waves, two per SIMD; the
 // pair (w, w + 4) shares regions 2 w and 2 w + 1 (each wave loads one of
@@ -493,7 +313,7 @@ __global__ __launch_bounds__(256 * SPLIT, 1) __attribute__((amdgpu_waves_per_eu(
     int *ex_row = dst_row + BM;
 
     TileInfo ti;
-    if (!tile_of<BM>(a, mode, gx, ti)) return;
+    if (!tile_of<BM, 32>(a, mode, gx, ti)) return;
     const ExpertDev &ex = a.experts[ti.g];
     const MatDev &W0 = UP ? ex.m[0] : ex.m[2];
     const MatDev &W1 = UP ? ex.m[1] : ex.m[2];
@@ -1166,7 +986,6 @@ int mfma_down_ksplit(int m_tiles, int n_rows, int K, int K_shared) {
     return ks;
 }
 
-namespace {
 int device_cus() {
     static int n = 0;
     if (!n) {
@@ -1179,18 +998,14 @@ int device_cus() {
     }
     return n;
 }
-// CUs per XCD for tile_of's split of the last round, or 0 (no split) when
-// the tiles hold about one 32-token tile or less: its second halves would
-// be empty blocks.
-int split_cus(double tokens_per_tile) { return tokens_per_tile >= 48.0 ? device_cus() / 8 : 0; }
-// Grid for `tiles` tile columns of `rows` weight rows.  With the split of
-// the last round (xcd_cus > 0, one K part): room for it (half a round per
-// XCD) and a multiple of 8 blocks, so the XCD order applies; `order` makes
-// it apply where the plain grid would not be a multiple of 8 (gate/up
-// launches: an expert's activations meet every N tile in one L2).  Down
-// launches keep their plain grid's order: with many token tiles per expert
-// (skewed routing) the XCD order re-reads each tile's activations for
-// every N tile, where the plain order keeps a token tile on one XCD.
+int split_cus(double tokens_per_tile, double min_tokens) {
+    return tokens_per_tile >= min_tokens ? device_cus() / 8 : 0;
+}
+// Down launches keep their plain grid's order (order = false): with many
+// token tiles per expert (skewed routing) the XCD order re-reads each tile's
+// activations for every N tile, where the plain order keeps a token tile on
+// one XCD.  Gate/up launches take it (an expert's activations meet every N
+// tile in one L2).
 dim3 tile_grid(int tiles, int rows, int cols, int ks, int xcd_cus, bool order) {
     const int gy = (rows + cols - 1) / cols;
     if (xcd_cus <= 0 || ks != 1) return dim3(tiles, gy, ks);
@@ -1200,12 +1015,11 @@ dim3 tile_grid(int tiles, int rows, int cols, int ks, int xcd_cus, bool order) {
     while (((long long)gx * gy) & 7) gx++;
     return dim3(gx, gy, ks);
 }
-}  // namespace
 
 hipError_t launch_mfma(bool up, const MfmaArgs &a0, int bm, const ExpertDev &e0, const ExpertDev *sh,
                        hipStream_t s) {
     MfmaArgs a = a0;
-    a.xcd_cus = split_cus(a.E > 0 ? (double)a.T * a.k / a.E : 0.0);
+    a.xcd_cus = split_cus(a.E > 0 ? (double)a.T * a.k / a.E : 0.0, 48.0);
     const MatDev &m = up ? e0.m[0] : e0.m[2];
     const int cols = up ? BW / 2 : BW;
     const int ks = up ? 1 : a.ksplit;
@@ -1219,7 +1033,7 @@ hipError_t launch_mfma(bool up, const MfmaArgs &a0, int bm, const ExpertDev &e0,
 
 hipError_t launch_mfma_single(bool up, const MfmaArgs &a0, int bm, const ExpertDev &ex, hipStream_t s) {
     MfmaArgs a = a0;
-    a.xcd_cus = split_cus((double)(a.T < bm ? a.T : bm));
+    a.xcd_cus = split_cus((double)(a.T < bm ? a.T : bm), 48.0);
     const MatDev &m = up ? ex.m[0] : ex.m[2];
     const int cols = up ? BW / 2 : BW;
     const int ks = up ? 1 : a.ksplit;

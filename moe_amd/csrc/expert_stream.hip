@@ -1,0 +1,574 @@
+// expert_stream.hip — grouped SwiGLU expert products on gfx950 matrix cores,
+// weight rows streamed through a deep LDS ring (mode 6 of the layer).
+//
+// A block computes a tile of up to BM = 32 S tokens x 256 weight rows of one
+// expert:
+//   up   : 128 gate rows and the same 128 up rows of the expert, K = H; the
+//          epilogue forms h = silu(G) * U in f32 (src/model.rs:31-33);
+//   down : 256 rows of W_down, K = I (or one K part of it); y in f32.
+// Eight waves, two per SIMD.  The SIMD's pair (w, w + 4) owns 64 weight rows
+// as two 32-row regions (up: gate rows 32 w .. 32 w + 31 and the same up
+// rows, so one lane holds a token's gate and up sums for one row; down:
+// rows 64 w .. 64 w + 63) and every token of the tile as S 32-token
+// subtiles; the two waves take the two 32-value blocks of every 64-value
+// ring step, so each decodes only its own block, and whenever one waits
+// (for LDS, its fmas or the barrier) the other issues MFMAs.  Accumulators,
+// S x 2 tiles of V_MFMA_F32_32X32X16_F16 per wave, stay in registers for the
+// whole K loop; at the end the two halves of each sum meet in LDS.
+//
+// Precision, the same arithmetic as expert_mfma.hip.  The reference
+// multiplies f32 activations by exactly dequantised f32 weights d q
+// (src/quant.rs:482-506).  Here split_rows writes each activation row as
+// hi + lo f16 pieces of v 2^ex (ex per row putting its largest |v| in
+// [2^14, 2^15): 22 significant bits), and the weights enter the MFMAs as
+// their codes q, exact in f16.  The four MFMAs of a 32-value block
+// ((hi + lo) q over two 16-value halves) accumulate the block's sum P from
+// zero, and the block's scale adds it into the tile, acc = fma(d, P, acc),
+// in f32; the epilogue multiplies by 2^-ex, which is exact.  SwiGLU's
+// sigmoid uses the hardware exp and reciprocal (v_exp_f32, v_rcp_f32, about
+// 1 ulp each).
+//
+// Operands reach LDS by DMA (global_load_lds): the activations' 16-byte
+// chunks (the chunk index XORed with bits 1..3 of the token row, so the
+// fragment reads of 16 consecutive rows hit 16 different bank groups) and
+// the raw quantised bytes of each wave's own region.  A ring of NS stages
+// (as many as fit in the LDS, up to 12) keeps NS - 1 K steps in flight with
+// exact vmcnt waits, the DMAs of a step spread over its subtiles so that no
+// wave stalls on a burst of issues; one barrier per step publishes the
+// stage, and the next step's codes are decoded while the current MFMAs run.
+#include <hip/hip_fp16.h>
+#include <hip/hip_runtime.h>
+
+#include <cstdlib>
+#include <type_traits>
+
+#include "gmem.h"
+#include "lds_dma.h"
+#include "mfma_tiles.h"
+#include "moe_internal.h"
+
+namespace moe {
+namespace {
+
+using namespace lds;
+typedef float floatx16 __attribute__((ext_vector_type(16)));
+
+// f(integral_constant<I>) for I = B .. E - 1, in order.
+template <int B, int E, typename F>
+__device__ inline void static_for(F &&f) {
+    if constexpr (B < E) {
+        f(std::integral_constant<int, B>{});
+        static_for<B + 1, E>(f);
+    }
+}
+
+constexpr int SW = 256;  // weight rows per tile
+constexpr int SK = 64;   // K values per ring step (two blocks)
+
+// Bytes of one activation piece of one ring stage: 32 S token rows of SK
+// f16 values.
+template <int S>
+constexpr int s_act() {
+    return 32 * S * SK * 2;
+}
+__device__ inline __half2 as_h2(uint32_t v) {
+    __half2 h;
+    __builtin_memcpy(&h, &v, 4);
+    return h;
+}
+__device__ inline uint32_t h2_bits(__half2 h) {
+    uint32_t v;
+    __builtin_memcpy(&v, &h, 4);
+    return v;
+}
+__device__ inline half8 pack8(const uint32_t (&o)[4]) {
+    half8 r;
+    __builtin_memcpy(&r, o, 16);
+    return r;
+}
+
+// ---- weight slots -------------------------------------------------------------
+// Lane (l32, h) multiplies row l32 of a region.  MFMA m of block kb takes
+// the block's values 16 m + 8 h .. + 7 in natural order; both MFMAs use the
+// same eight code bytes 8 h .. 8 h + 7 (Q4_0 / Q5_0: low nibbles for m = 0,
+// high nibbles for m = 1; Q8_0: bytes 16 m + 8 h ..).  Slot k of block kb is
+// dword base[k] + 2 h hm[k] of the row's ring step (rd dwords: block 0 at
+// byte 0, block 1 right after it):
+//   Q4_0 kb 0: d at bytes 0-1, codes 2..17   -> dw 0, then dw 2h, 2h + 1, 2h + 2 (codes shifted by 2)
+//        kb 1: d 18-19, codes 20..35         -> dw 4 (d in the high half), dw 5 + 2h, 6 + 2h
+//   Q5_0 kb 0: d 0-1, qh 2-5, codes 6..21    -> dw 0, 1 (d, qh shifted by 2), dw 1 + 2h .. 3 + 2h
+//        kb 1: d 22-23, qh 24-27, codes 28.. -> dw 5, 6, dw 7 + 2h, 8 + 2h
+//   Q8_0 kb 0: d 0-1, codes 2..33            -> dw 0, dw 2h .. 2h + 2, dw 4 + 2h .. 6 + 2h
+//        kb 1: d 34-35, codes 36..67         -> dw 8, dw 9 + 2h, 10 + 2h, 13 + 2h, 14 + 2h
+template <int DT, int KB>
+struct Slots;
+template <>
+struct Slots<MOE_DT_Q4_0, 0> {
+    static constexpr int n = 4;
+    static constexpr int base[n] = {0, 0, 1, 2}, hm[n] = {0, 1, 1, 1};
+};
+template <>
+struct Slots<MOE_DT_Q4_0, 1> {
+    static constexpr int n = 3;
+    static constexpr int base[n] = {4, 5, 6}, hm[n] = {0, 1, 1};
+};
+template <>
+struct Slots<MOE_DT_Q5_0, 0> {
+    static constexpr int n = 5;
+    static constexpr int base[n] = {0, 1, 1, 2, 3}, hm[n] = {0, 0, 1, 1, 1};
+};
+template <>
+struct Slots<MOE_DT_Q5_0, 1> {
+    static constexpr int n = 4;
+    static constexpr int base[n] = {5, 6, 7, 8}, hm[n] = {0, 0, 1, 1};
+};
+template <>
+struct Slots<MOE_DT_Q8_0, 0> {
+    static constexpr int n = 7;
+    static constexpr int base[n] = {0, 0, 1, 2, 4, 5, 6}, hm[n] = {0, 1, 1, 1, 1, 1, 1};
+};
+template <>
+struct Slots<MOE_DT_Q8_0, 1> {
+    static constexpr int n = 5;
+    static constexpr int base[n] = {8, 9, 10, 13, 14}, hm[n] = {0, 1, 1, 1, 1};
+};
+constexpr int kMaxSlots = 7;
+
+// Four codes b0..b3 (bytes of c) as f16 pairs (b0, b1), (b2, b3) minus the
+// code offset: 0x64 in each high byte makes the f16 exactly 1024 + b.
+__device__ inline void codes_q(uint32_t c, __half2 off2, uint32_t (&o)[4], int i) {
+    o[i] = h2_bits(__hsub2(as_h2(perm(0x64646464u, c, 0x04010400u)), off2));
+    o[i + 1] = h2_bits(__hsub2(as_h2(perm(0x64646464u, c, 0x04030402u)), off2));
+}
+// Block KB's codes (m = 0, 1) and its scale d, from the slot dwords v.
+template <int DT, int KB>
+__device__ inline void decode2(const uint32_t *v, int h, half8 (&bq)[2], float &d) {
+    const uint32_t s = KB == 0 ? (v[0] & 0xffffu) : (v[0] >> 16);
+    d = __half2float(__ushort_as_half((unsigned short)s));
+    uint32_t o[4];
+    if constexpr (DT == MOE_DT_Q4_0) {
+        const __half2 off2 = __floats2half2_rn(1032.0f, 1032.0f);
+        const uint32_t w0 = KB == 0 ? alignb(v[2], v[1], 2) : v[1];
+        const uint32_t w1 = KB == 0 ? alignb(v[3], v[2], 2) : v[2];
+        codes_q(w0 & 0x0f0f0f0fu, off2, o, 0);
+        codes_q(w1 & 0x0f0f0f0fu, off2, o, 2);
+        bq[0] = pack8(o);
+        codes_q((w0 >> 4) & 0x0f0f0f0fu, off2, o, 0);
+        codes_q((w1 >> 4) & 0x0f0f0f0fu, off2, o, 2);
+        bq[1] = pack8(o);
+    } else if constexpr (DT == MOE_DT_Q5_0) {
+        const __half2 off2 = __floats2half2_rn(1040.0f, 1040.0f);
+        const uint32_t qh = KB == 0 ? alignb(v[1], v[0], 2) : v[1];
+        const uint32_t w0 = KB == 0 ? alignb(v[3], v[2], 2) : v[2];
+        const uint32_t w1 = KB == 0 ? alignb(v[4], v[3], 2) : v[3];
+        const uint32_t hb = qh >> (8 * h);
+        codes_q((w0 & 0x0f0f0f0fu) | spread4(hb & 0xfu), off2, o, 0);
+        codes_q((w1 & 0x0f0f0f0fu) | spread4((hb >> 4) & 0xfu), off2, o, 2);
+        bq[0] = pack8(o);
+        codes_q(((w0 >> 4) & 0x0f0f0f0fu) | spread4((hb >> 16) & 0xfu), off2, o, 0);
+        codes_q(((w1 >> 4) & 0x0f0f0f0fu) | spread4((hb >> 20) & 0xfu), off2, o, 2);
+        bq[1] = pack8(o);
+    } else {
+        const __half2 off2 = __floats2half2_rn(1152.0f, 1152.0f);
+#pragma unroll
+        for (int m = 0; m < 2; m++) {
+            const uint32_t *c = v + 1 + (KB == 0 ? 3 : 2) * m;
+            const uint32_t w0 = KB == 0 ? alignb(c[1], c[0], 2) : c[0];
+            const uint32_t w1 = KB == 0 ? alignb(c[2], c[1], 2) : c[1];
+            codes_q(w0 ^ 0x80808080u, off2, o, 0);
+            codes_q(w1 ^ 0x80808080u, off2, o, 2);
+            bq[m] = pack8(o);
+        }
+    }
+}
+
+// DMAs per wave per step: one 32-row weight region (each wave of a SIMD
+// loads one of the SIMD's two), and S of the 8 S activation DMAs.
+template <int DT, int S>
+constexpr int s2_nd() {
+    return BLay<DT>::inst + S;
+}
+template <int DT, int S>
+constexpr int s2_stages() {
+    constexpr int per = 2 * s_act<S>() + BLay<DT>::stage;
+    constexpr int by_lds = (160 * 1024 - 3 * 32 * S * 4) / per;
+    constexpr int by_vm = 1 + 63 / s2_nd<DT, S>();
+    constexpr int n = by_lds < by_vm ? by_lds : by_vm;
+    return n > 12 ? 12 : n;
+}
+template <int DT, int S>
+constexpr int s2_lds() {
+    return s2_stages<DT, S>() * (2 * s_act<S>() + BLay<DT>::stage) + 3 * 32 * S * 4;
+}
+
+template <int DT, bool UP, int S>
+__global__ __launch_bounds__(512, 1) __attribute__((amdgpu_waves_per_eu(2, 2))) void stream2_kernel(MfmaArgs a,
+                                                                                                      int mode, int gx,
+                                                                                                      int ksplit) {
+    using BL = BLay<DT>;
+    constexpr int BM = 32 * S;
+    constexpr int NS = s2_stages<DT, S>();
+    constexpr int AS = s_act<S>();
+    constexpr int RS = 2 * AS + BL::stage;
+    constexpr int NB = BL::inst;  // weight DMAs per wave per step
+    static_assert(NS >= 3, "at least two steps in flight");
+    static_assert(NS * RS >= 4 * 8192, "the accumulator exchange fits in the ring");
+    extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+    int *src_row = reinterpret_cast<int *>(smem + NS * RS);
+    int *dst_row = src_row + BM;
+    int *ex_row = dst_row + BM;
+
+    TileInfo ti;
+    if (!tile_of<BM, 32>(a, mode, gx, ti)) return;
+    const ExpertDev &ex = a.experts[ti.g];
+    const MatDev &W0 = UP ? ex.m[0] : ex.m[2];
+    const MatDev &W1 = UP ? ex.m[1] : ex.m[2];
+    const int n0 = ti.ntile * (UP ? SW / 2 : SW);
+    if (n0 >= W0.rows) return;
+    const int kspan = W0.cols / ksplit;
+    const int kbeg = ti.ksplit * kspan;
+    const int nsteps = kspan / SK;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int sd = wv & 3, kh = wv >> 2;  // the wave's SIMD (its rows) and block of each step
+    const int l32 = lane & 31, hf = lane >> 5;
+    const int Icol = ti.shared ? a.I_s : a.I;
+    const int valid = min(BM, ti.n - ti.m0);
+    const int mt = (valid + 31) / 32;
+
+    const uint16_t *ahi = UP ? a.xhi : (ti.shared ? a.hshi : a.hhi);
+    const uint16_t *alo = UP ? a.xlo : (ti.shared ? a.hslo : a.hlo);
+    const int32_t *aex = UP ? a.xex : (ti.shared ? a.hsex : a.hex);
+    if (tid < BM) {
+        int s = -1, d = -1, e = 0;
+        if (tid < valid) {
+            d = ti.row0 + ti.m0 + tid;
+            s = UP ? (ti.shared ? ti.m0 + tid : a.perm_tok[d]) : d;
+            e = aex[s];
+        }
+        src_row[tid] = s;
+        dst_row[tid] = d;
+        ex_row[tid] = e;
+    }
+    __syncthreads();
+
+    const uint32_t lds0 = lds_addr(smem);
+    const lds_p sm = (lds_p)smem;
+    const uint32_t arow_bytes = (uint32_t)(UP ? a.H : Icol) * 2;
+
+    // Weight DMA: region kh of the SIMD's two (LDS region 2 sd + kh): up:
+    // gate (kh 0) or up (kh 1) rows n0 + 32 sd ..; down: rows
+    // n0 + 64 sd + 32 kh ..
+    const MatDev &Wd = (UP && kh == 1) ? W1 : W0;
+    const uint8_t *wbase = Wd.ptr;
+    uint32_t woff[BL::inst];
+    {
+        const int row0 = UP ? n0 + 32 * sd : n0 + 64 * sd + 32 * kh;
+        int row = row0 + l32;
+        if (row >= Wd.rows) row = 0;
+#pragma unroll
+        for (int i = 0; i < BL::inst; i++) {
+            const int qq = 64 * (i < BL::ix ? i : i - BL::ix) + lane;
+            uint32_t off;
+            if (i < BL::ix) {
+                off = (uint32_t)row * Wd.stride + 16u * (uint32_t)(qq >> 5);
+            } else {
+                const int e = qq >> 5;
+                off = e < BL::nd ? (uint32_t)row * Wd.stride + (uint32_t)(16 * BL::nx4 + 4 * e) : 0u;
+            }
+            woff[i] = off;
+        }
+    }
+    auto run = [&](auto mt_c, auto kh_c) {
+        constexpr int MT = decltype(mt_c)::value;
+        constexpr int KH = decltype(kh_c)::value;  // == kh
+        // Activations of subtile t, this wave's block KH, MFMA m, piece p.
+        uint32_t aoff[2];
+#pragma unroll
+        for (int m = 0; m < 2; m++)
+            aoff[m] = (uint32_t)l32 * 128u + ((uint32_t)((4 * KH + 2 * m + hf) ^ ((l32 >> 1) & 7)) << 4);
+        constexpr int NA = MT;  // activation DMAs per wave per step (8 MT over 8 waves)
+        constexpr int ND = NB + NA;
+        static_assert((NS - 1) * ND <= 63, "vmcnt range");
+        floatx16 acc[MT][2];
+#pragma unroll
+        for (int t = 0; t < MT; t++)
+#pragma unroll
+            for (int j = 0; j < 2; j++) acc[t][j] = floatx16{};
+        // Activation DMA u of this wave: instruction q = wv + 8 u of the
+        // step's 8 MT (piece q / (4 MT), 8-row group q % (4 MT)).
+        uint32_t aoffg[NA], adst[NA];
+        const uint16_t *asrc[NA];
+#pragma unroll
+        for (int u = 0; u < NA; u++) {
+            const int qd = wv + 8 * u, p = qd / (4 * MT), i = qd % (4 * MT);
+            const int r = 8 * i + (lane >> 3);
+            const int sr = src_row[r < valid ? r : 0];
+            aoffg[u] = (uint32_t)sr * arow_bytes + (uint32_t)kbeg * 2u + (uint32_t)(((lane & 7) ^ ((r >> 1) & 7)) << 4);
+            adst[u] = (uint32_t)p * AS + (uint32_t)i * 1024u;
+            asrc[u] = p == 0 ? ahi : alo;
+        }
+        auto dma = [&](auto d_c, int step, int st) {
+            constexpr int d = decltype(d_c)::value;
+            const int sc = step < nsteps ? step : nsteps - 1;
+            const uint32_t sb = lds0 + (uint32_t)st * RS;
+            if constexpr (d < NB) {
+                const uint8_t *wb = wbase + (size_t)(kbeg / 32 + 2 * sc) * Fmt<DT>::bytes;
+                const uint32_t lr = sb + 2 * AS + (uint32_t)(2 * sd + kh) * BL::region;
+                if constexpr (d < BL::ix)
+                    dma16(wb, woff[d], lr + 1024u * d);
+                else
+                    dma4(wb, woff[d], lr + BL::xbytes + 256u * (d - BL::ix));
+            } else {
+                constexpr int u = d - NB;
+                dma16(reinterpret_cast<const uint8_t *>(asrc[u]) + (size_t)sc * (SK * 2), aoffg[u], sb + adst[u]);
+            }
+        };
+        auto dma_all = [&](int step, int st) {
+            static_for<0, ND>([&](auto d_c) { dma(d_c, step, st); });
+        };
+        // A step's DMAs go out spread over the subtiles after the barrier
+        // that frees their stage: the weights with the step's last subtile,
+        // the activations Q per subtile of the next step (all with the last
+        // subtile when there is only one).  Issued together, the eight
+        // waves' DMAs would queue in the CU's memory pipeline and hold up
+        // the barrier that follows.
+        constexpr int K0 = MT == 1 ? ND : NB;
+        constexpr int Q = MT == 1 ? 0 : (ND - K0 + MT - 2) / (MT - 1);
+        auto dma_part = [&](auto t_c, int step, int st) {
+            constexpr int t = decltype(t_c)::value;
+            static_for<(K0 + t * Q < ND ? K0 + t * Q : ND), (K0 + (t + 1) * Q < ND ? K0 + (t + 1) * Q : ND)>(
+                [&](auto d_c) { dma(d_c, step, st); });
+        };
+
+        // Activation fragments (hi m0, lo m0, hi m1, lo m1) of one subtile;
+        // with room in the registers (tiles of at most 128 tokens) the next
+        // subtile's are read while this one's MFMAs run.
+        constexpr int NAB = S <= 4 ? 2 : 1;
+        half8 Ab[NAB][4];
+        half8 B[2][2];   // [region][m] codes of this wave's block
+        float dsc[2];    // [region] its scale
+        uint32_t raw[1][kMaxSlots];
+        auto read_a = [&](int st, int t, half8(&A)[4]) {
+            const lds_p p = sm + st * RS + 4096 * t;
+#pragma unroll
+            for (int m = 0; m < 2; m++) {
+                A[2 * m] = lds_h8(p + aoff[m]);
+                A[2 * m + 1] = lds_h8(p + AS + aoff[m]);
+            }
+        };
+        auto decode_block = [&](int st) {
+            using SL = Slots<DT, KH>;
+#pragma unroll
+            for (int j = 0; j < 2; j++) {
+                const lds_p rb = sm + st * RS + 2 * AS + (2 * sd + j) * BL::region;
+#pragma unroll
+                for (int k = 0; k < SL::n; k++) raw[0][k] = lds_u32(rb + BL::loc(SL::base[k] + 2 * hf * SL::hm[k], l32));
+                decode2<DT, KH>(raw[0], hf, B[j], dsc[j]);
+            }
+        };
+        // Subtile t: the block's sums P of both regions, four MFMAs each,
+        // then acc += d P.  Region 1's MFMAs go out before region 0's fmas
+        // (which wait for region 0's sums), and region 1's fmas follow the
+        // next subtile's region-0 MFMAs, so each wave's fmas run beside its
+        // own MFMAs as well as its partner's.
+        floatx16 ps[2];
+        auto sums = [&](int j, const half8(&A)[4]) {
+#pragma unroll
+            for (int m = 0; m < 2; m++)
+#pragma unroll
+                for (int p = 0; p < 2; p++)
+                    ps[j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(A[2 * m + p], B[j][m], (m | p) ? ps[j] : floatx16{},
+                                                                   0, 0, 0);
+        };
+        auto scale_add = [&](int t, int j) {
+#pragma unroll
+            for (int v = 0; v < 16; v++) acc[t][j][v] = fmaf(dsc[j], ps[j][v], acc[t][j][v]);
+        };
+        constexpr int WAIT_STEP = (NS - 2) * ND;  // step s + 1 complete
+
+        for (int p = 0; p < NS - 1; p++) dma_all(p, p);
+        wait_vm_barrier<WAIT_STEP>();
+        static_for<0, K0>([&](auto d_c) { dma(d_c, NS - 1, NS - 1); });
+        decode_block(0);
+
+        // Across steps too when the step has an even number of subtiles
+        // (the last one then uses buffer 1); otherwise each step reads its
+        // first subtile's fragments itself.
+        constexpr bool XS = NAB == 2 && MT % 2 == 0;
+        int st = 0;
+        if constexpr (XS) read_a(0, 0, Ab[0]);
+        for (int s = 0; s < nsteps; s++) {
+            const int st1 = st + 1 == NS ? 0 : st + 1;
+            const int st0 = st == 0 ? NS - 1 : st - 1;  // the stage step s + NS - 1's DMAs fill
+            static_for<0, MT>([&](auto t_c) {
+                constexpr int t = decltype(t_c)::value;
+                constexpr int ab = NAB == 2 ? t & 1 : 0;  // this subtile's buffer
+                if constexpr (NAB == 1 || (t == 0 && !XS)) read_a(st, t, Ab[0]);
+                if constexpr (NAB == 2 && t + 1 < MT) read_a(st, t + 1, Ab[ab ^ 1]);
+                if constexpr (t == MT - 1) {
+                    // Every read of this stage is done (the weights were
+                    // decoded at the end of the previous step): wait for
+                    // step s + 1, meet the other waves, start refilling this
+                    // stage.
+                    wait_vm_barrier<WAIT_STEP>();
+                    // (two buffers: the next step's first subtile, from the
+                    // stage the barrier completed)
+                    if constexpr (XS) read_a(st1, 0, Ab[0]);
+                    static_for<0, K0>([&](auto d_c) { dma(d_c, s + NS, st); });
+                } else {
+                    dma_part(t_c, s + NS - 1, st0);
+                }
+                sums(0, Ab[ab]);
+                if constexpr (t > 0) scale_add(t - 1, 1);
+                sums(1, Ab[ab]);
+                scale_add(t, 0);
+                __builtin_amdgcn_sched_barrier(0);
+            });
+            // The last subtile's region-1 fmas, then the next step's codes
+            // and scales (its weights are complete and, after the barrier,
+            // visible from both waves of the SIMD).
+            scale_add(MT - 1, 1);
+            decode_block(st1);
+            st = st1;
+        }
+        wait_vm<0>();
+        __syncthreads();
+
+        // ---- epilogue: the two halves of each subtile meet in LDS (the
+        // ring is free): the wave that does not own subtile t (owner: the
+        // wave of block t & 1) writes its sums, the owner adds them and
+        // stores.  Lane holds C[32 t + 8 (v / 4) + 4 hf + v % 4][row l32 of
+        // region j], scaled by 2^ex_row.
+        float *xb = reinterpret_cast<float *>(smem) + sd * 2048;
+#pragma unroll
+        for (int t = 0; t < MT; t++) {
+            if (KH != (t & 1)) {
+#pragma unroll
+                for (int j = 0; j < 2; j++)
+#pragma unroll
+                    for (int v = 0; v < 16; v++) xb[(j * 16 + v) * 64 + lane] = acc[t][j][v];
+            }
+            __syncthreads();
+            if (KH == (t & 1)) {
+#pragma unroll
+                for (int j = 0; j < 2; j++)
+#pragma unroll
+                    for (int v = 0; v < 16; v++) acc[t][j][v] += xb[(j * 16 + v) * 64 + lane];
+                if (UP) {
+                    float *hout = ti.shared ? a.hs : a.h;
+                    const int col = n0 + 32 * sd + l32;
+                    if (col < W0.rows) {
+#pragma unroll
+                        for (int v = 0; v < 16; v++) {
+                            const int row = 32 * t + 8 * (v / 4) + 4 * hf + (v % 4);
+                            const int d = dst_row[row];
+                            if (d < 0) continue;
+                            const int e = ex_row[row];
+                            const float g = ldexpf(acc[t][0][v], -e), u = ldexpf(acc[t][1][v], -e);
+                            hout[(size_t)d * Icol + col] = g * __builtin_amdgcn_rcpf(1.0f + __expf(-g)) * u;
+                        }
+                    }
+                } else {
+                    float *yout = ti.shared ? a.ys + ti.ksplit * a.yspart : a.y + ti.ksplit * a.ypart;
+#pragma unroll
+                    for (int j = 0; j < 2; j++) {
+                        const int col = n0 + 64 * sd + 32 * j + l32;
+                        if (col >= W0.rows) continue;
+#pragma unroll
+                        for (int v = 0; v < 16; v++) {
+                            const int row = 32 * t + 8 * (v / 4) + 4 * hf + (v % 4);
+                            const int d = dst_row[row];
+                            if (d >= 0) yout[(size_t)d * a.H + col] = ldexpf(acc[t][j][v], -ex_row[row]);
+                        }
+                    }
+                }
+            }
+            __syncthreads();
+        }
+    };
+    auto run_kh = [&](auto mt_c) {
+        if (kh == 0)
+            run(mt_c, std::integral_constant<int, 0>{});
+        else
+            run(mt_c, std::integral_constant<int, 1>{});
+    };
+    switch (mt) {
+    case 1: run_kh(std::integral_constant<int, 1>{}); break;
+    case 2: if constexpr (S >= 2) run_kh(std::integral_constant<int, 2>{}); break;
+    case 3: if constexpr (S >= 3) run_kh(std::integral_constant<int, 3>{}); break;
+    case 4: if constexpr (S >= 4) run_kh(std::integral_constant<int, 4>{}); break;
+    default: if constexpr (S >= 5) run_kh(std::integral_constant<int, 5>{}); break;
+    }
+}
+
+template <int DT, bool UP, int S>
+hipError_t launch_s(dim3 grid, const MfmaArgs &a, int mode, int ksplit, hipStream_t s) {
+    constexpr int lds = s2_lds<DT, S>();
+    static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void *>(&stream2_kernel<DT, UP, S>),
+                                                       hipFuncAttributeMaxDynamicSharedMemorySize, lds);
+    if (attr != hipSuccess) return attr;
+    hipLaunchKernelGGL((stream2_kernel<DT, UP, S>), grid, dim3(512), lds, s, a, mode, (int)grid.x, ksplit);
+    return hipGetLastError();
+}
+
+template <int DT, bool UP>
+hipError_t launch_fmt(int bm, dim3 grid, const MfmaArgs &a, int mode, int ksplit, hipStream_t s) {
+    switch (bm) {
+    case 32: return launch_s<DT, UP, 1>(grid, a, mode, ksplit, s);
+    case 64: return launch_s<DT, UP, 2>(grid, a, mode, ksplit, s);
+    case 128: return launch_s<DT, UP, 4>(grid, a, mode, ksplit, s);
+    case 160:
+        if constexpr (DT != MOE_DT_Q8_0) return launch_s<DT, UP, 5>(grid, a, mode, ksplit, s);
+        return hipErrorInvalidValue;
+    default: return hipErrorInvalidValue;
+    }
+}
+
+template <bool UP>
+hipError_t launch_dt(int dt, int bm, dim3 grid, const MfmaArgs &a, int mode, int ksplit, hipStream_t s) {
+    switch (dt) {
+    case MOE_DT_Q4_0: return launch_fmt<MOE_DT_Q4_0, UP>(bm, grid, a, mode, ksplit, s);
+    case MOE_DT_Q5_0: return launch_fmt<MOE_DT_Q5_0, UP>(bm, grid, a, mode, ksplit, s);
+    case MOE_DT_Q8_0: return launch_fmt<MOE_DT_Q8_0, UP>(bm, grid, a, mode, ksplit, s);
+    default: return hipErrorInvalidValue;
+    }
+}
+
+}  // namespace
+
+// Token tile for a launch whose tiles average `tokens` tokens: the smallest
+// of 32, 64, 128 and 160 that holds them with room for the spread of the
+// experts' counts (160 only where no matrix is Q8_0, whose ring needs the
+// LDS).
+int stream_tile(double tokens, bool q8) {
+    const double need = tokens * 1.15 + 8.0;
+    for (int b : {32, 64, 128})
+        if (b >= need) return b;
+    return q8 ? 128 : 160;
+}
+
+hipError_t launch_stream(bool up, const MfmaArgs &a0, int bm, const ExpertDev &e0, const ExpertDev *sh, hipStream_t s) {
+    MfmaArgs a = a0;
+    const double per = a.E > 0 ? (double)a.T * a.k / a.E : 0.0;
+    a.xcd_cus = split_cus(per < bm ? per : bm, 48.0);
+    const MatDev &m = up ? e0.m[0] : e0.m[2];
+    const int cols = up ? SW / 2 : SW;
+    const int ks = up ? 1 : a.ksplit;
+    const dim3 grid = tile_grid(a.max_tiles, m.rows, cols, ks, a.xcd_cus, up);
+    hipError_t err = up ? launch_dt<true>(m.dt, bm, grid, a, 0, ks, s) : launch_dt<false>(m.dt, bm, grid, a, 0, ks, s);
+    if (err != hipSuccess || !sh) return err;
+    return launch_stream_single(up, a, bm, *sh, s);
+}
+
+hipError_t launch_stream_single(bool up, const MfmaArgs &a0, int bm, const ExpertDev &ex, hipStream_t s) {
+    MfmaArgs a = a0;
+    a.xcd_cus = split_cus((double)(a.T < bm ? a.T : bm), 48.0);
+    const MatDev &m = up ? ex.m[0] : ex.m[2];
+    const int cols = up ? SW / 2 : SW;
+    const int ks = up ? 1 : a.ksplit;
+    const dim3 gs = tile_grid((a.T + bm - 1) / bm, m.rows, cols, ks, a.xcd_cus, up);
+    return up ? launch_dt<true>(m.dt, bm, gs, a, 1, ks, s) : launch_dt<false>(m.dt, bm, gs, a, 1, ks, s);
+}
+
+}  // namespace moe

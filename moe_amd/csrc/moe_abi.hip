@@ -61,7 +61,7 @@ struct Region {
 };
 
 // Forward path for a call.
-enum Path { kExact = 1, kGemv = 2, kMfma = 3, kDecode = 4, kBatch = 5 };
+enum Path { kExact = 1, kGemv = 2, kMfma = 3, kDecode = 4, kBatch = 5, kStream = 6 };
 
 // A normal or subnormal f16 magnitude (bits & 0x7fff, below inf) as float.
 float f16_bits_to_float(unsigned bits) {
@@ -484,10 +484,12 @@ int forward_on(moe_layer *L, const CallState &c, Workspace &w, const float *x, i
         const int dt_s = L->has_shared ? L->experts_host[L->E].m[0].dt : dt_r;
         if (t != 1 || !L->decode_ok || !decode_fits(L->I, L->I_s, k, L->has_shared, dt_r, dt_s)) path = kGemv;
     }
-    if (path == kMfma && !mfma_fits(t, k, L->H, L->I, L->has_shared ? L->I_s : 0)) path = kGemv;
-    const int bm = path == kMfma    ? mfma_call_tile(L->mfma_bm, t, k, L->E)
-                   : path == kBatch ? batch_tile_tokens(L->H, t, k, L->E)
-                                    : 0;
+    if (path == kStream && !L->mfma_ok) path = kGemv;
+    if ((path == kMfma || path == kStream) && !mfma_fits(t, k, L->H, L->I, L->has_shared ? L->I_s : 0)) path = kGemv;
+    const int bm = path == kMfma     ? mfma_call_tile(L->mfma_bm, t, k, L->E)
+                   : path == kStream ? stream_tile((double)t * k / L->E, L->mfma_bm != 160)
+                   : path == kBatch  ? batch_tile_tokens(L->H, t, k, L->E)
+                                     : 0;
     int rc = route_and_dispatch(L, c, w, x, t, bm, path == kDecode, routes, hits, prev, stats, nullptr, s);
     if (rc) return rc;
 
@@ -498,7 +500,7 @@ int forward_on(moe_layer *L, const CallState &c, Workspace &w, const float *x, i
     // (few-tokens and MFMA paths).  Not while stages are being timed on s,
     // nor for the no-allocation entry, nor while s is being captured into a
     // graph (the capture then holds one stream's launches only).
-    bool side = sh && c.side && !c.profile && L->ctx->side && (path == kBatch || path == kMfma);
+    bool side = sh && c.side && !c.profile && L->ctx->side && (path == kBatch || path == kMfma || path == kStream);
     if (side && s) {
         hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
         if (hipStreamIsCapturing(s, &cs) != hipSuccess) {
@@ -608,7 +610,8 @@ int forward_on(moe_layer *L, const CallState &c, Workspace &w, const float *x, i
         });
         if (rc) return rc;
         if (side && (e = join_side(L->ctx, s)) != hipSuccess) return hip_fail(e, "shared expert join");
-    } else if (path == kMfma) {
+    } else if (path == kMfma || path == kStream) {
+        const bool sp = path == kStream;
         MfmaArgs m{};
         m.experts = L->experts_dev;
         m.tiles = w.tiles;
@@ -653,14 +656,17 @@ int forward_on(moe_layer *L, const CallState &c, Workspace &w, const float *x, i
         if (rc) return rc;
         if (side) {
             e = fork_side(L->ctx, s);
-            if (e == hipSuccess) e = launch_mfma_single(true, m, bm, *sh, L->ctx->side);
+            const int bs = sp ? stream_tile((double)t, L->mfma_bm != 160) : bm;
+            if (e == hipSuccess)
+                e = sp ? launch_stream_single(true, m, bs, *sh, L->ctx->side) : launch_mfma_single(true, m, bm, *sh, L->ctx->side);
             if (e == hipSuccess) e = launch_split_rows(w.hs, t, L->I_s, w.hshi, w.hslo, w.hsex, L->ctx->side);
-            if (e == hipSuccess) e = launch_mfma_single(false, m, bm, *sh, L->ctx->side);
+            if (e == hipSuccess)
+                e = sp ? launch_stream_single(false, m, bs, *sh, L->ctx->side) : launch_mfma_single(false, m, bm, *sh, L->ctx->side);
             if (e != hipSuccess) return hip_fail(e, "shared expert (MFMA kernels)");
         }
         const ExpertDev *shs = side ? nullptr : sh;
         rc = stage(L, c.profile, 3, s, [&] {
-            e = launch_mfma(true, m, bm, e0, shs, s);
+            e = sp ? launch_stream(true, m, bm, e0, shs, s) : launch_mfma(true, m, bm, e0, shs, s);
             return e == hipSuccess ? MOE_OK : hip_fail(e, "MFMA up kernel");
         });
         if (rc) return rc;
@@ -671,7 +677,7 @@ int forward_on(moe_layer *L, const CallState &c, Workspace &w, const float *x, i
         });
         if (rc) return rc;
         rc = stage(L, c.profile, 4, s, [&] {
-            e = launch_mfma(false, m, bm, e0, shs, s);
+            e = sp ? launch_stream(false, m, bm, e0, shs, s) : launch_mfma(false, m, bm, e0, shs, s);
             return e == hipSuccess ? MOE_OK : hip_fail(e, "MFMA down kernel");
         });
         if (rc) return rc;
@@ -1101,11 +1107,12 @@ int moe_layer_set_routing(moe_layer *L, const moe_routing *r) {
 }
 
 int moe_layer_set_mode(moe_layer *L, int mode) {
-    if (!L || mode < 0 || mode > kBatch) return fail(MOE_EINVAL, "moe_layer_set_mode: mode %d", mode);
+    if (!L || mode < 0 || mode > kStream) return fail(MOE_EINVAL, "moe_layer_set_mode: mode %d", mode);
     if (mode == kBatch && !L->batch_ok) return fail(MOE_EUNSUP, "this layer's shapes do not fit the few-tokens kernels");
     if (mode == kDecode && !L->decode_ok) return fail(MOE_EUNSUP, "this layer's shapes do not fit the one-token kernels");
     if (mode == kGemv && !L->fast_ok) return fail(MOE_EUNSUP, "this layer's shapes do not fit the GEMV kernels");
-    if (mode == kMfma && !L->mfma_ok) return fail(MOE_EUNSUP, "this layer's shapes do not fit the MFMA kernels");
+    if ((mode == kMfma || mode == kStream) && !L->mfma_ok)
+        return fail(MOE_EUNSUP, "this layer's shapes do not fit the MFMA kernels");
     std::lock_guard<std::mutex> g(L->mu);
     L->mode = mode;
     return MOE_OK;

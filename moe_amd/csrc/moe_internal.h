@@ -286,6 +286,13 @@ hipError_t launch_mfma_single(bool up, const MfmaArgs &a, int bm, const ExpertDe
 // [2^14, 2^15) (0 for an all-zero or non-finite row).  cols % 4 == 0.
 hipError_t launch_split_rows(const float *src, int rows, int cols, uint16_t *hi, uint16_t *lo, int32_t *ex,
                              hipStream_t s);
+
+// The streaming expert kernels (expert_stream.hip): one wave per SIMD, tiles
+// of bm = 32, 64, 128 or 160 tokens (160 only for Q4_0 / Q5_0) x 256 weight
+// rows, the same arguments and activation pieces as launch_mfma.
+int stream_tile(double tokens, bool q8);
+hipError_t launch_stream(bool up, const MfmaArgs &a, int bm, const ExpertDev &e0, const ExpertDev *sh, hipStream_t s);
+hipError_t launch_stream_single(bool up, const MfmaArgs &a, int bm, const ExpertDev &ex, hipStream_t s);
 // Largest |d| (f16 bits) of every block scale of matrix m of expert g into
 // out[3 g + m], for the n experts of the table (F32 matrices give 0).
 hipError_t launch_scale_max(const ExpertDev *experts, int n, unsigned *out, hipStream_t s);

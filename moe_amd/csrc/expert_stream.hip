@@ -279,15 +279,31 @@ __global__ __launch_bounds__(512, 1) __attribute__((amdgpu_waves_per_eu(2, 2))) 
             woff[i] = off;
         }
     }
-    auto run = [&](auto mt_c, auto kh_c) {
+    // PK: one subtile of at most 16 tokens, whose hi and lo pieces share
+    // the MFMAs' 32 rows (rows 16 + r carry token r's lo piece): half the
+    // MFMAs and activation DMAs, and the two halves of each sum meet in the
+    // fmas (C rows r and 16 + r sit in one lane, at v and v + 8).
+    auto run = [&](auto mt_c, auto kh_c, auto pk_c) {
         constexpr int MT = decltype(mt_c)::value;
         constexpr int KH = decltype(kh_c)::value;  // == kh
-        // Activations of subtile t, this wave's block KH, MFMA m, piece p.
+        constexpr bool PK = decltype(pk_c)::value;
+        static_assert(!PK || MT == 1, "packed pieces: one 16-token subtile");
+        constexpr int NP = PK ? 1 : 2;  // MFMAs per 16-value half (one per piece unless packed)
+        constexpr int NM = 4 * NP;      // MFMAs per subtile (two regions, two halves)
+        constexpr int NV = PK ? 8 : 16; // accumulator values that hold tokens
+        // Activations of subtile t, this wave's block KH, MFMA m (piece p at
+        // + p AS; packed: lane l32 reads piece l32 / 16, row l32 % 16).
         uint32_t aoff[2];
 #pragma unroll
-        for (int m = 0; m < 2; m++)
-            aoff[m] = (uint32_t)l32 * 128u + ((uint32_t)((4 * KH + 2 * m + hf) ^ ((l32 >> 1) & 7)) << 4);
-        constexpr int NA = MT;  // activation DMAs per wave per step (8 MT over 8 waves)
+        for (int m = 0; m < 2; m++) {
+            const int r = PK ? (l32 & 15) : l32;
+            aoff[m] = (uint32_t)r * 128u + ((uint32_t)((4 * KH + 2 * m + hf) ^ ((r >> 1) & 7)) << 4) +
+                      (PK ? (uint32_t)(l32 >> 4) * AS : 0u);
+        }
+        // Activation DMAs per wave per step: the step's 8 MT (packed: 4, from
+        // the waves of block 0).
+        constexpr int NA = PK ? (KH == 0 ? 1 : 0) : MT;
+        constexpr int GA = PK ? 2 : 4 * MT;  // 8-row groups per piece
         constexpr int ND = NB + NA;
         static_assert((NS - 1) * ND <= 63, "vmcnt range");
         floatx16 acc[MT][2];
@@ -296,12 +312,13 @@ __global__ __launch_bounds__(512, 1) __attribute__((amdgpu_waves_per_eu(2, 2))) 
 #pragma unroll
             for (int j = 0; j < 2; j++) acc[t][j] = floatx16{};
         // Activation DMA u of this wave: instruction q = wv + 8 u of the
-        // step's 8 MT (piece q / (4 MT), 8-row group q % (4 MT)).
-        uint32_t aoffg[NA], adst[NA];
-        const uint16_t *asrc[NA];
+        // step's 2 GA (piece q / GA, 8-row group q % GA).
+        constexpr int NA1 = NA > 0 ? NA : 1;
+        uint32_t aoffg[NA1], adst[NA1];
+        const uint16_t *asrc[NA1];
 #pragma unroll
         for (int u = 0; u < NA; u++) {
-            const int qd = wv + 8 * u, p = qd / (4 * MT), i = qd % (4 * MT);
+            const int qd = wv + 8 * u, p = qd / GA, i = qd % GA;
             const int r = 8 * i + (lane >> 3);
             const int sr = src_row[r < valid ? r : 0];
             aoffg[u] = (uint32_t)sr * arow_bytes + (uint32_t)kbeg * 2u + (uint32_t)(((lane & 7) ^ ((r >> 1) & 7)) << 4);
@@ -328,11 +345,12 @@ __global__ __launch_bounds__(512, 1) __attribute__((amdgpu_waves_per_eu(2, 2))) 
             static_for<0, ND>([&](auto d_c) { dma(d_c, step, st); });
         };
         // A step's DMAs go out spread over the subtiles after the barrier
-        // that frees their stage: the weights with the step's last subtile,
-        // the activations Q per subtile of the next step (all with the last
-        // subtile when there is only one).  Issued together, the eight
-        // waves' DMAs would queue in the CU's memory pipeline and hold up
-        // the barrier that follows.
+        // that frees their stage: the weights between the MFMAs of the
+        // step's last subtile, the activations Q per subtile of the next
+        // step (all between the last subtile's MFMAs when there is only
+        // one).  Issued together, the eight waves' DMAs would queue in the
+        // CU's memory pipeline and stall their waves and the barrier that
+        // follows; between MFMAs a wave's stall leaves the matrix pipe busy.
         constexpr int K0 = MT == 1 ? ND : NB;
         constexpr int Q = MT == 1 ? 0 : (ND - K0 + MT - 2) / (MT - 1);
         auto dma_part = [&](auto t_c, int step, int st) {
@@ -353,8 +371,12 @@ __global__ __launch_bounds__(512, 1) __attribute__((amdgpu_waves_per_eu(2, 2))) 
             const lds_p p = sm + st * RS + 4096 * t;
 #pragma unroll
             for (int m = 0; m < 2; m++) {
-                A[2 * m] = lds_h8(p + aoff[m]);
-                A[2 * m + 1] = lds_h8(p + AS + aoff[m]);
+                if constexpr (PK) {
+                    A[m] = lds_h8(p + aoff[m]);
+                } else {
+                    A[2 * m] = lds_h8(p + aoff[m]);
+                    A[2 * m + 1] = lds_h8(p + AS + aoff[m]);
+                }
             }
         };
         auto decode_block = [&](int st) {
@@ -367,23 +389,27 @@ __global__ __launch_bounds__(512, 1) __attribute__((amdgpu_waves_per_eu(2, 2))) 
                 decode2<DT, KH>(raw[0], hf, B[j], dsc[j]);
             }
         };
-        // Subtile t: the block's sums P of both regions, four MFMAs each,
-        // then acc += d P.  Region 1's MFMAs go out before region 0's fmas
-        // (which wait for region 0's sums), and region 1's fmas follow the
-        // next subtile's region-0 MFMAs, so each wave's fmas run beside its
-        // own MFMAs as well as its partner's.
+        // Subtile t: the block's sums P of both regions, NM / 2 MFMAs
+        // each, then acc += d P.  Region 1's MFMAs go out before region 0's
+        // fmas (which wait for region 0's sums), and region 1's fmas follow
+        // the next subtile's region-0 MFMAs, so each wave's fmas run beside
+        // its own MFMAs as well as its partner's.  MFMA i: region i / (2 NP),
+        // half m, piece p.
         floatx16 ps[2];
-        auto sums = [&](int j, const half8(&A)[4]) {
-#pragma unroll
-            for (int m = 0; m < 2; m++)
-#pragma unroll
-                for (int p = 0; p < 2; p++)
-                    ps[j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(A[2 * m + p], B[j][m], (m | p) ? ps[j] : floatx16{},
-                                                                   0, 0, 0);
+        auto mm = [&](auto i_c, const half8(&A)[4]) {
+            constexpr int i = decltype(i_c)::value;
+            constexpr int j = i / (2 * NP), m = (i % (2 * NP)) / NP, p = i % NP;
+            ps[j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(A[NP * m + p], B[j][m],
+                                                           (i % (2 * NP)) ? ps[j] : floatx16{}, 0, 0, 0);
         };
         auto scale_add = [&](int t, int j) {
+            if constexpr (PK) {
 #pragma unroll
-            for (int v = 0; v < 16; v++) acc[t][j][v] = fmaf(dsc[j], ps[j][v], acc[t][j][v]);
+                for (int v = 0; v < 8; v++) acc[t][j][v] = fmaf(dsc[j], ps[j][v] + ps[j][v + 8], acc[t][j][v]);
+            } else {
+#pragma unroll
+                for (int v = 0; v < 16; v++) acc[t][j][v] = fmaf(dsc[j], ps[j][v], acc[t][j][v]);
+            }
         };
         constexpr int WAIT_STEP = (NS - 2) * ND;  // step s + 1 complete
 
@@ -415,13 +441,24 @@ __global__ __launch_bounds__(512, 1) __attribute__((amdgpu_waves_per_eu(2, 2))) 
                     // (two buffers: the next step's first subtile, from the
                     // stage the barrier completed)
                     if constexpr (XS) read_a(st1, 0, Ab[0]);
-                    static_for<0, K0>([&](auto d_c) { dma(d_c, s + NS, st); });
                 } else {
                     dma_part(t_c, s + NS - 1, st0);
                 }
-                sums(0, Ab[ab]);
-                if constexpr (t > 0) scale_add(t - 1, 1);
-                sums(1, Ab[ab]);
+                static_for<0, NM>([&](auto i_c) {
+                    constexpr int i = decltype(i_c)::value;
+                    mm(i_c, Ab[ab]);
+                    if constexpr (i == NM / 2 - 1 && t > 0) scale_add(t - 1, 1);
+                    if constexpr (t == MT - 1) {
+                        // The refill of this stage: DMAs d0 .. d1 - 1 of
+                        // the K0 after MFMA i.
+                        constexpr int d0 = (K0 * i + NM - 1) / NM, d1 = (K0 * (i + 1) + NM - 1) / NM;
+                        if constexpr (d1 > d0) {
+                            __builtin_amdgcn_sched_barrier(0);
+                            static_for<d0, d1>([&](auto d_c) { dma(d_c, s + NS, st); });
+                            __builtin_amdgcn_sched_barrier(0);
+                        }
+                    }
+                });
                 scale_add(t, 0);
                 __builtin_amdgcn_sched_barrier(0);
             });
@@ -447,20 +484,20 @@ __global__ __launch_bounds__(512, 1) __attribute__((amdgpu_waves_per_eu(2, 2))) 
 #pragma unroll
                 for (int j = 0; j < 2; j++)
 #pragma unroll
-                    for (int v = 0; v < 16; v++) xb[(j * 16 + v) * 64 + lane] = acc[t][j][v];
+                    for (int v = 0; v < NV; v++) xb[(j * 16 + v) * 64 + lane] = acc[t][j][v];
             }
             __syncthreads();
             if (KH == (t & 1)) {
 #pragma unroll
                 for (int j = 0; j < 2; j++)
 #pragma unroll
-                    for (int v = 0; v < 16; v++) acc[t][j][v] += xb[(j * 16 + v) * 64 + lane];
+                    for (int v = 0; v < NV; v++) acc[t][j][v] += xb[(j * 16 + v) * 64 + lane];
                 if (UP) {
                     float *hout = ti.shared ? a.hs : a.h;
                     const int col = n0 + 32 * sd + l32;
                     if (col < W0.rows) {
 #pragma unroll
-                        for (int v = 0; v < 16; v++) {
+                        for (int v = 0; v < NV; v++) {
                             const int row = 32 * t + 8 * (v / 4) + 4 * hf + (v % 4);
                             const int d = dst_row[row];
                             if (d < 0) continue;
@@ -476,7 +513,7 @@ __global__ __launch_bounds__(512, 1) __attribute__((amdgpu_waves_per_eu(2, 2))) 
                         const int col = n0 + 64 * sd + 32 * j + l32;
                         if (col >= W0.rows) continue;
 #pragma unroll
-                        for (int v = 0; v < 16; v++) {
+                        for (int v = 0; v < NV; v++) {
                             const int row = 32 * t + 8 * (v / 4) + 4 * hf + (v % 4);
                             const int d = dst_row[row];
                             if (d >= 0) yout[(size_t)d * a.H + col] = ldexpf(acc[t][j][v], -ex_row[row]);
@@ -487,18 +524,24 @@ __global__ __launch_bounds__(512, 1) __attribute__((amdgpu_waves_per_eu(2, 2))) 
             __syncthreads();
         }
     };
-    auto run_kh = [&](auto mt_c) {
+    auto run_kh = [&](auto mt_c, auto pk_c) {
         if (kh == 0)
-            run(mt_c, std::integral_constant<int, 0>{});
+            run(mt_c, std::integral_constant<int, 0>{}, pk_c);
         else
-            run(mt_c, std::integral_constant<int, 1>{});
+            run(mt_c, std::integral_constant<int, 1>{}, pk_c);
     };
+    using NoPk = std::false_type;
     switch (mt) {
-    case 1: run_kh(std::integral_constant<int, 1>{}); break;
-    case 2: if constexpr (S >= 2) run_kh(std::integral_constant<int, 2>{}); break;
-    case 3: if constexpr (S >= 3) run_kh(std::integral_constant<int, 3>{}); break;
-    case 4: if constexpr (S >= 4) run_kh(std::integral_constant<int, 4>{}); break;
-    default: if constexpr (S >= 5) run_kh(std::integral_constant<int, 5>{}); break;
+    case 1:
+        if (valid <= 16)
+            run_kh(std::integral_constant<int, 1>{}, std::true_type{});
+        else
+            run_kh(std::integral_constant<int, 1>{}, NoPk{});
+        break;
+    case 2: if constexpr (S >= 2) run_kh(std::integral_constant<int, 2>{}, NoPk{}); break;
+    case 3: if constexpr (S >= 3) run_kh(std::integral_constant<int, 3>{}, NoPk{}); break;
+    case 4: if constexpr (S >= 4) run_kh(std::integral_constant<int, 4>{}, NoPk{}); break;
+    default: if constexpr (S >= 5) run_kh(std::integral_constant<int, 5>{}, NoPk{}); break;
     }
 }
 

@@ -128,9 +128,9 @@ LAYER_CASES = [
     # rows one, so the shared down projection runs as a launch of its own)
     ("qwen2_moe", 1, None), ("qwen2_moe", 1, 4), ("qwen2_moe", 1, 2), ("qwen2_moe", 6, 5), ("qwen2_moe", 64, None),
     ("qwen2_moe", 64, 3), ("qwen2_moe", 17, 2), ("qwen2_moe", 512, None),
-    # streaming kernels forced (6): 16-, 32-, 64-, 128- and 160-token tiles, every format, shared experts
+    # streaming kernels forced (6): 16-, 32-, 64-, 128- and 160-token tiles (at most 16 tokens: packed pieces), every format, shared experts
     # (Q5_0 beside Q4_0, two shared experts, the sigmoid-gated one), tile boundaries, K split down
-    ("tiny_mixtral", 16, 6), ("tiny_mixtral", 257, 6), ("mixtral", 2, 6), ("mixtral", 32, 6), ("mixtral", 100, 6),
+    ("tiny_mixtral", 16, 6), ("tiny_mixtral", 257, 6), ("mixtral", 2, 6), ("mixtral", 32, 6), ("mixtral", 64, 6), ("mixtral", 100, 6),
     ("mixtral", 512, 6), ("qwen3", 128, 6), ("qwen3", 300, 6), ("qwen3", 2048, 6), ("v2_lite", 32, 6),
     ("v2_lite", 256, 6), ("deepseek_v3", 64, 6), ("qwen2_moe", 64, 6), ("qwen2_moe", 512, 6),
 ]

@@ -152,13 +152,21 @@ int moe_layer_set_routing(moe_layer *layer, const moe_routing *routing);
  * and a call with more tokens (or, after set_routing, more experts per token)
  * than reserved fails with MOE_EINVAL.  Without one, moe_layer_forward
  * allocates a stream's workspace on its first call there and grows it when
- * t grows; an outgrown workspace is released by moe_layer_destroy (queued
- * work may still use it), so growth never waits for the device.  No
+ * t grows, by at least half its size each time; an outgrown workspace is
+ * freed once the work queued before the growth has finished (queried at a
+ * later growth, never waited for) or by moe_layer_destroy.  No
  * counterpart in the reference, which allocates scratch per call
  * (src/model.rs:900-935). */
 int moe_layer_reserve_stream(moe_layer *layer, int32_t max_t, void *stream);
 /* moe_layer_reserve_stream on the null stream. */
 int moe_layer_reserve(moe_layer *layer, int32_t max_t);
+
+/* Drop the workspace moe_layer_forward keeps for `stream`: it is freed once
+ * the work already queued on the stream has finished (checked without
+ * waiting at later workspace growth, and at moe_layer_destroy).  Call it
+ * before destroying a stream whose handle value a new stream may reuse:
+ * workspaces are keyed by the handle.  No counterpart in the reference. */
+int moe_layer_release_stream(moe_layer *layer, void *stream);
 
 /* Bytes of a caller-owned workspace for moe_layer_forward_ws over up to
  * `max_t` tokens at the layer's current top_k. */

@@ -71,6 +71,7 @@ PROTOTYPES = {
     "moe_layer_set_routing": (C.c_int, [C.c_void_p, C.POINTER(RoutingC)]),
     "moe_layer_reserve": (C.c_int, [C.c_void_p, C.c_int32]),
     "moe_layer_reserve_stream": (C.c_int, [C.c_void_p, C.c_int32, C.c_void_p]),
+    "moe_layer_release_stream": (C.c_int, [C.c_void_p, C.c_void_p]),
     "moe_layer_workspace_size": (C.c_int, [C.c_void_p, C.c_int32, C.POINTER(C.c_uint64)]),
     "moe_layer_forward_noalloc": (C.c_int, [C.c_void_p, C.c_void_p, C.c_int32, C.c_void_p, C.c_void_p,
                                             C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p]),

@@ -75,6 +75,13 @@ struct StreamWs {
     Workspace w;
     int k;
 };
+// An outgrown or released workspace: free once `done` (recorded on its
+// stream when it was retired, after the last work that used it) has
+// completed; without an event, at moe_layer_destroy.
+struct Retired {
+    void *base;
+    hipEvent_t done;
+};
 
 }  // namespace
 
@@ -117,7 +124,7 @@ struct moe_layer {
     uint32_t disabled[kMaxExperts / 32] = {};
     bool any_disabled = false;
     std::vector<StreamWs> ws;            // one workspace per stream used with moe_layer_forward
-    std::vector<void *> retired;         // outgrown workspaces, freed by moe_layer_destroy
+    std::vector<Retired> retired;        // outgrown or released workspaces, not yet freed
     int reserved_t = 0, reserved_k = 0;  // after moe_layer_reserve: calls beyond these fail
     // stage timing
     bool profile = false;
@@ -269,7 +276,7 @@ size_t ws_layout(const moe_layer *L, int max_t, int k, Workspace *w, char *base)
         {(void **)&x.tiles, 4 * max_tiles * 4},
         {(void **)&x.dtasks, (size_t)(k + 1) * sizeof(DecodeTask)},
         {(void **)&x.ntiles, 4},
-        {(void **)&x.chunks, (size_t)dispatch_chunks((int)T) * E * 4},
+        {(void **)&x.chunks, (size_t)dispatch_chunks_upto((int)T) * E * 4},
         {(void **)&x.xhi, Tm * H * 2},
         {(void **)&x.xlo, Tm * H * 2},
         {(void **)&x.xex, Tm * 4},
@@ -296,14 +303,42 @@ size_t ws_layout(const moe_layer *L, int max_t, int k, Workspace *w, char *base)
     }
     x.base = base;
     x.bytes = off;
+    x.chunks_cap = (size_t)dispatch_chunks_upto((int)T) * E;
     return off;
+}
+
+// Retire a stream's workspace: queued work may still use it, so it is
+// freed only once an event recorded on the stream now has completed.
+void retire_ws(moe_layer *L, void *base, hipStream_t s) {
+    hipEvent_t ev = nullptr;
+    if (hipEventCreateWithFlags(&ev, hipEventDisableTiming) == hipSuccess && hipEventRecord(ev, s) != hipSuccess) {
+        hipEventDestroy(ev);
+        ev = nullptr;
+    }
+    L->retired.push_back({base, ev});
+}
+// Free the retired workspaces whose event has completed (a query, no wait).
+void reap_ws(moe_layer *L) {
+    for (size_t i = 0; i < L->retired.size();) {
+        Retired &r = L->retired[i];
+        if (r.done && hipEventQuery(r.done) == hipSuccess) {
+            hipFree(r.base);
+            hipEventDestroy(r.done);
+            r = L->retired.back();
+            L->retired.pop_back();
+        } else {
+            i++;
+        }
+    }
 }
 
 // The workspace of `stream` for t tokens (moe_layer_forward): the layer
 // keeps one per stream, so calls on different streams never share scratch.
-// Grows (without waiting for the device: an outgrown workspace is kept
-// until moe_layer_destroy, since queued work may still use it) unless the
-// layer was reserved, in which case a larger call fails.
+// Grows without waiting for the device, geometrically (at least 1.5 times
+// the old size, in 64-token steps) so that rising token counts allocate
+// O(final size) in total; the outgrown workspace is retired and freed at a
+// later growth once the work queued on it has finished.  A reserved layer
+// does not grow: a larger call fails.
 int stream_ws(moe_layer *L, hipStream_t s, int t, int k, Workspace &out) {
     std::lock_guard<std::mutex> g(L->mu);
     StreamWs *cur = nullptr;
@@ -317,7 +352,14 @@ int stream_ws(moe_layer *L, hipStream_t s, int t, int k, Workspace &out) {
         return fail(MOE_EINVAL, "%d tokens of %d experts exceed the reservation of %d tokens of %d experts", t, k,
                     L->reserved_t, L->reserved_k);
     int max_t = std::max(t, L->reserved_t), kk = std::max(k, L->reserved_k);
-    if (cur) max_t = std::max(max_t, cur->w.max_t), kk = std::max(kk, cur->k);
+    if (cur) {
+        if (t > cur->w.max_t && L->reserved_t == 0) {
+            const long long grown = (long long)cur->w.max_t + cur->w.max_t / 2;
+            max_t = (int)std::max<long long>(t, std::min<long long>((grown + 63) / 64 * 64, 1 << 24));
+        }
+        max_t = std::max(max_t, cur->w.max_t), kk = std::max(kk, cur->k);
+    }
+    reap_ws(L);
     const size_t bytes = ws_layout(L, max_t, kk, nullptr, nullptr);
     void *base = nullptr;
     hipError_t e = hipMalloc(&base, bytes);
@@ -329,7 +371,7 @@ int stream_ws(moe_layer *L, hipStream_t s, int t, int k, Workspace &out) {
     Workspace w;
     ws_layout(L, max_t, kk, &w, static_cast<char *>(base));
     if (cur) {
-        L->retired.push_back(cur->w.base);
+        retire_ws(L, cur->w.base, s);
         cur->w = w;
         cur->k = kk;
     } else {
@@ -440,7 +482,7 @@ int route_and_dispatch(moe_layer *L, const CallState &c, Workspace &w, const flo
     if (rc) return rc;
     if ((rc = copy_logits())) return rc;
     return stage(L, c.profile, 2, s, [&] {
-        e = launch_dispatch(a, w.chunks, s);
+        e = launch_dispatch(a, w.chunks, w.chunks_cap, s);
         return e == hipSuccess ? MOE_OK : hip_fail(e, "dispatch kernel");
     });
 }
@@ -1063,7 +1105,10 @@ void moe_layer_destroy(moe_layer *L) {
     DeviceGuard g(L->ctx->device);
     hipDeviceSynchronize();
     for (StreamWs &e : L->ws) hipFree(e.w.base);
-    for (void *p : L->retired) hipFree(p);
+    for (Retired &r : L->retired) {
+        hipFree(r.base);
+        if (r.done) hipEventDestroy(r.done);
+    }
     hipFree(L->router);
     hipFree(L->experts_dev);
     hipFree(L->expert_bytes);
@@ -1133,6 +1178,20 @@ int moe_layer_reserve_stream(moe_layer *L, int32_t max_t, void *stream) {
 }
 
 int moe_layer_reserve(moe_layer *L, int32_t max_t) { return moe_layer_reserve_stream(L, max_t, nullptr); }
+
+int moe_layer_release_stream(moe_layer *L, void *stream) {
+    if (!L) return fail(MOE_EINVAL, "moe_layer_release_stream: bad argument");
+    DeviceGuard g(L->ctx->device);
+    std::lock_guard<std::mutex> lk(L->mu);
+    for (size_t i = 0; i < L->ws.size(); i++) {
+        if (L->ws[i].stream != (hipStream_t)stream) continue;
+        retire_ws(L, L->ws[i].w.base, L->ws[i].stream);
+        L->ws.erase(L->ws.begin() + i);
+        break;
+    }
+    reap_ws(L);
+    return MOE_OK;
+}
 
 int moe_layer_k(const moe_layer *L) {
     if (!L) return 0;
@@ -1225,9 +1284,12 @@ int moe_layer_forward_noalloc(moe_layer *L, const float *x, int32_t t, float *ou
 struct moe_linear {
     moe_ctx *ctx = nullptr;
     ExpertDev host{};
-    ExpertDev *dev = nullptr;
+    ExpertDev *dev = nullptr;  // owned: freed with the object, also on a failed create
     bool fast = false, mfma = false;
     int bm = 160;
+    ~moe_linear() {
+        if (dev) hipFree(dev);
+    }
 };
 
 namespace {
@@ -1334,7 +1396,6 @@ void moe_linear_destroy(moe_linear *l) {
     if (!l) return;
     DeviceGuard g(l->ctx->device);
     hipDeviceSynchronize();
-    hipFree(l->dev);
     delete l;
 }
 

@@ -93,7 +93,8 @@ struct Workspace {
     DecodeTask *dtasks = nullptr; // [k + 1] one-token task table
     unsigned *route_count = nullptr;  // [1] finished router blocks (one-token route), zero between calls
     int32_t *ntiles = nullptr;    // [1]
-    int32_t *chunks = nullptr;    // [dispatch_chunks(T) * E] per-chunk expert counts / first rows
+    int32_t *chunks = nullptr;    // [dispatch_chunks_upto(max_t) * E] per-chunk expert counts / first rows
+    size_t chunks_cap = 0;        // entries of chunks
     uint16_t *xhi = nullptr, *xlo = nullptr;  // [T, H] f16 pieces of x (MFMA path)
     int32_t *xex = nullptr;       // [T] their row exponents
     uint16_t *hhi = nullptr, *hlo = nullptr;  // [T*k, I] f16 pieces of h (MFMA path)
@@ -152,9 +153,14 @@ struct DispatchArgs {
 };
 // More than 512 tokens: three launches (count per
 // chunk, scan, place per chunk) using chunk_scratch [dispatch_chunks(T) * E]
-// ints; otherwise one block.  The permuted rows are the same either way.
+// ints (chunk_cap of them: a launch that would need more fails with
+// hipErrorInvalidValue); otherwise one block.  The permuted rows are the
+// same either way.
 int dispatch_chunks(int T);
-hipError_t launch_dispatch(const DispatchArgs &a, int32_t *chunk_scratch, hipStream_t s);
+// The most chunks any T' <= T takes: dispatch_chunks is not monotonic (its
+// chunks widen past 4096 tokens), so scratch for up to T tokens holds this.
+int dispatch_chunks_upto(int T);
+hipError_t launch_dispatch(const DispatchArgs &a, int32_t *chunk_scratch, size_t chunk_cap, hipStream_t s);
 
 // Router + gating + dispatch of one token in one launch (n_rows blocks; the
 // last to finish gates and dispatches).  `counter` is zero between calls.

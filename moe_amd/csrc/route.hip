@@ -1399,8 +1399,13 @@ int dispatch_chunks(int T) {
     return T > kDispatchThreads ? (T + c - 1) / c : 0;
 }
 
-hipError_t launch_dispatch(const DispatchArgs &a, int32_t *chunk_scratch, hipStream_t s) {
+int dispatch_chunks_upto(int T) {
+    return std::max(dispatch_chunks(std::min(T, kSmallChunkMaxT)), dispatch_chunks(T));
+}
+
+hipError_t launch_dispatch(const DispatchArgs &a, int32_t *chunk_scratch, size_t chunk_cap, hipStream_t s) {
     const int nc = dispatch_chunks(a.T);
+    if (nc > 0 && chunk_scratch && (size_t)nc * a.E > chunk_cap) return hipErrorInvalidValue;
     if (nc == 0 || !chunk_scratch) {
         hipLaunchKernelGGL(dispatch_kernel, dim3(1), dim3(kDispatchThreads), 0, s, a);
         return hipGetLastError();

@@ -319,6 +319,13 @@ class MoeLayer:
         L.check(L.lib().moe_layer_reserve_stream(self.handle, max_t, C.c_void_p(_stream_ptr(stream))),
                 "moe_layer_reserve_stream")
 
+    def release_stream(self, stream=None) -> None:
+        """Drop the workspace kept for `stream` (freed once its queued work
+        has finished); call before destroying a stream whose handle may be
+        reused."""
+        L.check(L.lib().moe_layer_release_stream(self.handle, C.c_void_p(_stream_ptr(stream))),
+                "moe_layer_release_stream")
+
     def workspace_size(self, max_t: int) -> int:
         """Bytes of a caller-owned workspace for up to max_t tokens."""
         n = C.c_uint64()

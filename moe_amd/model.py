@@ -39,6 +39,10 @@ except ImportError:  # pragma: no cover - torch is part of the image
 
 ROPE_NONE, ROPE_LINEAR, ROPE_DYNAMIC, ROPE_YARN, ROPE_LLAMA3 = 0, 1, 2, 3, 4
 
+# Positions one attention row can cover: moe_attention holds the row's f32
+# scores in 64 KiB of LDS.
+ATTN_MAX_POSITIONS = 16384
+
 
 @dataclass
 class Rope:
@@ -447,6 +451,15 @@ class Model:
         return s.kv_heads * s.head_dim, s.kv_heads * s.head_dim
 
     def new_state(self, n_seq: int, ctx: int) -> State:
+        # moe_attention keeps one row's scores in LDS: at most
+        # ATTN_MAX_POSITIONS positions per row (the window, where a layer
+        # has one).  A longer context is refused here, before any step.
+        layers = self.spec.layers
+        wins = list(self.spec.windows) + [None] * max(0, layers - len(self.spec.windows))
+        widest = max(min(w, ctx) if w else ctx for w in wins) if wins else ctx
+        if widest > ATTN_MAX_POSITIONS:
+            raise ValueError(f"a context of {ctx} positions: attention here covers at most "
+                             f"{ATTN_MAX_POSITIONS} positions per row")
         return State(self, n_seq, ctx)
 
     def _workspace(self, t: int):

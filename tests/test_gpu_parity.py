@@ -549,3 +549,59 @@ def test_reservation_is_a_limit(ctx, oracle):
             gl.feed_forward(xd[:8], out[:8], workspace=ws)
     finally:
         gl.close()
+
+
+def test_reservation_above_chunk_widening(ctx, oracle):
+    """A stream reserved for more than 4096 tokens, where the dispatch's
+    chunks widen (fewer chunks at 8192 tokens than at 4096), then called with
+    4096 and 3000 tokens: its chunk scratch holds the most chunks of any
+    smaller call (the dispatch refuses a launch that would not fit), and the
+    outputs equal the CPU path's."""
+    from moe_amd import synth
+
+    host = synth.build_host_layer(synth.SHAPES["tiny_mixtral"], SEED)
+    gl = synth.make_layer(ctx, host)
+    ol = oracle.from_host_layer(host)
+    try:
+        gl.reserve(8192)
+        for t in (4096, 3000, 8192):
+            x = synth.activations(SEED + 80 + t, t, host.shape.hidden)
+            g = run_gpu(gl, x)
+            ref, sel, w, _, _ = ol.forward(x)
+            assert_routing_equal(g, sel, w, f"T={t}")
+            err = rel_err(g["out"], ref)
+            record("reserve", f"tiny_mixtral reserved 8192, T={t}", err)
+            assert err <= TOL, f"T={t}: max rel err {err:.2e}"
+    finally:
+        gl.close()
+
+
+def test_workspace_growth_and_release(ctx, oracle):
+    """Token counts rising one at a time on one stream (each growth retires
+    the outgrown workspace), then the stream's workspace released and the
+    stream used again: every output equals the CPU path's."""
+    import torch
+
+    from moe_amd import synth
+
+    host = synth.build_host_layer(synth.SHAPES["tiny_mixtral"], SEED)
+    gl = synth.make_layer(ctx, host)
+    ol = oracle.from_host_layer(host)
+    try:
+        s = torch.cuda.Stream()
+        xs = [synth.activations(SEED + 90 + t, t, host.shape.hidden) for t in list(range(1, 40)) + [300, 1, 700]]
+        outs = []
+        for i, x in enumerate(xs):
+            outs.append(_forward_async(gl, x, s))
+            if i == len(xs) - 3:
+                gl.release_stream(s)
+        torch.cuda.synchronize()
+        gl.release_stream(s)
+        gl.release_stream(s)  # nothing left to release
+        for x, (out, routes) in zip(xs, outs):
+            ref, sel, w, _, _ = ol.forward(x)
+            r = routes.cpu().numpy()
+            assert_routing_equal(dict(sel=r[..., 0], w=r[..., 1].view(np.float32)), sel, w, f"T={x.shape[0]}")
+            assert rel_err(out.cpu().numpy(), ref) <= TOL, f"T={x.shape[0]}"
+    finally:
+        gl.close()

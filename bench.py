@@ -49,18 +49,22 @@ def expert_flops(shape, t: int, k: int, up_only: bool = False) -> float:
 
 
 def time_steps(layers, x, out, steps: int, warmup: int):
+    """(median, mean) milliseconds per step: every step between an event
+    pair of its own on the stream the forward runs on (torch's current
+    stream), the K steps queued back to back between two synchronisations."""
     import torch
 
     for i in range(warmup):
         layers[i % len(layers)].feed_forward(x, out)
     torch.cuda.synchronize()
-    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    start.record()
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
     for i in range(steps):
+        ev[i][0].record()
         layers[i % len(layers)].feed_forward(x, out)
-    end.record()
+        ev[i][1].record()
     torch.cuda.synchronize()
-    return start.elapsed_time(end) / steps
+    ms = [a.elapsed_time(b) for a, b in ev]
+    return float(np.median(ms)), float(np.mean(ms))
 
 
 def stage_times(layers, x, out, steps: int):
@@ -160,7 +164,7 @@ def hbm_ceiling(mib: int) -> int:
             out = torch.empty(blocks, dtype=torch.int32, device=dev)
 
             def go():
-                L.check(L.lib().moe_debug_stream_read(C.c_void_p(buf.data_ptr()), buf.numel(),
+                L.diag_check(L.diag().moe_debug_stream_read(C.c_void_p(buf.data_ptr()), buf.numel(),
                                                       C.c_void_p(out.data_ptr()), blocks, nt, C.c_void_p(stream)),
                         "moe_debug_stream_read")
 
@@ -214,7 +218,7 @@ def grid_barrier_cost() -> int:
     for blocks in (cus, 2 * cus):
         us = {}
         for nb in (1, 101):
-            us[nb] = per_launch(lambda: L.check(L.lib().moe_debug_grid_barrier(
+            us[nb] = per_launch(lambda: L.diag_check(L.diag().moe_debug_grid_barrier(
                 blocks, nb, C.c_void_p(state.data_ptr()), C.c_void_p(stream)), "moe_debug_grid_barrier"))
         rows.append(dict(blocks=blocks, us_1_barrier=round(us[1], 2), us_101_barriers=round(us[101], 2),
                          us_per_barrier=round((us[101] - us[1]) / 100, 2)))
@@ -246,7 +250,7 @@ def mfma_valu_issue() -> int:
     for waves in (1, 2):
         for mf, va, mix in ((8, 0, 0), (0, 56, 0), (8, 56, 0), (8, 56, 1), (8, 32, 1)):
             def go(n):
-                L.check(L.lib().moe_debug_mfma_valu(mf, va, mix, waves, cus, n, C.c_void_p(out.data_ptr()),
+                L.diag_check(L.diag().moe_debug_mfma_valu(mf, va, mix, waves, cus, n, C.c_void_p(out.data_ptr()),
                                                     C.c_void_p(stream)), "moe_debug_mfma_valu")
             go(10)
             t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
@@ -504,11 +508,11 @@ def main() -> int:
             layer.reserve(t)
         x = torch.from_numpy(synth.activations(1, t, shape.hidden)).to(dev)
         out = torch.empty_like(x)
-        ms = time_steps(layers, x, out, args.steps, args.warmup)
+        ms, ms_mean = time_steps(layers, x, out, args.steps, args.warmup)
         stages = stage_times(layers, x, out, args.steps)
         up_bytes, down_bytes = selected_bytes(layers[0], host, x)
-        results[t] = dict(ms=ms, stages=stages, up_bytes=up_bytes, down_bytes=down_bytes)
-        log(f"T={t}: {ms:.4f} ms/step, {t / ms * 1e3:.0f} tok/s; stages " +
+        results[t] = dict(ms=ms, ms_mean=ms_mean, stages=stages, up_bytes=up_bytes, down_bytes=down_bytes)
+        log(f"T={t}: {ms:.4f} ms/step (median; mean {ms_mean:.4f}), {t / ms * 1e3:.0f} tok/s; stages " +
             ", ".join(f"{k_}={v * 1e3:.1f}us" for k_, v in stages.items()))
 
     # Prefill (headline): MFMA-bound gate/up kernel.
@@ -536,7 +540,7 @@ def main() -> int:
             2 * args.batch_tokens * shape.hidden * 4
         b_gbs = b_bytes / (tb["ms"] * 1e-3) / 1e9
         batch = {"tokens": args.batch_tokens, "value": round(args.batch_tokens / (tb["ms"] * 1e-3), 1),
-                 "unit": "tokens/s", "ms_per_step": round(tb["ms"], 5),
+                 "unit": "tokens/s", "ms_per_step": round(tb["ms"], 5), "ms_mean": round(tb["ms_mean"], 5),
                  "roofline": {"bound": "hbm", "kernel": "whole layer (hit experts' bytes once)",
                               "achieved": round(b_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                               "frac": round(b_gbs / HBM_PEAK_GBS, 4)},
@@ -563,10 +567,12 @@ def main() -> int:
         "steps": args.steps,
         "warmup": args.warmup,
         "ms_per_step": round(tp["ms"], 5),
+        "ms_mean": round(tp["ms_mean"], 5),
+        "timing": f"median of {args.steps} steps, each between its own HIP event pair",
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "f32",
+        "dtype": "f32-class (22-bit activation pieces)",
         "arithmetic": "f32 precision on the matrix cores: activations as two f16 pieces (22 significant bits, "
                       "per-row power-of-two scale), weights as their exact integer codes in f16; per 32-value "
                       "block (hi + lo) * q accumulated in f32 by V_MFMA_F32_32X32X16_F16 (2 MFMAs per product), "
@@ -584,7 +590,8 @@ def main() -> int:
                      "layer_frac": round(layer_tflops / MFMA_F16_PEAK_TFLOPS, 4)},
         "cpu_baseline": cpu,
         "decode": {"tokens": args.decode_tokens, "value": round(args.decode_tokens / (td["ms"] * 1e-3), 1),
-                   "unit": "tokens/s", "ms_per_step": round(td["ms"], 5), "dtype": "f32",
+                   "unit": "tokens/s", "ms_per_step": round(td["ms"], 5), "ms_mean": round(td["ms_mean"], 5),
+                   "dtype": "f32-class (three int8 activation levels)",
                    "arithmetic": "f32 precision: quantised codes dotted exactly (v_dot4_i32_i8) with activations "
                                  "held as three int8 levels (error 2^-24 of each 32-value block's range), f32 "
                                  "scales and sums",

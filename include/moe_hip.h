@@ -256,53 +256,25 @@ int moe_layer_stage_times(moe_layer *layer, double *ms, uint64_t *n);
 
 const char *moe_last_error(void);
 
-/* Diagnostics: y[i] = exp(x[i]) computed on the device by the gates' exp (a
+/* Test hook: y[i] = exp(x[i]) computed on the device by the gates' exp (a
  * port of glibc's expf), for checking it against the host libm.  x and y are
  * device f32 [n].  No counterpart in the reference. */
 int moe_debug_expf(const float *x, float *y, uint64_t n, void *stream);
 
-/* Diagnostics: which one-token gate/up kernel the forward uses, for every
+/* Test hook: which one-token gate/up kernel the forward uses, for every
  * layer of the process: 0 the automatic choice, 1 the strided kernel with
  * its separate encoding of h, 2 the unit-aligned kernel that encodes h
  * itself.  Returns the previous choice (>= 0) or MOE_EINVAL.  Both give the
  * same bits.  No counterpart in the reference. */
 int moe_debug_decode_kernel(int32_t choice);
 
-/* Diagnostics: which MFMA kernels the fast paths use, for every layer and
+/* Test hook: which MFMA kernels the fast paths use, for every layer and
  * projection of the process: 0 the two-pass kernels (weight codes times
  * the activations' two f16 pieces, the block scale applied to each block's
  * f32 sum), 1 the three-pass kernels (both operands in two f16 pieces).
  * Returns the previous choice (>= 0) or MOE_EINVAL.  No counterpart in the
  * reference. */
 int moe_debug_mfma_kernel(int32_t choice);
-
-/* Diagnostics: one cooperative launch of `blocks` blocks of 512 threads
- * (all resident: more is MOE_EINVAL) that pass `barriers` grid-wide
- * barriers (a device atomic per block on a counter, a polled generation
- * word; each poll bounded, state[2] set if a bound was hit).  `state`:
- * device u32[4], zero before the first call, left consistent for the next.
- * No counterpart in the reference. */
-int moe_debug_grid_barrier(int32_t blocks, int32_t barriers, uint32_t *state, void *stream);
-
-/* Diagnostics: the issue rate of the two-pass MFMA kernels' instruction
- * mix.  `blocks` blocks of 256 * waves_per_simd (1 or 2) threads; each wave
- * runs `iters` iterations of `mfmas` V_MFMA_F32_32X32X16_F16 (two
- * independent chains) and `valus` f32 fmas on registers of their own, the
- * fmas after the MFMAs (interleave 0) or spread between them (1); one
- * float per thread into out[blocks * 256 * waves_per_simd].  Supported
- * (mfmas, valus, interleave): (8,0,0), (0,56,0), (8,56,0), (8,56,1),
- * (8,32,1).  No counterpart in the reference. */
-int moe_debug_mfma_valu(int32_t mfmas, int32_t valus, int32_t interleave, int32_t waves_per_simd, int32_t blocks,
-                        int32_t iters, float *out, void *stream);
-
-/* Diagnostics: read `bytes` (a multiple of 16, 16-byte aligned device
- * memory) once with a grid-stride 16-byte-load kernel of `blocks` blocks
- * (eight loads in flight per thread; nontemporal != 0: nontemporal loads),
- * writing one xor-fold per block to out[blocks]: the HBM read rate the
- * weight-streaming kernels are measured against.  No counterpart in the
- * reference. */
-int moe_debug_stream_read(const void *src, uint64_t bytes, uint32_t *out, int32_t blocks, int32_t nontemporal,
-                          void *stream);
 
 /* ------------------------------------------------ the model around the layer
  * The rest of the reference's forward (src/model.rs:646-834) as device

@@ -92,10 +92,6 @@ PROTOTYPES = {
     "moe_debug_expf": (C.c_int, [C.c_void_p, C.c_void_p, C.c_uint64, C.c_void_p]),
     "moe_debug_decode_kernel": (C.c_int, [C.c_int32]),
     "moe_debug_mfma_kernel": (C.c_int, [C.c_int32]),
-    "moe_debug_grid_barrier": (C.c_int, [C.c_int32, C.c_int32, C.c_void_p, C.c_void_p]),
-    "moe_debug_mfma_valu": (C.c_int, [C.c_int32, C.c_int32, C.c_int32, C.c_int32, C.c_int32, C.c_int32, C.c_void_p,
-                                      C.c_void_p]),
-    "moe_debug_stream_read": (C.c_int, [C.c_void_p, C.c_uint64, C.c_void_p, C.c_int32, C.c_int32, C.c_void_p]),
     "moe_layer_profile": (C.c_int, [C.c_void_p, C.c_int]),
     "moe_container_open": (C.c_int, [C.c_void_p, C.c_uint64, C.POINTER(C.c_void_p)]),
     "moe_container_close": (None, [C.c_void_p]),
@@ -152,6 +148,40 @@ def lib() -> C.CDLL:
             fn.argtypes = args
         _lib = handle
     return _lib
+
+
+# The bench's measurement probes (moe_amd/diag/moe_diag.h), a library apart
+# from the layer's.
+DIAG_PATH = LIB_PATH.with_name("libmoe_diag.so")
+DIAG_PROTOTYPES = {
+    "moe_diag_last_error": (C.c_char_p, []),
+    "moe_debug_grid_barrier": (C.c_int, [C.c_int32, C.c_int32, C.c_void_p, C.c_void_p]),
+    "moe_debug_mfma_valu": (C.c_int, [C.c_int32, C.c_int32, C.c_int32, C.c_int32, C.c_int32, C.c_int32, C.c_void_p,
+                                      C.c_void_p]),
+    "moe_debug_stream_read": (C.c_int, [C.c_void_p, C.c_uint64, C.c_void_p, C.c_int32, C.c_int32, C.c_void_p]),
+}
+_diag = None
+
+
+def diag() -> C.CDLL:
+    """The probes library (raises if it has not been built)."""
+    global _diag
+    if _diag is None:
+        if not DIAG_PATH.exists():
+            raise RuntimeError(f"{DIAG_PATH} is missing: build it with `python -m moe_amd.build`")
+        handle = C.CDLL(str(DIAG_PATH))
+        for name, (res, args) in DIAG_PROTOTYPES.items():
+            fn = getattr(handle, name)
+            fn.restype = res
+            fn.argtypes = args
+        _diag = handle
+    return _diag
+
+
+def diag_check(code: int, what: str = "") -> None:
+    if code != MOE_OK:
+        msg = diag().moe_diag_last_error().decode(errors="replace")
+        raise MoeError(code, f"{what}: {msg}" if what else msg)
 
 
 def check(code: int, what: str = "") -> None:

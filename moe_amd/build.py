@@ -1,4 +1,4 @@
-"""Build libmoe_hip.so in-tree for gfx950.
+"""Build libmoe_hip.so (and the bench's probes, libmoe_diag.so) in-tree for gfx950.
 
     python -m moe_amd.build            # compile every source, link the library
 
@@ -21,6 +21,9 @@ PKG = Path(__file__).resolve().parent
 CSRC = PKG / "csrc"
 BUILD = PKG / "_build"
 LIB = PKG / "libmoe_hip.so"
+# The bench's measurement probes, a library of their own (not the layer ABI).
+DIAG_SRC = PKG / "diag" / "diag.hip"
+DIAG_LIB = PKG / "libmoe_diag.so"
 ARCH = os.environ.get("MOE_OFFLOAD_ARCH", "gfx950")
 
 HIPCC = shutil.which("hipcc") or "/opt/rocm/bin/hipcc"
@@ -81,8 +84,11 @@ def build(verbose: bool = False) -> Path:
     tmp = LIB.with_suffix(".so.tmp")
     _run([HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-pthread", *map(str, objs), "-o", str(tmp)])
     os.replace(tmp, LIB)
+    dtmp = DIAG_LIB.with_suffix(".so.tmp")
+    _run([HIPCC, *HIP_FLAGS, "-shared", str(DIAG_SRC), "-o", str(dtmp)])
+    os.replace(dtmp, DIAG_LIB)
     if verbose:
-        print(f"built {LIB}")
+        print(f"built {LIB} and {DIAG_LIB.name}")
     return LIB
 
 

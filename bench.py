@@ -431,6 +431,57 @@ def traffic_of(kernel_prefix: str):
     return max(hits, key=lambda k: k.get("grid", 0))["hbm_bytes"] if hits else None
 
 
+def zipf_histogram_md(out_path: str, tokens: int) -> int:
+    """Write the DeepSeek-V3 Zipf workload's achieved selection histogram
+    (synth.zipf_histogram at the bench's inputs) beside its Zipf targets."""
+    from moe_amd import synth
+
+    shape = synth.SHAPES["deepseek_v3_zipf"]
+    h = synth.zipf_histogram(shape, 1, tokens)
+    c, tg = h["counts"], h["target"]
+    total = int(c.sum())
+    cap = 0.45 * tokens
+    lines = [
+        f"# DeepSeek-V3 Zipf workload: achieved expert histogram at T={tokens}",
+        "",
+        f"Shape `deepseek_v3_zipf` (hidden {shape.hidden}, {shape.n_experts} experts of {shape.inter}, top-"
+        f"{shape.top_k}, sigmoid scores + correction bias, {shape.n_group} groups / top-{shape.topk_group}), "
+        f"layer seed 1, inputs `activations(1, {tokens}, {shape.hidden})` (the bench's).  Selections per expert "
+        "under the layer's routing rule, sorted, against `zipf_targets` (Zipf s = "
+        f"{shape.zipf} over the {shape.n_experts} ranks, total T·k = {total}, no rank above the 0.45·T = "
+        f"{cap:.0f} cap).  Counted on the host in float64 with the calibration's own rule "
+        "(`synth.zipf_histogram`); the GPU parity run of the same workload routes its top expert to the same "
+        "count.",
+        "",
+        "Command (from the repo root; CPU only):",
+        "",
+        f"    python bench.py --zipf-histogram profiles/deepseek_v3_zipf_histogram.md --tokens {tokens}",
+        "",
+        f"* experts hit: {h['hit']} of {shape.n_experts}",
+        f"* top expert: {int(c[0])} tokens ({c[0] / tokens:.1%} of T; target {tg[0]:.0f})",
+        f"* L1 distance to the targets: {np.abs(c - tg).sum():.0f} selections ({np.abs(c - tg).sum() / total:.1%} of "
+        "T·k)",
+        f"* selections held by the top 8 / top 32 experts: {c[:8].sum() / total:.1%} / {c[:32].sum() / total:.1%} "
+        f"(targets {tg[:8].sum() / total:.1%} / {tg[:32].sum() / total:.1%})",
+        "",
+        "| rank | achieved | target |",
+        "|---|---|---|",
+    ]
+    ranks = list(range(1, 17)) + [24, 32, 48, 64, 96, 128, 153, 154, 192, 256]
+    for r in ranks:
+        if r <= len(c):
+            lines.append(f"| {r} | {int(c[r - 1])} | {tg[r - 1]:.1f} |")
+    bands = [(17, 32), (33, 64), (65, 128), (129, 256)]
+    lines += ["", "| ranks | achieved (sum) | target (sum) |", "|---|---|---|"]
+    for a, b in bands:
+        lines.append(f"| {a}–{b} | {int(c[a - 1:b].sum())} | {tg[a - 1:b].sum():.0f} |")
+    with open(out_path, "w") as f:
+        f.write("\n".join(lines) + "\n")
+    print(json.dumps(dict(zipf_histogram=out_path, hit=h["hit"], top=int(c[0]),
+                          l1=round(float(np.abs(c - tg).sum()), 1))), flush=True)
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
@@ -458,6 +509,8 @@ def main() -> int:
                     help="time MFMA and VALU issue alone and together (moe_debug_mfma_valu) and exit")
     ap.add_argument("--hbm-ceiling", type=int, default=0, metavar="MIB",
                     help="only time a plain streaming read of MIB MiB (moe_debug_stream_read) and exit")
+    ap.add_argument("--zipf-histogram", metavar="OUT_MD",
+                    help="write the DeepSeek-V3 Zipf workload's achieved expert histogram at --tokens (CPU) and exit")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="only copy MIB MiB device-to-device 5 times (a plain copy kernel of known size, the "
                          "reference point for the FETCH_SIZE / WRITE_SIZE counters) and exit")
@@ -466,6 +519,8 @@ def main() -> int:
         print("bench.py measures one GPU: this build has no multi-GPU path (every GPU box here has one GPU); "
               "run with --gpus 1", file=sys.stderr)
         return 2
+    if args.zipf_histogram:
+        return zipf_histogram_md(args.zipf_histogram, args.tokens)
     if args.copy_calibration:
         return copy_calibration(args.copy_calibration)
     if args.hbm_ceiling:

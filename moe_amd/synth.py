@@ -199,6 +199,26 @@ def zipf_router_scales(router: np.ndarray, bias: np.ndarray, shape: Shape, seed:
     return np.exp(best_ab[0] - best_ab[1] * log_rank)
 
 
+def zipf_histogram(shape: Shape, seed: int, t: int, act_seed: int = 1) -> dict:
+    """The Zipf workload as routed: the layer's router and bias exactly as
+    build_host_layer makes them (same streams, same calibration), the
+    selections per expert of activations(act_seed, t) under the layer's rule
+    (float64, as the calibration counts them), sorted, beside zipf_targets at
+    the same total and cap."""
+    E, H = shape.n_experts, shape.hidden
+    router = np.empty((E, H), dtype=np.float32)
+    _fill(router.view(np.uint8).reshape(-1), seed, STREAM_ROUTER, L.DT_F32, E, H, 0.0, shape.router_std)
+    bias = np.zeros(E, dtype=np.float32)
+    if shape.e_bias_std > 0:
+        _fill(bias.view(np.uint8), seed, STREAM_EBIAS, L.DT_F32, 1, E, 0.0, shape.e_bias_std)
+    scales = zipf_router_scales(router, bias, shape, seed)
+    router *= scales.astype(np.float32)[:, None]
+    x = activations(act_seed, t, H).astype(np.float64)
+    counts = _route_counts(x @ router.astype(np.float64).T, bias.astype(np.float64), shape)
+    target = zipf_targets(E, shape.zipf, float(t * shape.top_k), 0.45 * t)
+    return dict(counts=np.sort(counts)[::-1], target=target, hit=int((counts > 0).sum()), t=t, k=shape.top_k)
+
+
 def build_host_layer(shape: Shape, seed: int) -> HostLayer:
     """Generate and quantise every tensor of a layer into one byte buffer."""
     E, H, I = shape.n_experts, shape.hidden, shape.inter

@@ -496,6 +496,8 @@ def main() -> int:
     ap.add_argument("--cpu-runs", type=int, default=5, help="timed CPU forwards per T (median)")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--mode", type=int, default=0, help="kernel path (moe_layer_set_mode): 0 automatic")
+    ap.add_argument("--tiled", action="store_true",
+                    help="keep the tiled expert copies (moe_layer_set_tiled) that few-tokens calls stream")
     ap.add_argument("--summarize-pmc", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
                     help="write the HBM traffic summary from two rocprofv3 counter passes and exit")
     ap.add_argument("--summarize-trace", nargs=2, metavar=("TRACE_DIR", "OUT_MD"),
@@ -554,6 +556,9 @@ def main() -> int:
     if args.mode:
         for layer in layers:
             layer.set_mode(args.mode)
+    if args.tiled:
+        for layer in layers:
+            layer.set_tiled(True)
     dev = torch.device("cuda:0")
     k = layers[0].k
 

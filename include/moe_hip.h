@@ -189,6 +189,18 @@ int moe_layer_workspace_size(const moe_layer *layer, int32_t max_t, uint64_t *by
  * has one CPU path. */
 int moe_layer_set_mode(moe_layer *layer, int mode);
 
+/* Keep (enable != 0) or drop a second, tiled copy of the layer's expert
+ * matrices on the device: each 32-row region's 64-value steps contiguous,
+ * each row's step with the bytes one MFMA lane needs side by side (Q4_0,
+ * Q5_0 and Q8_0 with K % 64 == 0; otherwise MOE_EUNSUP).  It costs the
+ * experts' bytes again (plus row padding to 32) and makes calls whose
+ * experts average at most ~20 tokens (t > 1) stream it through registers
+ * at about twice the rate of the row-major views; mode 6 uses it for its
+ * 32-token tiles.  Waits for the device; not to be called while another
+ * thread runs a forward on this layer.  No counterpart in the reference,
+ * which keeps one row-major copy. */
+int moe_layer_set_tiled(moe_layer *layer, int enable);
+
 /* Experts each token is routed to (min(top_k, E)) under the current routing. */
 int moe_layer_k(const moe_layer *layer);
 

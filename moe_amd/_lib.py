@@ -78,6 +78,7 @@ PROTOTYPES = {
     "moe_layer_forward_ws": (C.c_int, [C.c_void_p, C.c_void_p, C.c_int32, C.c_void_p, C.c_void_p, C.c_void_p,
                                        C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_uint64, C.c_void_p]),
     "moe_layer_set_mode": (C.c_int, [C.c_void_p, C.c_int]),
+    "moe_layer_set_tiled": (C.c_int, [C.c_void_p, C.c_int]),
     "moe_layer_k": (C.c_int, [C.c_void_p]),
     "moe_layer_forward": (C.c_int, [C.c_void_p, C.c_void_p, C.c_int32, C.c_void_p, C.c_void_p, C.c_void_p,
                                     C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p]),

@@ -545,8 +545,362 @@ __global__ __launch_bounds__(512, 1) __attribute__((amdgpu_waves_per_eu(2, 2))) 
     }
 }
 
+// ---- the tiled layout and its one-subtile kernel ------------------------------
+// Tiles of at most 32 tokens (about 4 to 20 per expert) carry too few
+// products per weight byte for the LDS ring: their time is the weight
+// stream's.  Read row-major, a 32-row region's ring step is a gather of 32
+// rows 36 bytes apart in 32 cache lines, which the CU serves at about a
+// third of HBM speed.  The tiled copy lays each 32-row region's steps out
+// contiguously, and inside a row's step puts the bytes each MFMA lane needs
+// next to each other:
+//   region r, step s at ((r * steps + s) * 32 + l) * RB bytes for row l of
+//   the region (rows past the matrix's are zero), RB = two blocks' bytes;
+//   Q4_0 (36): d0 d1 | codes0[0:8] codes1[0:8] | codes0[8:16] codes1[8:16]
+//   Q5_0 (44): d0 d1 | qh0 | qh1 | codes0[0:8] codes1[0:8] | codes0[8:16] codes1[8:16]
+//   Q8_0 (68): d0 d1 | c0[0:8] c0[16:24] c1[0:8] c1[16:24] | c0[8:16] c0[24:32] c1[8:16] c1[24:32]
+// so lane (l32, hf) loads the head (scales, and Q5_0's high bits) and its
+// own half's 16 (Q8_0: 32) code bytes, and a wave's loads of a step cover
+// 32 RB contiguous bytes.  Each of the eight waves owns one region for the
+// whole K (SIMD sd: regions 2 sd and 2 sd + 1 of the tile; up: gate (j = 0)
+// and up (j = 1) rows n0 + 32 sd ..; down: rows n0 + 64 sd + 32 j ..) and
+// keeps P steps of it in flight in registers; the activations go through
+// two one-step LDS stages filled by plain loads (issued P steps ahead,
+// written one step ahead) and published by one barrier per step.  Tiles of
+// at most 16 tokens pack their hi and lo pieces into the MFMAs' 32 rows.
+template <int DT>
+struct Tiled;
+template <>
+struct Tiled<MOE_DT_Q4_0> {
+    static constexpr int rb = 36, head = 1, half = 4, nd = head + half;
+    // source byte (of the row's two blocks) of each tiled byte
+    static constexpr unsigned char src[rb] = {0,  1,  18, 19, 2,  3,  4,  5,  6,  7,  8,  9,
+                                              20, 21, 22, 23, 24, 25, 26, 27, 10, 11, 12, 13,
+                                              14, 15, 16, 17, 28, 29, 30, 31, 32, 33, 34, 35};
+};
+template <>
+struct Tiled<MOE_DT_Q5_0> {
+    static constexpr int rb = 44, head = 3, half = 4, nd = head + half;
+    static constexpr unsigned char src[rb] = {0,  1,  22, 23, 2,  3,  4,  5,  24, 25, 26, 27, 6,  7,  8,
+                                              9,  10, 11, 12, 13, 28, 29, 30, 31, 32, 33, 34, 35, 14, 15,
+                                              16, 17, 18, 19, 20, 21, 36, 37, 38, 39, 40, 41, 42, 43};
+};
+template <>
+struct Tiled<MOE_DT_Q8_0> {
+    static constexpr int rb = 68, head = 1, half = 8, nd = head + half;
+    static constexpr unsigned char src[rb] = {
+        0,  1,  34, 35,                                  // d0 d1
+        2,  3,  4,  5,  6,  7,  8,  9,  18, 19, 20, 21, 22, 23, 24, 25,   // c0[0:8] c0[16:24]
+        36, 37, 38, 39, 40, 41, 42, 43, 52, 53, 54, 55, 56, 57, 58, 59,   // c1[0:8] c1[16:24]
+        10, 11, 12, 13, 14, 15, 16, 17, 26, 27, 28, 29, 30, 31, 32, 33,   // c0[8:16] c0[24:32]
+        44, 45, 46, 47, 48, 49, 50, 51, 60, 61, 62, 63, 64, 65, 66, 67};  // c1[8:16] c1[24:32]
+};
+template <int DT>
+struct TiledStep {
+    static constexpr int rb = Tiled<DT>::rb, step_bytes = 32 * rb;
+};
+// Steps of weights in flight per wave.
+template <int DT>
+constexpr int tiled_ring() {
+    return DT == MOE_DT_Q8_0 ? 6 : 8;
+}
+typedef uint32_t u32x2_dw __attribute__((ext_vector_type(2), aligned(4)));
+typedef uint32_t u32x3_dw __attribute__((ext_vector_type(3), aligned(4)));
+// Lane hf's dwords of one row step at p: the head, then its half.
+template <int DT>
+__device__ inline void tiled_load(const uint8_t *p, int hf, uint32_t (&v)[Tiled<DT>::nd]) {
+    using TL = Tiled<DT>;
+    const gptr<uint32_t> q = (gptr<uint32_t>)p;
+    if constexpr (TL::head == 1) {
+        v[0] = *q;
+    } else {
+        const u32x3_dw h = *(gptr<u32x3_dw>)q;
+        v[0] = h.x, v[1] = h.y, v[2] = h.z;
+    }
+#pragma unroll
+    for (int i = 0; i < TL::half / 4; i++) {
+        const u32x4_dw c = *(gptr<u32x4_dw>)(q + TL::head + TL::half * hf + 4 * i);
+        v[TL::head + 4 * i] = c.x, v[TL::head + 4 * i + 1] = c.y, v[TL::head + 4 * i + 2] = c.z,
+                       v[TL::head + 4 * i + 3] = c.w;
+    }
+}
+// Block KB's codes (m = 0, 1) and scale from a lane's tiled dwords (the
+// same values as decode2 gives from the row-major slots).
+template <int DT, int KB>
+__device__ inline void tiled_decode(const uint32_t *v, int h, half8 (&bq)[2], float &d) {
+    const uint32_t s = KB == 0 ? (v[0] & 0xffffu) : (v[0] >> 16);
+    d = __half2float(__ushort_as_half((unsigned short)s));
+    uint32_t o[4];
+    if constexpr (DT == MOE_DT_Q4_0) {
+        const __half2 off2 = __floats2half2_rn(1032.0f, 1032.0f);
+        const uint32_t w0 = v[1 + 2 * KB], w1 = v[2 + 2 * KB];
+        codes_q(w0 & 0x0f0f0f0fu, off2, o, 0);
+        codes_q(w1 & 0x0f0f0f0fu, off2, o, 2);
+        bq[0] = pack8(o);
+        codes_q((w0 >> 4) & 0x0f0f0f0fu, off2, o, 0);
+        codes_q((w1 >> 4) & 0x0f0f0f0fu, off2, o, 2);
+        bq[1] = pack8(o);
+    } else if constexpr (DT == MOE_DT_Q5_0) {
+        const __half2 off2 = __floats2half2_rn(1040.0f, 1040.0f);
+        const uint32_t w0 = v[3 + 2 * KB], w1 = v[4 + 2 * KB];
+        const uint32_t hb = v[1 + KB] >> (8 * h);
+        codes_q((w0 & 0x0f0f0f0fu) | spread4(hb & 0xfu), off2, o, 0);
+        codes_q((w1 & 0x0f0f0f0fu) | spread4((hb >> 4) & 0xfu), off2, o, 2);
+        bq[0] = pack8(o);
+        codes_q(((w0 >> 4) & 0x0f0f0f0fu) | spread4((hb >> 16) & 0xfu), off2, o, 0);
+        codes_q(((w1 >> 4) & 0x0f0f0f0fu) | spread4((hb >> 20) & 0xfu), off2, o, 2);
+        bq[1] = pack8(o);
+    } else {
+        const __half2 off2 = __floats2half2_rn(1152.0f, 1152.0f);
+#pragma unroll
+        for (int m = 0; m < 2; m++) {
+            codes_q(v[1 + 4 * KB + 2 * m] ^ 0x80808080u, off2, o, 0);
+            codes_q(v[2 + 4 * KB + 2 * m] ^ 0x80808080u, off2, o, 2);
+            bq[m] = pack8(o);
+        }
+    }
+}
+
+// One thread per (region, step, row): the row's step, permuted.
+template <int DT>
+__global__ __launch_bounds__(256) void tile_kernel(MatDev m, uint8_t *__restrict__ dst, size_t n) {
+    using TL = Tiled<DT>;
+    const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= n) return;
+    const int steps = m.cols / SK;
+    const int l = (int)(i & 31);
+    const size_t rs = i >> 5;
+    const int s = (int)(rs % steps);
+    const int row = (int)(rs / steps) * 32 + l;
+    uint32_t in[TL::rb / 4], out[TL::rb / 4];
+    if (row < m.rows) {
+        const uint32_t *p = reinterpret_cast<const uint32_t *>(m.ptr + (size_t)row * m.stride + (size_t)s * TL::rb);
+#pragma unroll
+        for (int k = 0; k < TL::rb / 4; k++) in[k] = gload(p + k);
+    } else {
+#pragma unroll
+        for (int k = 0; k < TL::rb / 4; k++) in[k] = 0;
+    }
+#pragma unroll
+    for (int k = 0; k < TL::rb / 4; k++) {
+        uint32_t w = 0;
+#pragma unroll
+        for (int b = 0; b < 4; b++) {
+            const int sb = TL::src[4 * k + b];
+            w |= ((in[sb >> 2] >> (8 * (sb & 3))) & 0xffu) << (8 * b);
+        }
+        out[k] = w;
+    }
+    uint32_t *q = reinterpret_cast<uint32_t *>(dst + i * TL::rb);
+#pragma unroll
+    for (int k = 0; k < TL::rb / 4; k++) gstore(q + k, out[k]);
+}
+
+template <int DT, bool UP>
+__global__ __launch_bounds__(512, 1) __attribute__((amdgpu_waves_per_eu(2, 2))) void tiled_kernel(MfmaArgs a,
+                                                                                                    int mode, int gx,
+                                                                                                    int ksplit) {
+    using TL = Tiled<DT>;
+    using TS = TiledStep<DT>;
+    constexpr int ND = TL::nd;
+    constexpr int P = tiled_ring<DT>();
+    __shared__ __attribute__((aligned(16))) uint8_t smem[2 * 8192];
+    __shared__ int src_row[32], dst_row[32], ex_row[32];
+
+    TileInfo ti;
+    if (!tile_of<32, 32>(a, mode, gx, ti)) return;
+    const ExpertDev &ex = a.experts[ti.g];
+    const MatDev &W0 = UP ? ex.m[0] : ex.m[2];
+    const MatDev &W1 = UP ? ex.m[1] : ex.m[2];
+    const int n0 = ti.ntile * (UP ? SW / 2 : SW);
+    if (n0 >= W0.rows) return;
+    const int kspan = W0.cols / ksplit;
+    const int kbeg = ti.ksplit * kspan;
+    const int nsteps = kspan / SK;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int sd = wv & 3, j = wv >> 2;  // the wave's SIMD and region
+    const int l32 = lane & 31, hf = lane >> 5;
+    const int Icol = ti.shared ? a.I_s : a.I;
+    const int valid = min(32, ti.n - ti.m0);
+
+    const uint16_t *ahi = UP ? a.xhi : (ti.shared ? a.hshi : a.hhi);
+    const uint16_t *alo = UP ? a.xlo : (ti.shared ? a.hslo : a.hlo);
+    const int32_t *aex = UP ? a.xex : (ti.shared ? a.hsex : a.hex);
+    if (tid < 32) {
+        int s = -1, d = -1, e = 0;
+        if (tid < valid) {
+            d = ti.row0 + ti.m0 + tid;
+            s = UP ? (ti.shared ? ti.m0 + tid : a.perm_tok[d]) : d;
+            e = aex[s];
+        }
+        src_row[tid] = s;
+        dst_row[tid] = d;
+        ex_row[tid] = e;
+    }
+    __syncthreads();
+
+    // The wave's region of the tiled copy (a region past the matrix's rows,
+    // whose sums no one stores, reads region 0), lane l32's row in it.
+    const MatDev &Wd = (UP && j == 1) ? W1 : W0;
+    const int row0 = UP ? n0 + 32 * sd : n0 + 64 * sd + 32 * j;
+    const size_t region = row0 < Wd.rows ? (size_t)(row0 / 32) : 0;
+    const uint8_t *wp = Wd.tiled + (region * (size_t)(Wd.cols / SK) + (size_t)(kbeg / SK)) * TS::step_bytes +
+                        (size_t)l32 * TL::rb;
+    const size_t arow_bytes = (size_t)(UP ? a.H : Icol) * 2;
+    const lds_p sm = (lds_p)smem;
+
+    auto run = [&](auto pk_c) {
+        constexpr bool PK = decltype(pk_c)::value;
+        constexpr int NP = PK ? 1 : 2;    // pieces per MFMA operand set
+        constexpr int NV = PK ? 8 : 16;   // accumulator values that hold tokens
+        constexpr int AST = PK ? 4096 : 8192;  // activation bytes per step
+        // Activation staging: thread tid moves AB bytes of each step.
+        //   unpacked: piece tid / 256, token row (tid / 8) % 32, 16-byte chunk tid % 8
+        //   packed:   MFMA row tid / 16 (piece row / 16, token row % 16), 8-byte unit tid % 16
+        constexpr int AB = PK ? 8 : 16;
+        const int arow = PK ? (tid >> 4) : ((tid >> 3) & 31);      // MFMA row in the stage
+        const int apiece = PK ? (arow >> 4) : (tid >> 8);
+        const int atok = PK ? (arow & 15) : arow;
+        const int achunk = PK ? ((tid & 15) >> 1) : (tid & 7);
+        const int sr = src_row[atok < valid ? atok : 0];
+        const uint8_t *asrc = reinterpret_cast<const uint8_t *>(apiece ? alo : ahi) + (size_t)sr * arow_bytes +
+                              (size_t)kbeg * 2 + (size_t)(PK ? 8 * (tid & 15) : 16 * (tid & 7));
+        const uint32_t adst = (uint32_t)(PK ? 0 : apiece * 4096) + (uint32_t)arow * 128u +
+                              ((uint32_t)(achunk ^ ((arow >> 1) & 7)) << 4) + (PK ? 8u * (tid & 1) : 0u);
+        typedef uint32_t areg_t __attribute__((ext_vector_type(AB / 4)));
+        auto aload = [&](int step) {
+            const int sc = step < nsteps ? step : nsteps - 1;
+            return *(gptr<areg_t>)(asrc + (size_t)sc * (SK * 2));
+        };
+        auto awrite = [&](int stage, areg_t v) { *(lptr<areg_t>)(smem + stage * 8192 + adst) = v; };
+        // A fragments of step stage `stage`: block kb, half m, piece p.
+        uint32_t aoff[2][2];
+#pragma unroll
+        for (int kb = 0; kb < 2; kb++)
+#pragma unroll
+            for (int m = 0; m < 2; m++)
+                aoff[kb][m] = (uint32_t)l32 * 128u + ((uint32_t)((4 * kb + 2 * m + hf) ^ ((l32 >> 1) & 7)) << 4);
+
+        floatx16 acc = floatx16{};
+        uint32_t raw[P][ND];
+        areg_t areg[P];
+        // Prologue: step 0's activations into stage 0, then the loads of
+        // steps 1 .. P (activations) and 0 .. P - 1 (weights) in the order
+        // the loop issues them, so that the loop's waits find the same
+        // number of loads in flight on its first round as on the others.
+        {
+            const areg_t a0 = aload(0);
+#pragma unroll
+            for (int i = 0; i < P; i++) {
+                areg[(i + 1) % P] = aload(i + 1);
+                tiled_load<DT>(wp + (size_t)(i < nsteps ? i : nsteps - 1) * TS::step_bytes, hf, raw[i]);
+            }
+            awrite(0, a0);
+        }
+        asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+
+        // Step s with ring slot i = s % P.
+        auto step = [&](auto i_c, int s) {
+            constexpr int i = decltype(i_c)::value, i1 = (i + 1) % P;
+            // The next step's activations into the other stage (last
+            // read before the previous barrier), then the loads of
+            // step s + 1 + P into the freed registers.
+            awrite((s + 1) & 1, areg[i1]);
+            areg[i1] = aload(s + 1 + P);
+            // This step's codes and scales, then step s + P's weights.
+            half8 B[2][2];
+            float dsc[2];
+            tiled_decode<DT, 0>(raw[i], hf, B[0], dsc[0]);
+            tiled_decode<DT, 1>(raw[i], hf, B[1], dsc[1]);
+            // The codes and scales exist in registers of their own before
+            // the slot's next load is issued: the compiler would otherwise
+            // keep reading the loaded registers, hold them across the load
+            // and copy them at the loop's end, waiting for loads in flight.
+            asm volatile("" : "+v"(dsc[0]), "+v"(dsc[1]), "+v"(B[0][0]), "+v"(B[0][1]), "+v"(B[1][0]), "+v"(B[1][1]));
+            tiled_load<DT>(wp + (size_t)(s + P < nsteps ? s + P : nsteps - 1) * TS::step_bytes, hf, raw[i]);
+            const lds_p st = sm + (s & 1) * 8192;
+            floatx16 ps[2];
+#pragma unroll
+            for (int kb = 0; kb < 2; kb++) {
+#pragma unroll
+                for (int m = 0; m < 2; m++) {
+#pragma unroll
+                    for (int p = 0; p < NP; p++) {
+                        const half8 A = lds_h8(st + p * 4096 + aoff[kb][m]);
+                        ps[kb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(A, B[kb][m], (m | p) ? ps[kb] : floatx16{},
+                                                                        0, 0, 0);
+                    }
+                }
+            }
+#pragma unroll
+            for (int kb = 0; kb < 2; kb++) {
+#pragma unroll
+                for (int v = 0; v < NV; v++)
+                    acc[v] = fmaf(dsc[kb], PK ? ps[kb][v] + ps[kb][v + 8] : ps[kb][v], acc[v]);
+            }
+            asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+        };
+        // Whole rounds of the ring without guards (a guard per step would
+        // merge each slot's registers with their reloaded values and copy
+        // them, waiting for loads just issued), then the rest.
+        int s0 = 0;
+        for (; s0 + P <= nsteps; s0 += P) static_for<0, P>([&](auto i_c) { step(i_c, s0 + decltype(i_c)::value); });
+        static_for<0, P>([&](auto i_c) {
+            if (s0 + decltype(i_c)::value < nsteps) step(i_c, s0 + decltype(i_c)::value);
+        });
+
+        // ---- epilogue.  Lane holds C[8 (v / 4) + 4 hf + v % 4][row l32 of
+        // its region], scaled by 2^ex_row.
+        if (UP) {
+            // The up wave (j = 1) hands its sums to the gate wave of its SIMD.
+            float *xb = reinterpret_cast<float *>(smem) + sd * 1024;
+            if (j == 1) {
+#pragma unroll
+                for (int v = 0; v < NV; v++) xb[v * 64 + lane] = acc[v];
+            }
+            __syncthreads();
+            if (j == 0) {
+                float *hout = ti.shared ? a.hs : a.h;
+                const int col = n0 + 32 * sd + l32;
+                if (col < W0.rows) {
+#pragma unroll
+                    for (int v = 0; v < NV; v++) {
+                        const int row = 8 * (v / 4) + 4 * hf + (v % 4);
+                        const int d = dst_row[row];
+                        if (d < 0) continue;
+                        const int e = ex_row[row];
+                        const float g = ldexpf(acc[v], -e), u = ldexpf(xb[v * 64 + lane], -e);
+                        hout[(size_t)d * Icol + col] = g * __builtin_amdgcn_rcpf(1.0f + __expf(-g)) * u;
+                    }
+                }
+            }
+        } else {
+            float *yout = ti.shared ? a.ys + ti.ksplit * a.yspart : a.y + ti.ksplit * a.ypart;
+            const int col = n0 + 64 * sd + 32 * j + l32;
+            if (col < W0.rows) {
+#pragma unroll
+                for (int v = 0; v < NV; v++) {
+                    const int row = 8 * (v / 4) + 4 * hf + (v % 4);
+                    const int d = dst_row[row];
+                    if (d >= 0) yout[(size_t)d * a.H + col] = ldexpf(acc[v], -ex_row[row]);
+                }
+            }
+        }
+    };
+    if (valid <= 16)
+        run(std::true_type{});
+    else
+        run(std::false_type{});
+}
+
 template <int DT, bool UP, int S>
-hipError_t launch_s(dim3 grid, const MfmaArgs &a, int mode, int ksplit, hipStream_t s) {
+hipError_t launch_s(dim3 grid, const MfmaArgs &a, int mode, int ksplit, bool tiled, hipStream_t s) {
+    if constexpr (S == 1) {
+        if (tiled) {
+            hipLaunchKernelGGL((tiled_kernel<DT, UP>), grid, dim3(512), 0, s, a, mode, (int)grid.x, ksplit);
+            return hipGetLastError();
+        }
+    }
     constexpr int lds = s2_lds<DT, S>();
     static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void *>(&stream2_kernel<DT, UP, S>),
                                                        hipFuncAttributeMaxDynamicSharedMemorySize, lds);
@@ -556,24 +910,24 @@ hipError_t launch_s(dim3 grid, const MfmaArgs &a, int mode, int ksplit, hipStrea
 }
 
 template <int DT, bool UP>
-hipError_t launch_fmt(int bm, dim3 grid, const MfmaArgs &a, int mode, int ksplit, hipStream_t s) {
+hipError_t launch_fmt(int bm, dim3 grid, const MfmaArgs &a, int mode, int ksplit, bool tiled, hipStream_t s) {
     switch (bm) {
-    case 32: return launch_s<DT, UP, 1>(grid, a, mode, ksplit, s);
-    case 64: return launch_s<DT, UP, 2>(grid, a, mode, ksplit, s);
-    case 128: return launch_s<DT, UP, 4>(grid, a, mode, ksplit, s);
+    case 32: return launch_s<DT, UP, 1>(grid, a, mode, ksplit, tiled, s);
+    case 64: return launch_s<DT, UP, 2>(grid, a, mode, ksplit, tiled, s);
+    case 128: return launch_s<DT, UP, 4>(grid, a, mode, ksplit, tiled, s);
     case 160:
-        if constexpr (DT != MOE_DT_Q8_0) return launch_s<DT, UP, 5>(grid, a, mode, ksplit, s);
+        if constexpr (DT != MOE_DT_Q8_0) return launch_s<DT, UP, 5>(grid, a, mode, ksplit, tiled, s);
         return hipErrorInvalidValue;
     default: return hipErrorInvalidValue;
     }
 }
 
 template <bool UP>
-hipError_t launch_dt(int dt, int bm, dim3 grid, const MfmaArgs &a, int mode, int ksplit, hipStream_t s) {
+hipError_t launch_dt(int dt, int bm, dim3 grid, const MfmaArgs &a, int mode, int ksplit, bool tiled, hipStream_t s) {
     switch (dt) {
-    case MOE_DT_Q4_0: return launch_fmt<MOE_DT_Q4_0, UP>(bm, grid, a, mode, ksplit, s);
-    case MOE_DT_Q5_0: return launch_fmt<MOE_DT_Q5_0, UP>(bm, grid, a, mode, ksplit, s);
-    case MOE_DT_Q8_0: return launch_fmt<MOE_DT_Q8_0, UP>(bm, grid, a, mode, ksplit, s);
+    case MOE_DT_Q4_0: return launch_fmt<MOE_DT_Q4_0, UP>(bm, grid, a, mode, ksplit, tiled, s);
+    case MOE_DT_Q5_0: return launch_fmt<MOE_DT_Q5_0, UP>(bm, grid, a, mode, ksplit, tiled, s);
+    case MOE_DT_Q8_0: return launch_fmt<MOE_DT_Q8_0, UP>(bm, grid, a, mode, ksplit, tiled, s);
     default: return hipErrorInvalidValue;
     }
 }
@@ -591,6 +945,31 @@ int stream_tile(double tokens, bool q8) {
     return q8 ? 128 : 160;
 }
 
+size_t tiled_bytes(const MatDev &m) {
+    if (m.cols <= 0 || m.cols % SK || m.rows <= 0) return 0;
+    size_t rb = 0;
+    switch (m.dt) {
+    case MOE_DT_Q4_0: rb = Tiled<MOE_DT_Q4_0>::rb; break;
+    case MOE_DT_Q5_0: rb = Tiled<MOE_DT_Q5_0>::rb; break;
+    case MOE_DT_Q8_0: rb = Tiled<MOE_DT_Q8_0>::rb; break;
+    default: return 0;
+    }
+    return (size_t)((m.rows + 31) / 32) * (m.cols / SK) * 32 * rb;
+}
+
+hipError_t tile_matrix(const MatDev &m, uint8_t *dst, hipStream_t s) {
+    const size_t bytes = tiled_bytes(m);
+    if (!bytes || !dst) return hipErrorInvalidValue;
+    const size_t n = (size_t)((m.rows + 31) / 32) * (m.cols / SK) * 32;
+    const dim3 grid((unsigned)((n + 255) / 256));
+    switch (m.dt) {
+    case MOE_DT_Q4_0: hipLaunchKernelGGL(tile_kernel<MOE_DT_Q4_0>, grid, dim3(256), 0, s, m, dst, n); break;
+    case MOE_DT_Q5_0: hipLaunchKernelGGL(tile_kernel<MOE_DT_Q5_0>, grid, dim3(256), 0, s, m, dst, n); break;
+    default: hipLaunchKernelGGL(tile_kernel<MOE_DT_Q8_0>, grid, dim3(256), 0, s, m, dst, n); break;
+    }
+    return hipGetLastError();
+}
+
 hipError_t launch_stream(bool up, const MfmaArgs &a0, int bm, const ExpertDev &e0, const ExpertDev *sh, hipStream_t s) {
     MfmaArgs a = a0;
     const double per = a.E > 0 ? (double)a.T * a.k / a.E : 0.0;
@@ -599,9 +978,14 @@ hipError_t launch_stream(bool up, const MfmaArgs &a0, int bm, const ExpertDev &e
     const int cols = up ? SW / 2 : SW;
     const int ks = up ? 1 : a.ksplit;
     const dim3 grid = tile_grid(a.max_tiles, m.rows, cols, ks, a.xcd_cus, up);
-    hipError_t err = up ? launch_dt<true>(m.dt, bm, grid, a, 0, ks, s) : launch_dt<false>(m.dt, bm, grid, a, 0, ks, s);
+    // Tiled copies exist for every routed expert or for none.
+    const bool tiled = m.tiled && (!up || e0.m[1].tiled);
+    hipError_t err = up ? launch_dt<true>(m.dt, bm, grid, a, 0, ks, tiled, s)
+                        : launch_dt<false>(m.dt, bm, grid, a, 0, ks, tiled, s);
     if (err != hipSuccess || !sh) return err;
-    return launch_stream_single(up, a, bm, *sh, s);
+    // The shared expert takes every token: its own tile for T tokens.
+    const bool q8 = m.dt == MOE_DT_Q8_0 || sh->m[0].dt == MOE_DT_Q8_0 || sh->m[2].dt == MOE_DT_Q8_0;
+    return launch_stream_single(up, a, stream_tile((double)a.T, q8), *sh, s);
 }
 
 hipError_t launch_stream_single(bool up, const MfmaArgs &a0, int bm, const ExpertDev &ex, hipStream_t s) {
@@ -611,7 +995,8 @@ hipError_t launch_stream_single(bool up, const MfmaArgs &a0, int bm, const Exper
     const int cols = up ? SW / 2 : SW;
     const int ks = up ? 1 : a.ksplit;
     const dim3 gs = tile_grid((a.T + bm - 1) / bm, m.rows, cols, ks, a.xcd_cus, up);
-    return up ? launch_dt<true>(m.dt, bm, gs, a, 1, ks, s) : launch_dt<false>(m.dt, bm, gs, a, 1, ks, s);
+    const bool tiled = m.tiled && (!up || ex.m[1].tiled);
+    return up ? launch_dt<true>(m.dt, bm, gs, a, 1, ks, tiled, s) : launch_dt<false>(m.dt, bm, gs, a, 1, ks, tiled, s);
 }
 
 }  // namespace moe

@@ -125,6 +125,7 @@ struct moe_layer {
     bool any_disabled = false;
     std::vector<StreamWs> ws;            // one workspace per stream used with moe_layer_forward
     std::vector<Retired> retired;        // outgrown or released workspaces, not yet freed
+    void *tiled_mem = nullptr;           // the experts' tiled copies (moe_layer_set_tiled), one allocation
     int reserved_t = 0, reserved_k = 0;  // after moe_layer_reserve: calls beyond these fail
     // stage timing
     bool profile = false;
@@ -517,6 +518,8 @@ int forward_on(moe_layer *L, const CallState &c, Workspace &w, const float *x, i
         path = L->mfma_ok ? kMfma : kGemv;
         if (t == 1 && L->decode_ok)
             path = kDecode;
+        else if (L->tiled_mem && stream_tile((double)t * k / L->E, L->mfma_bm != 160) == 32)
+            path = kStream;  // 32-token tiles stream the tiled copies
         else if (L->batch_ok && batch_pays(t, k, L->E, L->H, batch_tile_tokens(L->H, t, k, L->E)))
             path = kBatch;
     }
@@ -1109,6 +1112,7 @@ void moe_layer_destroy(moe_layer *L) {
         hipFree(r.base);
         if (r.done) hipEventDestroy(r.done);
     }
+    hipFree(L->tiled_mem);
     hipFree(L->router);
     hipFree(L->experts_dev);
     hipFree(L->expert_bytes);
@@ -1148,6 +1152,55 @@ int moe_layer_set_routing(moe_layer *L, const moe_routing *r) {
     L->n_forced = n_forced;
     L->temp = temp;
     L->top_k_override = top_k;
+    return MOE_OK;
+}
+
+int moe_layer_set_tiled(moe_layer *L, int enable) {
+    if (!L) return fail(MOE_EINVAL, "moe_layer_set_tiled: bad argument");
+    if (enable && !L->mfma_ok) return fail(MOE_EUNSUP, "this layer's shapes do not fit the MFMA kernels");
+    DeviceGuard g(L->ctx->device);
+    std::lock_guard<std::mutex> lk(L->mu);
+    if ((L->tiled_mem != nullptr) == (enable != 0)) return MOE_OK;
+    hipError_t he = hipDeviceSynchronize();  // queued calls may read the expert table
+    if (he != hipSuccess) return hip_fail(he, "moe_layer_set_tiled");
+    const int n = L->E + (L->has_shared ? 1 : 0);
+    if (!enable) {
+        for (int e = 0; e < n; e++)
+            for (MatDev &m : L->experts_host[e].m) m.tiled = nullptr;
+        he = hipMemcpy(L->experts_dev, L->experts_host.data(), sizeof(ExpertDev) * (L->E + 1), hipMemcpyHostToDevice);
+        hipFree(L->tiled_mem);
+        L->tiled_mem = nullptr;
+        return he == hipSuccess ? MOE_OK : hip_fail(he, "expert table");
+    }
+    size_t total = 0;
+    for (int e = 0; e < n; e++)
+        for (const MatDev &m : L->experts_host[e].m) {
+            const size_t b = tiled_bytes(m);
+            if (!b) return fail(MOE_EUNSUP, "expert %d: a matrix's format or shape has no tiled layout", e);
+            total += (b + 255) / 256 * 256;
+        }
+    uint8_t *mem = nullptr;
+    if ((he = hipMalloc(&mem, total)) != hipSuccess)
+        return fail(MOE_ENOMEM, "tiled expert copies (%zu bytes): %s", total, hipGetErrorString(he));
+    size_t off = 0;
+    std::vector<ExpertDev> table = L->experts_host;
+    for (int e = 0; e < n && he == hipSuccess; e++)
+        for (MatDev &m : table[e].m) {
+            if ((he = tile_matrix(m, mem + off, nullptr)) != hipSuccess) break;
+            m.tiled = mem + off;
+            off += (tiled_bytes(m) + 255) / 256 * 256;
+        }
+    if (he == hipSuccess) he = hipDeviceSynchronize();
+    if (he == hipSuccess)
+        he = hipMemcpy(L->experts_dev, table.data(), sizeof(ExpertDev) * (L->E + 1), hipMemcpyHostToDevice);
+    if (he != hipSuccess) {
+        hipFree(mem);
+        (void)hipMemcpy(L->experts_dev, L->experts_host.data(), sizeof(ExpertDev) * (L->E + 1),
+                        hipMemcpyHostToDevice);
+        return hip_fail(he, "tiled expert copies");
+    }
+    L->experts_host = table;
+    L->tiled_mem = mem;
     return MOE_OK;
 }
 

@@ -34,6 +34,10 @@ struct MatDev {
     // weights are split into f16 pieces (exact: a power of two), so that the
     // matrix's largest |d q| lies in [2^14, 2^15).
     int32_t wexp;
+    int32_t _pad = 0;
+    // The matrix in the tiled layout of the one-subtile streaming kernel
+    // (tile_matrix), or null.
+    const uint8_t *tiled = nullptr;
 };
 
 // A SwiGLU expert: gate [I,H], up [I,H], down [H,I].  Routed experts occupy
@@ -293,10 +297,17 @@ hipError_t launch_mfma_single(bool up, const MfmaArgs &a, int bm, const ExpertDe
 hipError_t launch_split_rows(const float *src, int rows, int cols, uint16_t *hi, uint16_t *lo, int32_t *ex,
                              hipStream_t s);
 
-// The streaming expert kernels (expert_stream.hip): one wave per SIMD, tiles
-// of bm = 32, 64, 128 or 160 tokens (160 only for Q4_0 / Q5_0) x 256 weight
-// rows, the same arguments and activation pieces as launch_mfma.
+// The streaming expert kernels (expert_stream.hip): eight waves per tile of
+// bm = 32, 64, 128 or 160 tokens (160 only for Q4_0 / Q5_0) x 256 weight
+// rows, the same arguments and activation pieces as launch_mfma.  With
+// every matrix of the launch tiled (MatDev::tiled), 32-token tiles stream
+// their weights through registers from the tiled copy.
 int stream_tile(double tokens, bool q8);
+// The tiled layout: bytes of matrix m's copy (0 if its format or shape has
+// none: Q4_0 / Q5_0 / Q8_0 with cols % 64 == 0), and the copy written to
+// dst (tiled_bytes(m) bytes of device memory) on stream s.
+size_t tiled_bytes(const MatDev &m);
+hipError_t tile_matrix(const MatDev &m, uint8_t *dst, hipStream_t s);
 hipError_t launch_stream(bool up, const MfmaArgs &a, int bm, const ExpertDev &e0, const ExpertDev *sh, hipStream_t s);
 hipError_t launch_stream_single(bool up, const MfmaArgs &a, int bm, const ExpertDev &ex, hipStream_t s);
 // Largest |d| (f16 bits) of every block scale of matrix m of expert g into

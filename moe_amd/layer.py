@@ -313,6 +313,11 @@ class MoeLayer:
     def set_mode(self, mode: int) -> None:
         L.check(L.lib().moe_layer_set_mode(self.handle, mode), "moe_layer_set_mode")
 
+    def set_tiled(self, enable: bool = True) -> None:
+        """Keep (or drop) the tiled copy of the expert matrices that calls of
+        few tokens per expert stream at about twice the row-major rate."""
+        L.check(L.lib().moe_layer_set_tiled(self.handle, 1 if enable else 0), "moe_layer_set_tiled")
+
     def reserve(self, max_t: int, stream=None) -> None:
         """Allocate the workspace for `stream` up front (no later call on it
         allocates; calls beyond max_t tokens fail)."""

@@ -156,6 +156,53 @@ def test_layer_parity(ctx, oracle, name, t, mode):
     assert err <= TOL, f"{name} T={t}: max rel err {err:.3e} > {TOL}"
 
 
+# The tiled copies (moe_layer_set_tiled): calls of few tokens per expert take
+# the register-streaming kernel in the automatic path, and mode 6 uses it for
+# its 32-token tiles.  Per shape: tiles of at most 16 tokens (packed pieces)
+# and of 17-32, the shared expert, every format; one fresh layer per shape.
+TILED_CASES = [
+    ("tiny_mixtral", [2, 24, 40, 100], [None, 6]),
+    ("mixtral", [8, 32, 64], [None, 6]),
+    ("qwen3", [32, 128, 300], [None, 6]),
+    ("v2_lite", [32, 96], [None, 6]),
+    ("deepseek_v3", [64], [None]),
+    ("qwen2_moe", [17, 64], [None, 6]),
+]
+
+
+@pytest.mark.parametrize("name,ts,modes", TILED_CASES, ids=[c[0] for c in TILED_CASES])
+def test_tiled_parity(ctx, oracle, name, ts, modes):
+    """With the tiled copies kept: routing bit-exact, hits and counters
+    equal, output within TOL of the CPU path, for the automatic path and the
+    forced streaming mode; dropping the copies returns the row-major path."""
+    from moe_amd import synth
+
+    host = synth.build_host_layer(synth.SHAPES[name], SEED)
+    gl = synth.make_layer(ctx, host)
+    ol = oracle.from_host_layer(host)
+    try:
+        gl.set_tiled(True)
+        gl.set_tiled(True)  # already kept: nothing to do
+        for t in ts:
+            x = synth.activations(SEED + 100 + t, t, host.shape.hidden)
+            out, sel, w, hits, stats = ol.forward(x)
+            for mode in modes:
+                g = run_gpu(gl, x, mode=mode if mode is not None else 0)
+                assert_routing_equal(g, sel, w, f"{name} T={t} mode={mode}")
+                assert np.array_equal(g["hits"][:hits[0] + 1], hits[:hits[0] + 1]), "hit lists differ"
+                assert np.array_equal(g["stats"][:3], stats[:3]), f"counters gpu {g['stats']} ref {stats}"
+                err = rel_err(g["out"], out)
+                log(f"{name} T={t} tiled mode={mode}: max rel err {err:.2e}")
+                record("tiled", f"{name} T={t} mode={mode if mode is not None else 'auto'}", err)
+                assert err <= TOL, f"{name} T={t} mode={mode}: max rel err {err:.3e} > {TOL}"
+        gl.set_tiled(False)
+        x = synth.activations(SEED + 100 + ts[0], ts[0], host.shape.hidden)
+        g = run_gpu(gl, x, mode=0)
+        assert rel_err(g["out"], ol.forward(x)[0]) <= TOL
+    finally:
+        gl.close()
+
+
 @pytest.mark.parametrize("name,t", [("deepseek_v3_zipf", 4096), ("v2_lite", 8192)])
 def test_layer_parity_full_size(ctx, oracle, name, t):
     """A full-size prefill (DeepSeek-V3 with Zipf-skewed popularity: the top

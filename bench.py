@@ -496,8 +496,8 @@ def main() -> int:
     ap.add_argument("--cpu-runs", type=int, default=5, help="timed CPU forwards per T (median)")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--mode", type=int, default=0, help="kernel path (moe_layer_set_mode): 0 automatic")
-    ap.add_argument("--tiled", action="store_true",
-                    help="keep the tiled expert copies (moe_layer_set_tiled) that few-tokens calls stream")
+    ap.add_argument("--no-tiled", action="store_true",
+                    help="do not keep the tiled expert copies (moe_layer_set_tiled) that few-tokens calls stream")
     ap.add_argument("--summarize-pmc", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
                     help="write the HBM traffic summary from two rocprofv3 counter passes and exit")
     ap.add_argument("--summarize-trace", nargs=2, metavar=("TRACE_DIR", "OUT_MD"),
@@ -556,7 +556,7 @@ def main() -> int:
     if args.mode:
         for layer in layers:
             layer.set_mode(args.mode)
-    if args.tiled:
+    if not args.no_tiled:
         for layer in layers:
             layer.set_tiled(True)
     dev = torch.device("cuda:0")
@@ -641,7 +641,7 @@ def main() -> int:
         "config": {"workload": f"{shape.name}_moe_layer_T{args.tokens}", "hidden": shape.hidden,
                    "inter": shape.inter, "experts": shape.n_experts, "top_k": shape.top_k,
                    "weights": DT_NAMES.get(shape.expert_dt, str(shape.expert_dt)), "tokens": args.tokens,
-                   "weight_copies": args.copies},
+                   "weight_copies": args.copies, "tiled_copies": not args.no_tiled},
         "roofline": {"bound": "mfma", "kernel": f"mfma_kernel<{DT_NAMES.get(shape.expert_dt)}, up> (expert gate/up, "
                                                 f"MFMA grouped GEMM)",
                      "achieved": round(achieved, 2), "peak": MFMA_F16_PEAK_TFLOPS, "unit": "TFLOP/s",

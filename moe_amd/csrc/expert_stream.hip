@@ -564,9 +564,11 @@ __global__ __launch_bounds__(512, 1) __attribute__((amdgpu_waves_per_eu(2, 2))) 
 // whole K (SIMD sd: regions 2 sd and 2 sd + 1 of the tile; up: gate (j = 0)
 // and up (j = 1) rows n0 + 32 sd ..; down: rows n0 + 64 sd + 32 j ..) and
 // keeps P steps of it in flight in registers; the activations go through
-// two one-step LDS stages filled by plain loads (issued P steps ahead,
-// written one step ahead) and published by one barrier per step.  Tiles of
-// at most 16 tokens pack their hi and lo pieces into the MFMAs' 32 rows.
+// LDS in groups of G steps, double-buffered, filled by plain loads (issued
+// P steps ahead, written G steps ahead) and published by one barrier per
+// group.  Tiles of
+// at most 16 tokens pack their hi and lo pieces into the MFMAs' 32 rows, and
+// tiles of at most 8 skip the fmas of the rows that hold no token.
 template <int DT>
 struct Tiled;
 template <>
@@ -601,7 +603,7 @@ struct TiledStep {
 // Steps of weights in flight per wave.
 template <int DT>
 constexpr int tiled_ring() {
-    return DT == MOE_DT_Q8_0 ? 6 : 8;
+    return DT == MOE_DT_Q4_0 ? 8 : 6;
 }
 typedef uint32_t u32x2_dw __attribute__((ext_vector_type(2), aligned(4)));
 typedef uint32_t u32x3_dw __attribute__((ext_vector_type(3), aligned(4)));
@@ -703,7 +705,9 @@ __global__ __launch_bounds__(512, 1) __attribute__((amdgpu_waves_per_eu(2, 2))) 
     using TS = TiledStep<DT>;
     constexpr int ND = TL::nd;
     constexpr int P = tiled_ring<DT>();
-    __shared__ __attribute__((aligned(16))) uint8_t smem[2 * 8192];
+    constexpr int G = 2;  // steps of activations per LDS group (one barrier per group)
+    static_assert(P % G == 0, "ring rounds hold whole groups");
+    __shared__ __attribute__((aligned(16))) uint8_t smem[2 * G * 8192];
     __shared__ int src_row[32], dst_row[32], ex_row[32];
 
     TileInfo ti;
@@ -749,10 +753,12 @@ __global__ __launch_bounds__(512, 1) __attribute__((amdgpu_waves_per_eu(2, 2))) 
     const size_t arow_bytes = (size_t)(UP ? a.H : Icol) * 2;
     const lds_p sm = (lds_p)smem;
 
-    auto run = [&](auto pk_c) {
+    // NV: accumulator values that hold tokens (C rows 8 (v / 4) + 4 hf + v % 4
+    // for v < NV): 16 unpacked, 8 packed, 4 for at most 8 tokens.
+    auto run = [&](auto pk_c, auto nv_c) {
         constexpr bool PK = decltype(pk_c)::value;
         constexpr int NP = PK ? 1 : 2;    // pieces per MFMA operand set
-        constexpr int NV = PK ? 8 : 16;   // accumulator values that hold tokens
+        constexpr int NV = decltype(nv_c)::value;
         constexpr int AST = PK ? 4096 : 8192;  // activation bytes per step
         // Activation staging: thread tid moves AB bytes of each step.
         //   unpacked: piece tid / 256, token row (tid / 8) % 32, 16-byte chunk tid % 8
@@ -772,7 +778,9 @@ __global__ __launch_bounds__(512, 1) __attribute__((amdgpu_waves_per_eu(2, 2))) 
             const int sc = step < nsteps ? step : nsteps - 1;
             return *(gptr<areg_t>)(asrc + (size_t)sc * (SK * 2));
         };
-        auto awrite = [&](int stage, areg_t v) { *(lptr<areg_t>)(smem + stage * 8192 + adst) = v; };
+        // Step q's activations: stage (group q / G's buffer, q % G of it).
+        auto stage_of = [&](int q) { return ((q / G) & 1) * G + q % G; };
+        auto awrite = [&](int q, areg_t v) { *(lptr<areg_t>)(smem + stage_of(q) * 8192 + adst) = v; };
         // A fragments of step stage `stage`: block kb, half m, piece p.
         uint32_t aoff[2][2];
 #pragma unroll
@@ -784,42 +792,58 @@ __global__ __launch_bounds__(512, 1) __attribute__((amdgpu_waves_per_eu(2, 2))) 
         floatx16 acc = floatx16{};
         uint32_t raw[P][ND];
         areg_t areg[P];
-        // Prologue: step 0's activations into stage 0, then the loads of
-        // steps 1 .. P (activations) and 0 .. P - 1 (weights) in the order
-        // the loop issues them, so that the loop's waits find the same
-        // number of loads in flight on its first round as on the others.
+        // Prologue: group 0's activations into its stages, then the loads
+        // of steps G .. G + P - 1 (activations) and 0 .. P - 1 (weights) in
+        // the order the loop issues them, so that the loop's waits find the
+        // same number of loads in flight on its first round as on the
+        // others.
         {
-            const areg_t a0 = aload(0);
+            areg_t a0[G];
+#pragma unroll
+            for (int g = 0; g < G; g++) a0[g] = aload(g);
 #pragma unroll
             for (int i = 0; i < P; i++) {
-                areg[(i + 1) % P] = aload(i + 1);
+                areg[(i + G) % P] = aload(i + G);
                 tiled_load<DT>(wp + (size_t)(i < nsteps ? i : nsteps - 1) * TS::step_bytes, hf, raw[i]);
             }
-            awrite(0, a0);
+#pragma unroll
+            for (int g = 0; g < G; g++) awrite(g, a0[g]);
         }
         asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
 
-        // Step s with ring slot i = s % P.
+        // Step s with ring slot i = s % P, software-pipelined over three
+        // steps: step s's MFMAs go out, then step s - 1's fmas (its sums
+        // long done), then step s + 1's codes are decoded, so no wave waits
+        // on its own MFMAs.  The codes, scales and sums of a step live in the
+        // register set of its parity (P is even, so i & 1 is s's parity).
+        static_assert(P % 2 == 0, "ring slots keep the steps' parity");
+        half8 Bq[2][2][2];  // [parity][block][m]
+        float dq[2][2];     // [parity][block]
+        floatx16 pq[2][2];  // [parity][block]
+        auto decode = [&](int slot_dummy, const uint32_t(&v)[ND], int q) {
+            (void)slot_dummy;
+            tiled_decode<DT, 0>(v, hf, Bq[q][0], dq[q][0]);
+            tiled_decode<DT, 1>(v, hf, Bq[q][1], dq[q][1]);
+        };
+        auto scale_add = [&](int q) {
+#pragma unroll
+            for (int kb = 0; kb < 2; kb++) {
+#pragma unroll
+                for (int v = 0; v < NV; v++)
+                    acc[v] = fmaf(dq[q][kb], PK ? pq[q][kb][v] + pq[q][kb][v + 8] : pq[q][kb][v], acc[v]);
+            }
+        };
+        decode(0, raw[0], 0);
+        pq[1][0] = pq[1][1] = floatx16{};
+        dq[1][0] = dq[1][1] = 0.0f;
         auto step = [&](auto i_c, int s) {
-            constexpr int i = decltype(i_c)::value, i1 = (i + 1) % P;
-            // The next step's activations into the other stage (last
-            // read before the previous barrier), then the loads of
-            // step s + 1 + P into the freed registers.
-            awrite((s + 1) & 1, areg[i1]);
-            areg[i1] = aload(s + 1 + P);
-            // This step's codes and scales, then step s + P's weights.
-            half8 B[2][2];
-            float dsc[2];
-            tiled_decode<DT, 0>(raw[i], hf, B[0], dsc[0]);
-            tiled_decode<DT, 1>(raw[i], hf, B[1], dsc[1]);
-            // The codes and scales exist in registers of their own before
-            // the slot's next load is issued: the compiler would otherwise
-            // keep reading the loaded registers, hold them across the load
-            // and copy them at the loop's end, waiting for loads in flight.
-            asm volatile("" : "+v"(dsc[0]), "+v"(dsc[1]), "+v"(B[0][0]), "+v"(B[0][1]), "+v"(B[1][0]), "+v"(B[1][1]));
-            tiled_load<DT>(wp + (size_t)(s + P < nsteps ? s + P : nsteps - 1) * TS::step_bytes, hf, raw[i]);
-            const lds_p st = sm + (s & 1) * 8192;
-            floatx16 ps[2];
+            constexpr int i = decltype(i_c)::value, i1 = (i + 1) % P, q = i & 1, ia = (i + G) % P;
+            // Step s + G's activations into the next group's buffer (last
+            // read before the previous group's barrier), then the loads of
+            // step s + G + P into the freed registers.
+            awrite(s + G, areg[ia]);
+            areg[ia] = aload(s + G + P);
+            const lds_p st = sm + stage_of(s) * 8192;
 #pragma unroll
             for (int kb = 0; kb < 2; kb++) {
 #pragma unroll
@@ -827,18 +851,23 @@ __global__ __launch_bounds__(512, 1) __attribute__((amdgpu_waves_per_eu(2, 2))) 
 #pragma unroll
                     for (int p = 0; p < NP; p++) {
                         const half8 A = lds_h8(st + p * 4096 + aoff[kb][m]);
-                        ps[kb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(A, B[kb][m], (m | p) ? ps[kb] : floatx16{},
-                                                                        0, 0, 0);
+                        pq[q][kb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(A, Bq[q][kb][m],
+                                                                           (m | p) ? pq[q][kb] : floatx16{}, 0, 0, 0);
                     }
                 }
             }
-#pragma unroll
-            for (int kb = 0; kb < 2; kb++) {
-#pragma unroll
-                for (int v = 0; v < NV; v++)
-                    acc[v] = fmaf(dsc[kb], PK ? ps[kb][v] + ps[kb][v + 8] : ps[kb][v], acc[v]);
-            }
-            asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+            scale_add(q ^ 1);  // step s - 1 (zero sums before the first step)
+            decode(i1, raw[i1], q ^ 1);
+            // The codes and scales exist in registers of their own before
+            // the slot's next load is issued: the compiler would otherwise
+            // keep reading the loaded registers, hold them across the load
+            // and copy them at the loop's end, waiting for loads in flight.
+            asm volatile("" : "+v"(dq[q ^ 1][0]), "+v"(dq[q ^ 1][1]), "+v"(Bq[q ^ 1][0][0]), "+v"(Bq[q ^ 1][0][1]),
+                         "+v"(Bq[q ^ 1][1][0]), "+v"(Bq[q ^ 1][1][1]));
+            tiled_load<DT>(wp + (size_t)(s + P < nsteps ? s + P : nsteps - 1) * TS::step_bytes, hf, raw[i]);
+            // The group's last step: publish the next group, free this one.
+            if constexpr ((i + 1) % G == 0) asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+            __builtin_amdgcn_sched_barrier(0);  // each step's code stays in its step
         };
         // Whole rounds of the ring without guards (a guard per step would
         // merge each slot's registers with their reloaded values and copy
@@ -848,6 +877,14 @@ __global__ __launch_bounds__(512, 1) __attribute__((amdgpu_waves_per_eu(2, 2))) 
         static_for<0, P>([&](auto i_c) {
             if (s0 + decltype(i_c)::value < nsteps) step(i_c, s0 + decltype(i_c)::value);
         });
+        if ((nsteps - 1) & 1)  // the last step's fmas
+            scale_add(1);
+        else
+            scale_add(0);
+        // Every wave's last reads of the stages are done before the epilogue
+        // reuses their memory (a last group of fewer than G steps ends
+        // without a barrier).
+        __syncthreads();
 
         // ---- epilogue.  Lane holds C[8 (v / 4) + 4 hf + v % 4][row l32 of
         // its region], scaled by 2^ex_row.
@@ -887,10 +924,12 @@ __global__ __launch_bounds__(512, 1) __attribute__((amdgpu_waves_per_eu(2, 2))) 
             }
         }
     };
-    if (valid <= 16)
-        run(std::true_type{});
+    if (valid <= 8)
+        run(std::true_type{}, std::integral_constant<int, 4>{});
+    else if (valid <= 16)
+        run(std::true_type{}, std::integral_constant<int, 8>{});
     else
-        run(std::false_type{});
+        run(std::false_type{}, std::integral_constant<int, 16>{});
 }
 
 template <int DT, bool UP, int S>
@@ -970,6 +1009,8 @@ hipError_t tile_matrix(const MatDev &m, uint8_t *dst, hipStream_t s) {
     return hipGetLastError();
 }
 
+int stream_tile_exact(int tokens, bool q8) { return tokens <= 32 ? 32 : stream_tile((double)tokens, q8); }
+
 hipError_t launch_stream(bool up, const MfmaArgs &a0, int bm, const ExpertDev &e0, const ExpertDev *sh, hipStream_t s) {
     MfmaArgs a = a0;
     const double per = a.E > 0 ? (double)a.T * a.k / a.E : 0.0;
@@ -985,7 +1026,7 @@ hipError_t launch_stream(bool up, const MfmaArgs &a0, int bm, const ExpertDev &e
     if (err != hipSuccess || !sh) return err;
     // The shared expert takes every token: its own tile for T tokens.
     const bool q8 = m.dt == MOE_DT_Q8_0 || sh->m[0].dt == MOE_DT_Q8_0 || sh->m[2].dt == MOE_DT_Q8_0;
-    return launch_stream_single(up, a, stream_tile((double)a.T, q8), *sh, s);
+    return launch_stream_single(up, a, stream_tile_exact(a.T, q8), *sh, s);
 }
 
 hipError_t launch_stream_single(bool up, const MfmaArgs &a0, int bm, const ExpertDev &ex, hipStream_t s) {

@@ -701,7 +701,7 @@ int forward_on(moe_layer *L, const CallState &c, Workspace &w, const float *x, i
         if (rc) return rc;
         if (side) {
             e = fork_side(L->ctx, s);
-            const int bs = sp ? stream_tile((double)t, L->mfma_bm != 160) : bm;
+            const int bs = sp ? stream_tile_exact(t, L->mfma_bm != 160) : bm;
             if (e == hipSuccess)
                 e = sp ? launch_stream_single(true, m, bs, *sh, L->ctx->side) : launch_mfma_single(true, m, bm, *sh, L->ctx->side);
             if (e == hipSuccess) e = launch_split_rows(w.hs, t, L->I_s, w.hshi, w.hslo, w.hsex, L->ctx->side);

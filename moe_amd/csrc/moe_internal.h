@@ -303,6 +303,9 @@ hipError_t launch_split_rows(const float *src, int rows, int cols, uint16_t *hi,
 // every matrix of the launch tiled (MatDev::tiled), 32-token tiles stream
 // their weights through registers from the tiled copy.
 int stream_tile(double tokens, bool q8);
+// The tile of a launch whose one tile holds exactly `tokens` (the shared
+// expert): 32 up to 32 tokens, else stream_tile's.
+int stream_tile_exact(int tokens, bool q8);
 // The tiled layout: bytes of matrix m's copy (0 if its format or shape has
 // none: Q4_0 / Q5_0 / Q8_0 with cols % 64 == 0), and the copy written to
 // dst (tiled_bytes(m) bytes of device memory) on stream s.

@@ -516,11 +516,16 @@ int forward_on(moe_layer *L, const CallState &c, Workspace &w, const float *x, i
         path = (Path)c.mode;
     } else if (L->fast_ok) {
         path = L->mfma_ok ? kMfma : kGemv;
+        // The tiled copies' 32-token tiles beat the few-tokens kernels down
+        // to half a token per expert on average (below it, each hit expert
+        // holds about one token, which the integer-dot kernels stream faster).
+        const bool tiled = L->tiled_mem && stream_tile((double)t * k / L->E, L->mfma_bm != 160) == 32;
+        const bool batch = L->batch_ok && batch_pays(t, k, L->E, L->H, batch_tile_tokens(L->H, t, k, L->E));
         if (t == 1 && L->decode_ok)
             path = kDecode;
-        else if (L->tiled_mem && stream_tile((double)t * k / L->E, L->mfma_bm != 160) == 32)
-            path = kStream;  // 32-token tiles stream the tiled copies
-        else if (L->batch_ok && batch_pays(t, k, L->E, L->H, batch_tile_tokens(L->H, t, k, L->E)))
+        else if (tiled && (!batch || 2 * t * k >= L->E))
+            path = kStream;
+        else if (batch)
             path = kBatch;
     }
     if (path == kBatch && (!L->batch_ok || t > w.batch_t)) path = L->mfma_ok ? kMfma : kGemv;

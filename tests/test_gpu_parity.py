@@ -168,6 +168,17 @@ TILED_CASES = [
     ("deepseek_v3", [64], [None]),
     ("qwen2_moe", [17, 64], [None, 6]),
 ]
+# Tiles of 2 to 5 subtiles (forced streaming mode): 64- to 160-token tiles,
+# every format, shared experts of every width.
+TILED_PREFILL_CASES = [
+    ("tiny_mixtral", [100, 257], [6]),
+    ("mixtral", [100, 512], [6]),
+    ("qwen3", [2048], [6]),
+    ("v2_lite", [256], [6]),
+    ("deepseek_v3", [1024], [6]),
+    ("qwen2_moe", [512], [6]),
+]
+TILED_CASES += [(n + "_prefill", ts, modes) for n, ts, modes in TILED_PREFILL_CASES]
 
 
 @pytest.mark.parametrize("name,ts,modes", TILED_CASES, ids=[c[0] for c in TILED_CASES])
@@ -177,6 +188,7 @@ def test_tiled_parity(ctx, oracle, name, ts, modes):
     forced streaming mode; dropping the copies returns the row-major path."""
     from moe_amd import synth
 
+    name = name.replace("_prefill", "")
     host = synth.build_host_layer(synth.SHAPES[name], SEED)
     gl = synth.make_layer(ctx, host)
     ol = oracle.from_host_layer(host)

@@ -711,15 +711,23 @@ __global__ __launch_bounds__(512, 1) __attribute__((amdgpu_waves_per_eu(2, 2))) 
     __shared__ int src_row[32], dst_row[32], ex_row[32];
 
     TileInfo ti;
-    if (!tile_of<32, 32>(a, mode, gx, ti)) return;
+    if (!tile_of<32, 32, UP>(a, mode, gx, ti)) return;
     const ExpertDev &ex = a.experts[ti.g];
     const MatDev &W0 = UP ? ex.m[0] : ex.m[2];
     const MatDev &W1 = UP ? ex.m[1] : ex.m[2];
     const int n0 = ti.ntile * (UP ? SW / 2 : SW);
     if (n0 >= W0.rows) return;
     const int kspan = W0.cols / ksplit;
-    const int kbeg = ti.ksplit * kspan;
-    const int nsteps = kspan / SK;
+    int kbeg = ti.ksplit * kspan;
+    int nsteps = kspan / SK;
+    // A tile of the launch's last round split along K (gate/up): half 0
+    // takes the first nsteps / 2 steps, half 1 the rest.
+    const bool khalf = UP && ti.khalf >= 0;
+    if (khalf) {
+        const int h0 = nsteps / 2;
+        kbeg += ti.khalf ? h0 * SK : 0;
+        nsteps = ti.khalf ? nsteps - h0 : h0;
+    }
     const int tid = threadIdx.x, lane = tid & 63;
     const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int sd = wv & 3, j = wv >> 2;  // the wave's SIMD and region
@@ -885,6 +893,32 @@ __global__ __launch_bounds__(512, 1) __attribute__((amdgpu_waves_per_eu(2, 2))) 
         // reuses their memory (a last group of fewer than G steps ends
         // without a barrier).
         __syncthreads();
+
+        // A K half: both blocks write their sums to the tile's slot; the one
+        // that counts second adds the other's and goes on, the first is done
+        // (no block waits for another).  Sums of either half are added in
+        // the same order whichever finishes first (a + b = b + a).
+        if (khalf) {
+            float *part = a.tail_part + (size_t)ti.slot * (2 * 8 * 16 * 64);
+#pragma unroll
+            for (int v = 0; v < NV; v++) part[((ti.khalf * 8 + wv) * 16 + v) * 64 + lane] = acc[v];
+            __syncthreads();
+            __shared__ int s_second;
+            if (tid == 0) {
+                __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+                const bool second = atomicAdd(&a.tail_cnt[ti.slot], 1u) == 1u;
+                if (second) {
+                    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+                    a.tail_cnt[ti.slot] = 0u;  // zero for the next call
+                }
+                s_second = second;
+            }
+            __syncthreads();
+            if (!s_second) return;
+#pragma unroll
+            for (int v = 0; v < NV; v++) acc[v] += part[(((1 - ti.khalf) * 8 + wv) * 16 + v) * 64 + lane];
+            __syncthreads();
+        }
 
         // ---- epilogue.  Lane holds C[8 (v / 4) + 4 hf + v % 4][row l32 of
         // its region], scaled by 2^ex_row.
@@ -1254,13 +1288,18 @@ int stream_tile_exact(int tokens, bool q8) { return tokens <= 32 ? 32 : stream_t
 hipError_t launch_stream(bool up, const MfmaArgs &a0, int bm, const ExpertDev &e0, const ExpertDev *sh, hipStream_t s) {
     MfmaArgs a = a0;
     const double per = a.E > 0 ? (double)a.T * a.k / a.E : 0.0;
-    a.xcd_cus = split_cus(per < bm ? per : bm, 48.0);
     const MatDev &m = up ? e0.m[0] : e0.m[2];
+    // Tiled copies exist for every routed expert or for none.
+    const bool tiled = m.tiled && (!up || e0.m[1].tiled);
+    // One-subtile gate/up tiles split the last round's tiles along K (their
+    // tokens cannot be halved usefully); other launches along tokens, when
+    // the tiles hold enough of them.
+    const bool ktail = up && tiled && bm == 32 && a.tail_part && a.tail_cnt && device_cus() / 8 <= 2 * kTailPerXcd;
+    a.xcd_cus = ktail ? device_cus() / 8 : split_cus(per < bm ? per : bm, 48.0);
+    if (!ktail) a.tail_part = nullptr, a.tail_cnt = nullptr;
     const int cols = up ? SW / 2 : SW;
     const int ks = up ? 1 : a.ksplit;
     const dim3 grid = tile_grid(a.max_tiles, m.rows, cols, ks, a.xcd_cus, up);
-    // Tiled copies exist for every routed expert or for none.
-    const bool tiled = m.tiled && (!up || e0.m[1].tiled);
     hipError_t err = up ? launch_dt<true>(m.dt, bm, grid, a, 0, ks, tiled, s)
                         : launch_dt<false>(m.dt, bm, grid, a, 0, ks, tiled, s);
     if (err != hipSuccess || !sh) return err;
@@ -1271,6 +1310,7 @@ hipError_t launch_stream(bool up, const MfmaArgs &a0, int bm, const ExpertDev &e
 
 hipError_t launch_stream_single(bool up, const MfmaArgs &a0, int bm, const ExpertDev &ex, hipStream_t s) {
     MfmaArgs a = a0;
+    a.tail_part = nullptr, a.tail_cnt = nullptr;  // the shared expert's tiles split along tokens only
     a.xcd_cus = split_cus((double)(a.T < bm ? a.T : bm), 48.0);
     const MatDev &m = up ? ex.m[0] : ex.m[2];
     const int cols = up ? SW / 2 : SW;

@@ -21,11 +21,15 @@ namespace moe {
 // in two blocks along its tokens: SUB-token subtiles [0, ceil(MT / 2)) in
 // one and the rest in the other, at the end of the XCD's range, so the last
 // round is full and each of its blocks does about half a tile's products.
+// KHALF: the last tiles are split along K instead (khalf 0: the first half
+// of the steps, 1: the rest), each such tile with a slot of its own (XCD
+// x's i-th: x * kTailPerXcd + i) where the two blocks meet.
 struct TileInfo {
     int g, m0, n, row0, ntile, ksplit;
     bool shared;
+    int khalf = -1, slot = 0;
 };
-template <int BM, int SUB>
+template <int BM, int SUB, bool KHALF = false>
 __device__ inline bool tile_of(const MfmaArgs &a, int mode, int gx, TileInfo &ti) {
     const int gy = gridDim.y, gz = gridDim.z;
     const int total = gx * gy;
@@ -41,7 +45,8 @@ __device__ inline bool tile_of(const MfmaArgs &a, int mode, int gx, TileInfo &ti
         const int per = (valid + 7) >> 3;
         const int j = lin >> 3;
         const int tail = gz == 1 && a.xcd_cus > 0 ? per % a.xcd_cus : 0;
-        if (tail > 0 && 2 * tail <= a.xcd_cus && 8 * (per + tail) <= total) {
+        if (tail > 0 && 2 * tail <= a.xcd_cus && 8 * (per + tail) <= total &&
+            (!KHALF || (tail <= kTailPerXcd && a.tail_part && a.tail_cnt))) {
             // Blocks head .. head + tail - 1 take the first halves of the
             // XCD's last `tail` tiles, the next `tail` blocks their second.
             const int head = per - tail;
@@ -51,6 +56,7 @@ __device__ inline bool tile_of(const MfmaArgs &a, int mode, int gx, TileInfo &ti
             } else {
                 half = j - head >= tail;
                 t = (lin & 7) * per + head + (j - head - (half ? tail : 0));
+                if (KHALF) ti.khalf = half, ti.slot = (lin & 7) * kTailPerXcd + (j - head - (half ? tail : 0));
             }
         } else {
             if (j >= per) return false;
@@ -72,7 +78,7 @@ __device__ inline bool tile_of(const MfmaArgs &a, int mode, int gx, TileInfo &ti
         if (g >= a.E) return false;
         ti.g = g, ti.m0 = a.tiles[4 * i + 1], ti.n = a.counts[g], ti.row0 = a.offsets[g], ti.shared = false;
     }
-    if (half >= 0) {
+    if (half >= 0 && !KHALF) {
         // The tile's tokens [m0, end), end - m0 <= BM, in two parts.
         const int end = min(ti.n, ti.m0 + BM);
         const int mh = (end - ti.m0 + 2 * SUB - 1) / (2 * SUB);  // ceil(MT / 2) subtiles

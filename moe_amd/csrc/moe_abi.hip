@@ -263,7 +263,8 @@ size_t ws_layout(const moe_layer *L, int max_t, int k, Workspace *w, char *base)
         size_t bytes;
     };
     const Item items[] = {
-        {(void **)&x.route_count, 4},
+        {(void **)&x.route_count, kZeroBytes},  // with the K-half tiles' counts
+        {(void **)&x.tail_part, L->tiled_mem ? (size_t)kTailSlots * 2 * 8 * 16 * 64 * 4 : 0},
         {(void **)&x.logits, T * (E + 1) * 4},
         {(void **)&x.sel, T * k * 4},
         {(void **)&x.wsel, T * k * 4},
@@ -305,6 +306,8 @@ size_t ws_layout(const moe_layer *L, int max_t, int k, Workspace *w, char *base)
     x.base = base;
     x.bytes = off;
     x.chunks_cap = (size_t)dispatch_chunks_upto((int)T) * E;
+    if (base) x.tail_cnt = x.route_count + 64;
+    if (!L->tiled_mem) x.tail_part = nullptr;
     return off;
 }
 
@@ -365,7 +368,7 @@ int stream_ws(moe_layer *L, hipStream_t s, int t, int k, Workspace &out) {
     void *base = nullptr;
     hipError_t e = hipMalloc(&base, bytes);
     if (e != hipSuccess) return fail(MOE_ENOMEM, "workspace of %zu bytes for %d tokens: %s", bytes, max_t, hipGetErrorString(e));
-    if ((e = hipMemset(base, 0, 256)) != hipSuccess) {
+    if ((e = hipMemset(base, 0, kZeroBytes)) != hipSuccess) {
         hipFree(base);
         return fail(MOE_EHIP, "workspace counters: %s", hipGetErrorString(e));
     }
@@ -682,6 +685,8 @@ int forward_on(moe_layer *L, const CallState &c, Workspace &w, const float *x, i
         m.hsex = w.hsex;
         m.y = w.y;
         m.ys = w.ys;
+        m.tail_part = w.tail_part;
+        m.tail_cnt = w.tail_cnt;
         m.T = t;
         m.H = L->H;
         m.I = L->I;

@@ -81,6 +81,15 @@ struct GateParams {
 };
 
 // Per-call scratch, sized for max_t tokens (see moe_layer_reserve).
+// K-half tiles of a launch's last round (tile_of): at most kTailPerXcd per
+// XCD, one slot each.
+constexpr int kTailPerXcd = 16;
+constexpr int kTailSlots = 8 * kTailPerXcd;
+// Bytes at the start of a workspace that must be zero before its first call
+// (every call leaves them zero): the one-token route's block count and the
+// K-half tiles' counts (at byte 256).
+constexpr size_t kZeroBytes = 1024;
+
 struct Workspace {
     int32_t max_t = 0;
     float *logits = nullptr;      // [T, E+1]
@@ -96,6 +105,8 @@ struct Workspace {
     int32_t *tiles = nullptr;     // [4 * max_tiles] (group, m0, group's first tile, group's tiles) for the MFMA path
     DecodeTask *dtasks = nullptr; // [k + 1] one-token task table
     unsigned *route_count = nullptr;  // [1] finished router blocks (one-token route), zero between calls
+    unsigned *tail_cnt = nullptr;     // [kTailSlots] K-half tiles' counts, zero between calls
+    float *tail_part = nullptr;       // K-half tiles' partial sums (with tiled copies), or null
     int32_t *ntiles = nullptr;    // [1]
     int32_t *chunks = nullptr;    // [dispatch_chunks_upto(max_t) * E] per-chunk expert counts / first rows
     size_t chunks_cap = 0;        // entries of chunks
@@ -272,6 +283,11 @@ struct MfmaArgs {
     int shared_tiles;             // tiles of the shared expert at the end of the tile list (0 if none)
     int ksplit;                   // down projection: K parts (1, 2 or 4), part p written at y + p * ypart
     int xcd_cus;                  // CUs per XCD (set by the launchers)
+    // One-subtile gate/up tiles split along K in a launch's last round:
+    // partial sums [slots][2][8 waves][16][64] f32 and a count per slot
+    // (zero between calls), or null (no such split).
+    float *tail_part = nullptr;
+    unsigned *tail_cnt = nullptr;
 };
 // Token tile of the MFMA kernels for a layer whose matrices have formats
 // dts[0..n): 160, or 128 when a Q8_0 matrix leaves LDS room for fewer rows.

@@ -824,7 +824,7 @@ int scratch_on(int device, void *&out) {
         hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
         if (e != hipSuccess) return hip_fail(e, "hipGetSymbolAddress(scratch)");
         if (!p || (uintptr_t)p % 256) return fail(MOE_EHIP, "scratch array at %p is not 256-byte aligned", p);
-        if ((e = hipMemset(p, 0, 256)) != hipSuccess) return hip_fail(e, "clearing the scratch counters");
+        if ((e = hipMemset(p, 0, kZeroBytes)) != hipSuccess) return hip_fail(e, "clearing the scratch counters");
         g_scratch_ptr[device] = p;
     }
     out = g_scratch_ptr[device];

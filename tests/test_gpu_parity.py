@@ -635,6 +635,50 @@ def test_reservation_above_chunk_widening(ctx, oracle):
         gl.close()
 
 
+@pytest.mark.parametrize("name,tiled", [("tiny_mixtral", False), ("qwen2_moe", True)])
+def test_graph_capture_replays(ctx, oracle, name, tiled):
+    """moe_layer_forward captured into a HIP graph on a reserved stream (the
+    shared expert then stays on that stream): three replays, with eager
+    calls and synchronisations between them, each equal bit for bit to the
+    eager call's output, for one-token, few-tokens and MFMA-sized calls."""
+    import torch
+
+    from moe_amd import synth
+
+    host = synth.build_host_layer(synth.SHAPES[name], SEED)
+    gl = synth.make_layer(ctx, host)
+    ol = oracle.from_host_layer(host)
+    try:
+        if tiled:
+            gl.set_tiled(True)
+        s = torch.cuda.Stream()
+        for t in (1, 24, 300):
+            gl.reserve(t, stream=s)
+            x = torch.from_numpy(synth.activations(SEED + 110 + t, t, host.shape.hidden)).cuda()
+            out = torch.empty_like(x)
+            with torch.cuda.stream(s):
+                gl.feed_forward(x, out, stream=s)
+            torch.cuda.synchronize()
+            eager = out.clone()
+            assert rel_err(eager.cpu().numpy(), ol.forward(x.cpu().numpy())[0]) <= TOL
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g, stream=s):
+                gl.feed_forward(x, out, stream=s)
+            torch.cuda.synchronize()
+            other = torch.from_numpy(synth.activations(SEED + 120 + t, t, host.shape.hidden)).cuda()
+            for rep in range(3):
+                out.fill_(float("nan"))
+                g.replay()
+                torch.cuda.synchronize()
+                assert torch.equal(out, eager), f"{name} T={t} replay {rep}"
+                gl.feed_forward(other, torch.empty_like(other))  # eager work between replays
+                torch.cuda.synchronize()
+            del g
+    finally:
+        torch.cuda.synchronize()
+        gl.close()
+
+
 def test_workspace_growth_and_release(ctx, oracle):
     """Token counts rising one at a time on one stream (each growth retires
     the outgrown workspace), then the stream's workspace released and the

@@ -83,8 +83,7 @@ __device__ inline bool btile_of(const BatchArgs &a, int mode, int nt, BTile &b) 
     const int gx = gridDim.x, gy = gridDim.y;
     const int total = gx * gy;
     const int lin = blockIdx.x + gx * blockIdx.y;
-    const int nall = gload(a.ntiles);
-    const int routed = nall - a.shared_tiles;
+    const int routed = mode == 1 ? 0 : gload(a.ntiles) - a.shared_tiles;
     const int valid = (mode == 1 ? a.shared_tiles : routed) * gx;
     int t = lin;
     if ((total & 7) == 0) {
@@ -94,20 +93,23 @@ __device__ inline bool btile_of(const BatchArgs &a, int mode, int nt, BTile &b) 
         t = (lin & 7) * per + j;
     }
     if (t >= valid) return false;
-    int i;
+    int g, m0;
     if (mode == 1) {
+        // The shared expert's tiles: every token in tiles of a.nt, as the
+        // dispatch lists them after the routed ones, taken from the
+        // arguments so that these launches need nothing the routing writes.
         const int mt = a.shared_tiles;
         b.rb = t / mt;
-        i = routed + t % mt;
+        g = a.E, m0 = (t % mt) * a.nt;
     } else {
         // The tiles of one expert are contiguous: t / gx lies inside t's expert.
         const int ie = t / gx;
         const int f = gload(a.tiles + 4 * ie + 2), mt = gload(a.tiles + 4 * ie + 3);
         const int local = t - f * gx;
-        i = f + local % mt;
+        const int i = f + local % mt;
         b.rb = local / mt;
+        g = gload(a.tiles + 4 * i), m0 = gload(a.tiles + 4 * i + 1);
     }
-    const int g = gload(a.tiles + 4 * i), m0 = gload(a.tiles + 4 * i + 1);
     b.shared = mode == 1;
     if (!b.shared && g >= a.E) return false;
     b.g = g;

@@ -89,12 +89,14 @@ struct moe_ctx {
     int device = 0;
     std::mutex mu;
     std::vector<Region> regions;
-    // The stream the shared expert's kernels run on beside the routed ones
-    // (few-tokens and MFMA paths), and the events that fork it from and
-    // join it to the caller's stream; side_mu makes each record-and-wait
-    // pair atomic between callers.  Null if they could not be created.
+    // The stream that runs the encoding of x beside the routing and the
+    // shared expert's kernels beside the routed ones (few-tokens and MFMA
+    // paths), and the events that fork it from the caller's stream, mark the
+    // end of x's encoding, and join it back; side_mu makes each
+    // record-and-wait pair atomic between callers.  Null if they could not
+    // be created.
     hipStream_t side = nullptr;
-    hipEvent_t ev_fork = nullptr, ev_join = nullptr;
+    hipEvent_t ev_fork = nullptr, ev_join = nullptr, ev_x = nullptr;
     std::mutex side_mu;
 };
 
@@ -491,17 +493,30 @@ int route_and_dispatch(moe_layer *L, const CallState &c, Workspace &w, const flo
     });
 }
 
-// The side stream waits for what stream s has queued so far (fork), or s
-// for what the side stream has (join).
-hipError_t fork_side(moe_ctx *ctx, hipStream_t s) {
-    std::lock_guard<std::mutex> g(ctx->side_mu);
-    hipError_t e = hipEventRecord(ctx->ev_fork, s);
-    return e == hipSuccess ? hipStreamWaitEvent(ctx->side, ctx->ev_fork, 0) : e;
-}
+// Stream s waits for what the side stream has queued so far.
 hipError_t join_side(moe_ctx *ctx, hipStream_t s) {
     std::lock_guard<std::mutex> g(ctx->side_mu);
     hipError_t e = hipEventRecord(ctx->ev_join, ctx->side);
     return e == hipSuccess ? hipStreamWaitEvent(s, ctx->ev_join, 0) : e;
+}
+// x's encoding on the side stream: fork the side stream from s, encode x
+// there (pieces for the MFMA and streaming kernels, int8 codes for the
+// few-tokens kernels) and mark its end with ev_x, all before the routing is
+// queued on s, so that the two run together.  wait_x then makes s wait for
+// that mark before the first expert kernel.  A later call may record ev_x
+// again before this call's wait_x; the side stream runs in order, so s then
+// waits for a later point of it, which includes this call's encoding.
+hipError_t encode_x_beside(moe_ctx *ctx, hipStream_t s, bool codes, const float *x, int t, int H, Workspace &w) {
+    std::lock_guard<std::mutex> g(ctx->side_mu);
+    hipError_t e = hipEventRecord(ctx->ev_fork, s);
+    if (e == hipSuccess) e = hipStreamWaitEvent(ctx->side, ctx->ev_fork, 0);
+    if (e == hipSuccess)
+        e = codes ? launch_qenc(x, t, H, w.xq, ctx->side) : launch_split_rows(x, t, H, w.xhi, w.xlo, w.xex, ctx->side);
+    return e == hipSuccess ? hipEventRecord(ctx->ev_x, ctx->side) : e;
+}
+hipError_t wait_x(moe_ctx *ctx, hipStream_t s) {
+    std::lock_guard<std::mutex> g(ctx->side_mu);
+    return hipStreamWaitEvent(s, ctx->ev_x, 0);
 }
 
 // The routed layer on workspace w (sized for at least t tokens of c.k
@@ -543,16 +558,18 @@ int forward_on(moe_layer *L, const CallState &c, Workspace &w, const float *x, i
                    : path == kStream ? stream_tile((double)t * k / L->E, L->mfma_bm != 160)
                    : path == kBatch  ? batch_tile_tokens(L->H, t, k, L->E)
                                      : 0;
-    int rc = route_and_dispatch(L, c, w, x, t, bm, path == kDecode, routes, hits, prev, stats, nullptr, s);
-    if (rc) return rc;
-
     const ExpertDev &e0 = L->experts_host[0];
     const ExpertDev *sh = L->has_shared ? &L->experts_host[L->E] : nullptr;
-    // The shared expert on the context's side stream, forked from s after
-    // the activations are encoded and joined back before the combine
-    // (few-tokens and MFMA paths).  Not while stages are being timed on s,
-    // nor for the no-allocation entry, nor while s is being captured into a
-    // graph (the capture then holds one stream's launches only).
+    // The shared expert on the context's side stream (few-tokens and MFMA
+    // paths): x is encoded there while s routes, the shared expert then runs
+    // there beside the routed experts, and it is joined back before the
+    // combine.  Measured on MI355X against forking after the routing:
+    // Qwen2-MoE T=32 0.197 -> 0.175 ms, T=512 0.424 -> 0.410, V2-Lite T=256
+    // 0.348 -> 0.330.  Layers without a shared expert keep x's encoding on
+    // s: the cross-stream wait costs more than the encoding (Mixtral T=32
+    // 0.262 -> 0.273 ms with it beside).  Not while stages are being timed
+    // on s, nor for the no-allocation entry, nor while s is being captured
+    // into a graph (the capture then holds one stream's launches only).
     bool side = sh && c.side && !c.profile && L->ctx->side && (path == kBatch || path == kMfma || path == kStream);
     if (side && s) {
         hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
@@ -564,6 +581,10 @@ int forward_on(moe_layer *L, const CallState &c, Workspace &w, const float *x, i
         }
     }
     hipError_t e = hipSuccess;
+    if (side && (e = encode_x_beside(L->ctx, s, path == kBatch, x, t, L->H, w)) != hipSuccess)
+        return hip_fail(e, "activation encoding (side stream)");
+    int rc = route_and_dispatch(L, c, w, x, t, bm, path == kDecode, routes, hits, prev, stats, nullptr, s);
+    if (rc) return rc;
     int ksplit = 1;
     if (path == kDecode) {
         DecodeArgs d{};
@@ -631,16 +652,20 @@ int forward_on(moe_layer *L, const CallState &c, Workspace &w, const float *x, i
         if ((size_t)b.ksplit * t * k > w.y_rows || (size_t)b.ksplit * t > w.ys_rows)
             return fail(MOE_EUNSUP, "few-tokens path: %d K parts do not fit the workspace", b.ksplit);
         ksplit = b.ksplit;
-        rc = stage(L, c.profile, 6, s, [&] {
-            e = launch_qenc(x, t, L->H, w.xq, s);
-            return e == hipSuccess ? MOE_OK : hip_fail(e, "activation encoding");
-        });
-        if (rc) return rc;
+        if (side) {
+            if ((e = wait_x(L->ctx, s)) != hipSuccess) return hip_fail(e, "activation encoding (wait)");
+        } else {
+            rc = stage(L, c.profile, 6, s, [&] {
+                e = launch_qenc(x, t, L->H, w.xq, s);
+                return e == hipSuccess ? MOE_OK : hip_fail(e, "activation encoding");
+            });
+            if (rc) return rc;
+        }
         if (side) {
             // The shared expert (its own buffers: hs, hsq, ys) beside the
-            // routed experts; the combine waits for both.
-            e = fork_side(L->ctx, s);
-            if (e == hipSuccess) e = launch_batch_up_shared(b, *sh, L->ctx->side);
+            // routed experts, after x's encoding on the side stream; the
+            // combine waits for both.
+            e = launch_batch_up_shared(b, *sh, L->ctx->side);
             if (e == hipSuccess) e = launch_qenc(w.hs, t, L->I_s, w.hsq, L->ctx->side);
             if (e == hipSuccess) e = launch_batch_down_shared(b, *sh, L->ctx->side);
             if (e != hipSuccess) return hip_fail(e, "shared expert (few-tokens kernels)");
@@ -704,16 +729,19 @@ int forward_on(moe_layer *L, const CallState &c, Workspace &w, const float *x, i
         while (m.ksplit > 1 && ((size_t)m.ksplit * t * k > w.y_rows || (size_t)m.ksplit * t > w.ys_rows))
             m.ksplit /= 2;
         ksplit = m.ksplit;
-        rc = stage(L, c.profile, 6, s, [&] {
-            e = launch_split_rows(x, t, L->H, w.xhi, w.xlo, w.xex, s);
-            return e == hipSuccess ? MOE_OK : hip_fail(e, "activation pieces");
-        });
-        if (rc) return rc;
         if (side) {
-            e = fork_side(L->ctx, s);
+            if ((e = wait_x(L->ctx, s)) != hipSuccess) return hip_fail(e, "activation pieces (wait)");
+        } else {
+            rc = stage(L, c.profile, 6, s, [&] {
+                e = launch_split_rows(x, t, L->H, w.xhi, w.xlo, w.xex, s);
+                return e == hipSuccess ? MOE_OK : hip_fail(e, "activation pieces");
+            });
+            if (rc) return rc;
+        }
+        if (side) {
+            // After x's pieces on the side stream.
             const int bs = sp ? stream_tile_exact(t, L->mfma_bm != 160) : bm;
-            if (e == hipSuccess)
-                e = sp ? launch_stream_single(true, m, bs, *sh, L->ctx->side) : launch_mfma_single(true, m, bm, *sh, L->ctx->side);
+            e = sp ? launch_stream_single(true, m, bs, *sh, L->ctx->side) : launch_mfma_single(true, m, bm, *sh, L->ctx->side);
             if (e == hipSuccess) e = launch_split_rows(w.hs, t, L->I_s, w.hshi, w.hslo, w.hsex, L->ctx->side);
             if (e == hipSuccess)
                 e = sp ? launch_stream_single(false, m, bs, *sh, L->ctx->side) : launch_mfma_single(false, m, bm, *sh, L->ctx->side);
@@ -868,7 +896,8 @@ int moe_ctx_create(int device, moe_ctx **out) {
         DeviceGuard g(device);
         if (hipStreamCreateWithFlags(&c->side, hipStreamNonBlocking) != hipSuccess ||
             hipEventCreateWithFlags(&c->ev_fork, hipEventDisableTiming) != hipSuccess ||
-            hipEventCreateWithFlags(&c->ev_join, hipEventDisableTiming) != hipSuccess) {
+            hipEventCreateWithFlags(&c->ev_join, hipEventDisableTiming) != hipSuccess ||
+            hipEventCreateWithFlags(&c->ev_x, hipEventDisableTiming) != hipSuccess) {
             (void)hipGetLastError();
             c->side = nullptr;  // everything on the caller's stream
         }
@@ -885,6 +914,7 @@ void moe_ctx_destroy(moe_ctx *ctx) {
         if (r.ptr) hipFree(r.ptr);
     if (ctx->ev_fork) hipEventDestroy(ctx->ev_fork);
     if (ctx->ev_join) hipEventDestroy(ctx->ev_join);
+    if (ctx->ev_x) hipEventDestroy(ctx->ev_x);
     if (ctx->side) hipStreamDestroy(ctx->side);
     delete ctx;
 }

@@ -172,7 +172,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 2))) voi
 // and never reach -0), so padding does not change a single bit.
 constexpr int kRT = 32;   // rows per tile
 constexpr int kKC = 64;   // K chunk
-template <int TPT>
+template <int TPT, bool VEC>
 __global__ __launch_bounds__(256) void router_tiled_kernel(const float *__restrict__ W, const float *__restrict__ x,
                                                            int T, int n_rows, int E, int H, float temp,
                                                            float *__restrict__ logits) {
@@ -195,17 +195,30 @@ __global__ __launch_bounds__(256) void router_tiled_kernel(const float *__restri
         for (int u = 0; u < TPT; u++) acc[i][u] = 0.0f;
     // Each thread moves 2 float4 of W (32 rows x 16 float4) and up to 2 of x
     // (kTTv tokens) per chunk, through two register buffers: the loads of
-    // chunk c + 2 are issued before chunk c's FMAs.
-    const bool vec = (H & 3) == 0;
+    // chunk c + 2 are issued before chunk c's FMAs.  VEC (H % 4 == 0): every
+    // thread issues the same loads in every chunk, from addresses clamped
+    // into the matrices, so that the compiler counts the loads in flight
+    // exactly (a load under a condition, or a select of its value, makes it
+    // wait for all of them, and a chunk then waited for the next chunk's
+    // loads: one chunk in flight instead of two).  Rows past the router's
+    // and tokens past T then hold copies of valid ones, which only feed
+    // their own chains, never stored; the values past kfull are zeroed
+    // where the last, partial chunk is stored to LDS.  Threads without a
+    // token row of their own load one of the tile's (lines another thread
+    // loads too), and the loads past the last chunk fill a buffer that is
+    // never read.  VEC needs H >= 16 (addresses clamped into the last full
+    // 16-value chunk).
     auto load_chunk = [&](int k0, float4(&pw)[2], float4(&px)[2]) {
 #pragma unroll
         for (int u = 0; u < 2; u++) {
             const int q = tid + 256 * u, rr = q >> 4, kk = (q & 15) * 4;
             const int gk = k0 + kk, gr = r0 + rr, gt = t0 + rr;
             float4 w4 = make_float4(0.f, 0.f, 0.f, 0.f), x4 = w4;
-            if (vec) {
-                if (gr < n_rows && gk < kfull) w4 = *reinterpret_cast<const float4 *>(W + (size_t)gr * H + gk);
-                if (rr < kTTv && gt < T && gk < kfull) x4 = *reinterpret_cast<const float4 *>(x + (size_t)gt * H + gk);
+            if constexpr (VEC) {
+                const int ck = min(gk, kfull - 4);
+                const int xt_row = min(t0 + min(rr, kTTv - 1), T - 1);
+                w4 = *reinterpret_cast<const float4 *>(W + (size_t)min(gr, n_rows - 1) * H + ck);
+                x4 = *reinterpret_cast<const float4 *>(x + (size_t)xt_row * H + ck);
             } else {
                 float *wp = &w4.x, *xp = &x4.x;
                 for (int e = 0; e < 4; e++) {
@@ -217,8 +230,9 @@ __global__ __launch_bounds__(256) void router_tiled_kernel(const float *__restri
         }
     };
     float4 pwa[2], pxa[2], pwb[2], pxb[2];
-    if (kfull > 0) load_chunk(0, pwa, pxa);
-    if (kKC < kfull) load_chunk(kKC, pwb, pxb);
+    const int nch = (kfull + kKC - 1) / kKC;  // chunks, the last possibly partial
+    if (VEC || nch > 0) load_chunk(0, pwa, pxa);
+    if (VEC || nch > 1) load_chunk(kKC, pwb, pxb);
     // Chunk k0 from register buffer (pw, px), which then takes chunk
     // k0 + 2 kKC.
     auto chunk = [&](int k0, float4(&pw)[2], float4(&px)[2]) {
@@ -227,6 +241,8 @@ __global__ __launch_bounds__(256) void router_tiled_kernel(const float *__restri
             const int q = tid + 256 * u, rr = q >> 4, kk = (q & 15) * 4;
             // Values kk..kk+3 are (s, j) = (kk / 16, kk % 16 + e).
             const int s0 = kk >> 4, j0 = kk & 15;
+            if (VEC && k0 + kKC > kfull && k0 + kk >= kfull)
+                pw[u] = px[u] = make_float4(0.f, 0.f, 0.f, 0.f);  // past the last full 16-value chunk
             float *wr = &wt[rr][0];
             wr[4 * (j0 + 0) + s0] = pw[u].x, wr[4 * (j0 + 1) + s0] = pw[u].y;
             wr[4 * (j0 + 2) + s0] = pw[u].z, wr[4 * (j0 + 3) + s0] = pw[u].w;
@@ -237,7 +253,7 @@ __global__ __launch_bounds__(256) void router_tiled_kernel(const float *__restri
             }
         }
         __syncthreads();
-        if (k0 + 2 * kKC < kfull) load_chunk(k0 + 2 * kKC, pw, px);
+        if (VEC || k0 + 2 * kKC < kfull) load_chunk(k0 + 2 * kKC, pw, px);
         static_assert(kKC == 64, "four 16-value steps per chunk");
         float4 wq[8], xq[TPT];
 #pragma unroll
@@ -258,10 +274,12 @@ __global__ __launch_bounds__(256) void router_tiled_kernel(const float *__restri
         }
         __syncthreads();
     };
-    for (int k0 = 0; k0 < kfull; k0 += 2 * kKC) {
-        chunk(k0, pwa, pxa);
-        if (k0 + kKC < kfull) chunk(k0 + kKC, pwb, pxb);
+    int c = 0;
+    for (; c + 2 <= nch; c += 2) {
+        chunk(c * kKC, pwa, pxa);
+        chunk((c + 1) * kKC, pwb, pxb);
     }
+    if (c < nch) chunk(c * kKC, pwa, pxa);
     const bool has8 = (H % 16) >= 8;
     const int tail = kfull + (has8 ? 8 : 0);
 #pragma unroll
@@ -1341,14 +1359,20 @@ hipError_t launch_router(const float *W, const float *x, int T, int n_rows, int 
         hipLaunchKernelGGL(router_lds_kernel, grid, dim3(256), lds, s, W, x, T, n_rows, E, H, RB, TB, temp, logits);
     } else {
         dim3 grid((n_rows + kRT - 1) / kRT, (T + 4 * tpt - 1) / (4 * tpt));
-        if (tpt == 8)
-            hipLaunchKernelGGL(router_tiled_kernel<8>, grid, dim3(256), 0, s, W, x, T, n_rows, E, H, temp, logits);
-        else if (tpt == 4)
-            hipLaunchKernelGGL(router_tiled_kernel<4>, grid, dim3(256), 0, s, W, x, T, n_rows, E, H, temp, logits);
-        else if (tpt == 2)
-            hipLaunchKernelGGL(router_tiled_kernel<2>, grid, dim3(256), 0, s, W, x, T, n_rows, E, H, temp, logits);
-        else
-            hipLaunchKernelGGL(router_tiled_kernel<1>, grid, dim3(256), 0, s, W, x, T, n_rows, E, H, temp, logits);
+        if ((H & 3) != 0 || H < 16) {
+            // Rows of a length that is not a multiple of 4, or shorter than
+            // 16: scalar loads.
+            dim3 g1((n_rows + kRT - 1) / kRT, (T + 3) / 4);
+            hipLaunchKernelGGL((router_tiled_kernel<1, false>), g1, dim3(256), 0, s, W, x, T, n_rows, E, H, temp, logits);
+        } else if (tpt == 8) {
+            hipLaunchKernelGGL((router_tiled_kernel<8, true>), grid, dim3(256), 0, s, W, x, T, n_rows, E, H, temp, logits);
+        } else if (tpt == 4) {
+            hipLaunchKernelGGL((router_tiled_kernel<4, true>), grid, dim3(256), 0, s, W, x, T, n_rows, E, H, temp, logits);
+        } else if (tpt == 2) {
+            hipLaunchKernelGGL((router_tiled_kernel<2, true>), grid, dim3(256), 0, s, W, x, T, n_rows, E, H, temp, logits);
+        } else {
+            hipLaunchKernelGGL((router_tiled_kernel<1, true>), grid, dim3(256), 0, s, W, x, T, n_rows, E, H, temp, logits);
+        }
     }
     return hipGetLastError();
 }

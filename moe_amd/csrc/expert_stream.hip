@@ -966,251 +966,13 @@ __global__ __launch_bounds__(512, 1) __attribute__((amdgpu_waves_per_eu(2, 2))) 
         run(std::false_type{}, std::integral_constant<int, 16>{});
 }
 
-// ---- tiled copies, tiles of 2 to 5 subtiles ------------------------------------
-// The same waves as tiled_kernel (one 32-row region each, its weights from
-// the tiled copy straight into a register ring), over every 32-token subtile
-// of the tile, so each weight value is loaded and decoded once for up to
-// 160 tokens.  The activations, S times more per step, reach LDS by DMA
-// (global_load_lds, as in the ring kernels) in a ring of D + 2 one-step
-// stages, D steps ahead, one DMA after each subtile's MFMAs, one barrier per
-// step.  The compiler sees the
-// weight loads but not the DMAs, so its waits for a weight step count too
-// few loads and wait for more than they need: the register ring is deep
-// enough (P) that those waits still leave D steps of weights in flight,
-// and the waits for the DMAs (explicit) leave the last D steps' loads in
-// flight.  Per step and subtile: block 0's four MFMAs into the subtile's
-// sum, its fmas, then block 1's into the same sum.
-template <int DT>
-constexpr int wmt_nw() {  // weight load instructions per row step (tiled_load)
-    return DT == MOE_DT_Q8_0 ? 3 : 2;
-}
-template <int S>
-constexpr int wmt_delay() {  // steps the activation DMAs run ahead
-    return S >= 5 ? 1 : 2;
-}
-template <int DT, int S>
-constexpr int wmt_ring() {  // weight ring: the compiler's waits keep D steps in flight
-    constexpr int nw = wmt_nw<DT>(), d = wmt_delay<S>();
-    return (d * (nw + S) + nw - 1) / nw + 1;
-}
-template <int S>
-constexpr int wmt_lds() {
-    return (wmt_delay<S>() + 2) * 2 * S * 4096 + 3 * 32 * S * 4;
-}
-
-template <int DT, bool UP, int S>
-__global__ __launch_bounds__(512, 1) __attribute__((amdgpu_waves_per_eu(2, 2))) void wmt_kernel(MfmaArgs a, int mode,
-                                                                                                  int gx, int ksplit) {
-    using TL = Tiled<DT>;
-    using TS = TiledStep<DT>;
-    constexpr int ND = TL::nd;
-    constexpr int BM = 32 * S;
-    constexpr int D = wmt_delay<S>();
-    constexpr int NSA = D + 2;        // activation stages
-    constexpr int AS = S * 4096;      // one piece of one stage: 32 S rows of 64 f16
-    constexpr int RS = 2 * AS;        // stage bytes
-    constexpr int NW = wmt_nw<DT>();
-    constexpr int P = wmt_ring<DT, S>();
-    extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
-    int *src_row = reinterpret_cast<int *>(smem + NSA * RS);
-    int *dst_row = src_row + BM;
-    int *ex_row = dst_row + BM;
-
-    TileInfo ti;
-    if (!tile_of<BM, 32>(a, mode, gx, ti)) return;
-    const ExpertDev &ex = a.experts[ti.g];
-    const MatDev &W0 = UP ? ex.m[0] : ex.m[2];
-    const MatDev &W1 = UP ? ex.m[1] : ex.m[2];
-    const int n0 = ti.ntile * (UP ? SW / 2 : SW);
-    if (n0 >= W0.rows) return;
-    const int kspan = W0.cols / ksplit;
-    const int kbeg = ti.ksplit * kspan;
-    const int nsteps = kspan / SK;
-    const int tid = threadIdx.x, lane = tid & 63;
-    const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int sd = wv & 3, j = wv >> 2;
-    const int l32 = lane & 31, hf = lane >> 5;
-    const int Icol = ti.shared ? a.I_s : a.I;
-    const int valid = min(BM, ti.n - ti.m0);
-    const int mt = (valid + 31) / 32;
-
-    const uint16_t *ahi = UP ? a.xhi : (ti.shared ? a.hshi : a.hhi);
-    const uint16_t *alo = UP ? a.xlo : (ti.shared ? a.hslo : a.hlo);
-    const int32_t *aex = UP ? a.xex : (ti.shared ? a.hsex : a.hex);
-    if (tid < BM) {
-        int s = -1, d = -1, e = 0;
-        if (tid < valid) {
-            d = ti.row0 + ti.m0 + tid;
-            s = UP ? (ti.shared ? ti.m0 + tid : a.perm_tok[d]) : d;
-            e = aex[s];
-        }
-        src_row[tid] = s;
-        dst_row[tid] = d;
-        ex_row[tid] = e;
-    }
-    __syncthreads();
-
-    const MatDev &Wd = (UP && j == 1) ? W1 : W0;
-    const int row0 = UP ? n0 + 32 * sd : n0 + 64 * sd + 32 * j;
-    const size_t region = row0 < Wd.rows ? (size_t)(row0 / 32) : 0;
-    const uint8_t *wp = Wd.tiled + (region * (size_t)(Wd.cols / SK) + (size_t)(kbeg / SK)) * TS::step_bytes +
-                        (size_t)l32 * TL::rb;
-    const uint32_t arow_bytes = (uint32_t)(UP ? a.H : Icol) * 2;
-    const uint32_t lds0 = lds_addr(smem);
-    const lds_p sm = (lds_p)smem;
-
-    auto run = [&](auto mt_c) {
-        constexpr int MT = decltype(mt_c)::value;
-        // Activation DMA u of this wave: instruction q = wv + 8 u of the
-        // step's 8 MT (piece q / (4 MT), 8-row group q % (4 MT)).
-        uint32_t aoffg[MT], adst[MT];
-        const uint16_t *asrc[MT];
-#pragma unroll
-        for (int u = 0; u < MT; u++) {
-            const int qd = wv + 8 * u, p = qd / (4 * MT), i = qd % (4 * MT);
-            const int r = 8 * i + (lane >> 3);
-            const int sr = src_row[r < valid ? r : 0];
-            aoffg[u] = (uint32_t)sr * arow_bytes + (uint32_t)kbeg * 2u + (uint32_t)(((lane & 7) ^ ((r >> 1) & 7)) << 4);
-            adst[u] = (uint32_t)p * AS + (uint32_t)i * 1024u;
-            asrc[u] = p == 0 ? ahi : alo;
-        }
-        auto dma_one = [&](int u, int step) {
-            const int sc = step < nsteps ? step : nsteps - 1;
-            const uint32_t sb = lds0 + (uint32_t)(step % NSA) * RS;
-            dma16(reinterpret_cast<const uint8_t *>(asrc[u]) + (size_t)sc * (SK * 2), aoffg[u], sb + adst[u]);
-        };
-        auto dma_act = [&](int step) {
-#pragma unroll
-            for (int u = 0; u < MT; u++) dma_one(u, step);
-        };
-        uint32_t aoff[2][2];
-#pragma unroll
-        for (int kb = 0; kb < 2; kb++)
-#pragma unroll
-            for (int m = 0; m < 2; m++)
-                aoff[kb][m] = (uint32_t)l32 * 128u + ((uint32_t)((4 * kb + 2 * m + hf) ^ ((l32 >> 1) & 7)) << 4);
-
-        floatx16 acc[MT];
-#pragma unroll
-        for (int t = 0; t < MT; t++) acc[t] = floatx16{};
-        uint32_t raw[P][ND];
-        // Prologue: the activations of steps 0 .. D, then the weights of
-        // steps 0 .. P - 1; step 0's activations in LDS before the loop.
-        for (int q = 0; q <= D; q++) dma_act(q);
-#pragma unroll
-        for (int i = 0; i < P; i++) tiled_load<DT>(wp + (size_t)(i < nsteps ? i : nsteps - 1) * TS::step_bytes, hf, raw[i]);
-        wait_vm_barrier<MT * D + NW * P>();
-
-        auto step = [&](auto i_c, int s) {
-            constexpr int i = decltype(i_c)::value;
-            half8 B[2][2];
-            float dsc[2];
-            tiled_decode<DT, 0>(raw[i], hf, B[0], dsc[0]);
-            tiled_decode<DT, 1>(raw[i], hf, B[1], dsc[1]);
-            asm volatile("" : "+v"(dsc[0]), "+v"(dsc[1]), "+v"(B[0][0]), "+v"(B[0][1]), "+v"(B[1][0]), "+v"(B[1][1]));
-            tiled_load<DT>(wp + (size_t)(s + P < nsteps ? s + P : nsteps - 1) * TS::step_bytes, hf, raw[i]);
-            const lds_p st = sm + (s % NSA) * RS;
-#pragma unroll
-            for (int t = 0; t < MT; t++) {
-                floatx16 ps;
-#pragma unroll
-                for (int kb = 0; kb < 2; kb++) {
-#pragma unroll
-                    for (int m = 0; m < 2; m++) {
-#pragma unroll
-                        for (int p = 0; p < 2; p++) {
-                            const half8 A = lds_h8(st + p * AS + t * 4096 + aoff[kb][m]);
-                            ps = __builtin_amdgcn_mfma_f32_32x32x16_f16(A, B[kb][m], (m | p) ? ps : floatx16{}, 0, 0, 0);
-                        }
-                    }
-#pragma unroll
-                    for (int v = 0; v < 16; v++) acc[t][v] = fmaf(dsc[kb], ps[v], acc[t][v]);
-                }
-                // Step s + D + 1's activation DMA u = t, between the
-                // subtiles' MFMAs: issued together they stall the wave.
-                __builtin_amdgcn_sched_barrier(0);
-                dma_one(t, s + D + 1);
-                __builtin_amdgcn_sched_barrier(0);
-            }
-            // Step s + 1's activations (DMAs issued D iterations ago) are in,
-            // every wave is done with stage s.
-            wait_vm_barrier<(NW + MT) * D>();
-            __builtin_amdgcn_sched_barrier(0);
-        };
-        int s0 = 0;
-        for (; s0 + P <= nsteps; s0 += P) static_for<0, P>([&](auto i_c) { step(i_c, s0 + decltype(i_c)::value); });
-        static_for<0, P>([&](auto i_c) {
-            if (s0 + decltype(i_c)::value < nsteps) step(i_c, s0 + decltype(i_c)::value);
-        });
-        wait_vm<0>();
-        __syncthreads();
-
-        // ---- epilogue.  Lane holds C[32 t + 8 (v / 4) + 4 hf + v % 4][row
-        // l32 of its region], scaled by 2^ex_row.
-        if (UP) {
-            float *xb = reinterpret_cast<float *>(smem) + sd * (MT * 1024);
-            if (j == 1) {
-#pragma unroll
-                for (int t = 0; t < MT; t++)
-#pragma unroll
-                    for (int v = 0; v < 16; v++) xb[(t * 16 + v) * 64 + lane] = acc[t][v];
-            }
-            __syncthreads();
-            if (j == 0) {
-                float *hout = ti.shared ? a.hs : a.h;
-                const int col = n0 + 32 * sd + l32;
-                if (col < W0.rows) {
-#pragma unroll
-                    for (int t = 0; t < MT; t++)
-#pragma unroll
-                        for (int v = 0; v < 16; v++) {
-                            const int row = 32 * t + 8 * (v / 4) + 4 * hf + (v % 4);
-                            const int d = dst_row[row];
-                            if (d < 0) continue;
-                            const int e = ex_row[row];
-                            const float g = ldexpf(acc[t][v], -e), u = ldexpf(xb[(t * 16 + v) * 64 + lane], -e);
-                            hout[(size_t)d * Icol + col] = g * __builtin_amdgcn_rcpf(1.0f + __expf(-g)) * u;
-                        }
-                }
-            }
-        } else {
-            float *yout = ti.shared ? a.ys + ti.ksplit * a.yspart : a.y + ti.ksplit * a.ypart;
-            const int col = n0 + 64 * sd + 32 * j + l32;
-            if (col < W0.rows) {
-#pragma unroll
-                for (int t = 0; t < MT; t++)
-#pragma unroll
-                    for (int v = 0; v < 16; v++) {
-                        const int row = 32 * t + 8 * (v / 4) + 4 * hf + (v % 4);
-                        const int d = dst_row[row];
-                        if (d >= 0) yout[(size_t)d * a.H + col] = ldexpf(acc[t][v], -ex_row[row]);
-                    }
-            }
-        }
-    };
-    switch (mt) {
-    case 1: run(std::integral_constant<int, 1>{}); break;
-    case 2: if constexpr (S >= 2) run(std::integral_constant<int, 2>{}); break;
-    case 3: if constexpr (S >= 3) run(std::integral_constant<int, 3>{}); break;
-    case 4: if constexpr (S >= 4) run(std::integral_constant<int, 4>{}); break;
-    default: if constexpr (S >= 5) run(std::integral_constant<int, 5>{}); break;
-    }
-}
-
 template <int DT, bool UP, int S>
 hipError_t launch_s(dim3 grid, const MfmaArgs &a, int mode, int ksplit, bool tiled, hipStream_t s) {
+    // One-subtile tiles stream the tiled copies; wider tiles read the
+    // row-major matrices, which every layer keeps.
     if constexpr (S == 1) {
         if (tiled) {
             hipLaunchKernelGGL((tiled_kernel<DT, UP>), grid, dim3(512), 0, s, a, mode, (int)grid.x, ksplit);
-            return hipGetLastError();
-        }
-    } else {
-        if (tiled) {
-            constexpr int lds = wmt_lds<S>();
-            static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void *>(&wmt_kernel<DT, UP, S>),
-                                                               hipFuncAttributeMaxDynamicSharedMemorySize, lds);
-            if (attr != hipSuccess) return attr;
-            hipLaunchKernelGGL((wmt_kernel<DT, UP, S>), grid, dim3(512), lds, s, a, mode, (int)grid.x, ksplit);
             return hipGetLastError();
         }
     }

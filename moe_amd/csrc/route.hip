@@ -114,8 +114,11 @@ __device__ inline void stage2_to_lds(const float *__restrict__ a, float *__restr
 __host__ __device__ inline int router_lds_stride(int H) { return (H % 64 == 0) ? H + 16 : H; }
 
 // Latency-bound router: a block stages RB router rows and TB token rows in
-// LDS (the whole of H), then thread (pair, j) runs lane j of dot_avx2 for one
-// (row, token) pair — one chain per thread, read eight steps at a time.
+// LDS (the whole of H), then thread (g, j) runs lane j of dot_avx2 for the
+// (row, token) pairs g, g + 16, ..., PPT of them (RB TB <= 16 PPT), their
+// chains interleaved and read eight steps at a time.  Each chain keeps its
+// order, so PPT changes no bit; it puts more pairs on each staged row.
+template <int PPT>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 2))) void router_lds_kernel(const float *__restrict__ W, const float *__restrict__ x,
                                                          int T, int n_rows, int E, int H, int RB, int TB, float temp,
                                                          float *__restrict__ logits) {
@@ -135,33 +138,51 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 2))) voi
         for (int r = 0; r < nt; r++) stage_to_lds(x + (size_t)(t0 + r) * H, xl + (size_t)r * LS, H);
     }
     __syncthreads();
-    const int tid = threadIdx.x, j = tid & 15, p = tid >> 4;
-    if (p >= nr * nt) return;  // whole 16-lane groups leave together
-    const int rl = p / nt, tl = p % nt;
-    const float *a = wl + (size_t)rl * LS;
-    const float *b = xl + (size_t)tl * LS;
+    const int tid = threadIdx.x, j = tid & 15, g = tid >> 4;
+    const int np = nr * nt;
+    if (g >= np) return;  // whole 16-lane groups leave together
+    // Pairs past np repeat the group's first pair (never stored).
+    const float *a[PPT], *b[PPT];
+#pragma unroll
+    for (int q = 0; q < PPT; q++) {
+        const int p = g + 16 * q < np ? g + 16 * q : g;
+        a[q] = wl + (size_t)(p / nt) * LS;
+        b[q] = xl + (size_t)(p % nt) * LS;
+    }
     const int n16 = H / 16;
     const bool has8 = (H % 16) >= 8;
-    float acc = 0.0f;
+    float acc[PPT];
+#pragma unroll
+    for (int q = 0; q < PPT; q++) acc[q] = 0.0f;
     int c = 0;
     for (; c + 8 <= n16; c += 8) {
-        float av[8], bv[8];
+        float av[PPT][8], bv[PPT][8];
 #pragma unroll
-        for (int u = 0; u < 8; u++) {
-            av[u] = a[16 * (c + u) + j];
-            bv[u] = b[16 * (c + u) + j];
-        }
+        for (int q = 0; q < PPT; q++)
 #pragma unroll
-        for (int u = 0; u < 8; u++) acc = fmaf(av[u], bv[u], acc);
+            for (int u = 0; u < 8; u++) {
+                av[q][u] = a[q][16 * (c + u) + j];
+                bv[q][u] = b[q][16 * (c + u) + j];
+            }
+#pragma unroll
+        for (int u = 0; u < 8; u++)
+#pragma unroll
+            for (int q = 0; q < PPT; q++) acc[q] = fmaf(av[q][u], bv[q][u], acc[q]);
     }
-    for (; c < n16; c++) acc = fmaf(a[16 * c + j], b[16 * c + j], acc);
-    if (has8 && j < 8) acc = fmaf(a[16 * n16 + j], b[16 * n16 + j], acc);
-    float v = reduce16_avx2(acc);
-    if (j == 0) {
-        v = dot_tail(v, a, b, 16 * n16 + (has8 ? 8 : 0), H);
-        const int r = r0 + rl;
-        if (temp > 0.0f && r < E) v = v / temp;
-        logits[(size_t)(t0 + tl) * n_rows + r] = v;
+    for (; c < n16; c++)
+#pragma unroll
+        for (int q = 0; q < PPT; q++) acc[q] = fmaf(a[q][16 * c + j], b[q][16 * c + j], acc[q]);
+#pragma unroll
+    for (int q = 0; q < PPT; q++) {
+        if (has8 && j < 8) acc[q] = fmaf(a[q][16 * n16 + j], b[q][16 * n16 + j], acc[q]);
+        float v = reduce16_avx2(acc[q]);
+        const int p = g + 16 * q;
+        if (j == 0 && p < np) {
+            v = dot_tail(v, a[q], b[q], 16 * n16 + (has8 ? 8 : 0), H);
+            const int r = r0 + p / nt;
+            if (temp > 0.0f && r < E) v = v / temp;
+            logits[(size_t)(t0 + p % nt) * n_rows + r] = v;
+        }
     }
 }
 
@@ -1325,20 +1346,25 @@ hipError_t launch_router(const float *W, const float *x, int T, int n_rows, int 
     // tile: per round of resident blocks, one memory round trip (~1 us) per
     // 16 float4 per thread, the staged bytes through each CU at ~64 B per
     // cycle, and the H/16-step chain at ~10 cycles per step.
-    int best_rb = 0, best_tb = 0;
+    // PPT pairs per thread (RB TB <= 16 PPT): interleaved chains, assumed
+    // to cost (1 + (PPT - 1) / 2) times one chain.
+    int best_rb = 0, best_tb = 0, best_ppt = 1;
     double best = 1e30;
-    for (int RB = 1; RB <= 16 && RB < 2 * n_rows; RB *= 2)
-        for (int TB = 1; RB * TB <= 16 && TB < 2 * T; TB *= 2) {
-            const double lds = (RB + TB) * (double)router_lds_stride(H) * 4;
-            if (lds > budget) continue;
-            const long long blocks = (long long)((n_rows + RB - 1) / RB) * ((T + TB - 1) / TB);
-            int per_cu = (int)(budget / lds);
-            if (per_cu > 8) per_cu = 8;
-            const double rounds = std::ceil((double)blocks / (256.0 * per_cu));
-            const double trips = std::ceil((double)std::max(RB, TB) * H / 4 / (16 * 256));
-            const double t = rounds * (trips + per_cu * lds / 64.0 / clk_us + (H / 16) * 10.0 / clk_us);
-            if (t < best) best = t, best_rb = RB, best_tb = TB;
-        }
+    for (int ppt = 1; ppt <= 4; ppt *= 2)
+        for (int RB = 1; RB <= 16 * ppt && RB < 2 * n_rows; RB *= 2)
+            for (int TB = 1; RB * TB <= 16 * ppt && TB < 2 * T; TB *= 2) {
+                if (ppt > 1 && RB * TB <= 8 * ppt) continue;  // fits fewer pairs per thread
+                const double lds = (RB + TB) * (double)router_lds_stride(H) * 4;
+                if (lds > budget) continue;
+                const long long blocks = (long long)((n_rows + RB - 1) / RB) * ((T + TB - 1) / TB);
+                int per_cu = (int)(budget / lds);
+                if (per_cu > 8) per_cu = 8;
+                const double rounds = std::ceil((double)blocks / (256.0 * per_cu));
+                const double trips = std::ceil((double)std::max(RB, TB) * H / 4 / (16 * 256));
+                const double chain = (H / 16) * 10.0 / clk_us * (1.0 + 0.5 * (ppt - 1));
+                const double t = rounds * (trips + per_cu * lds / 64.0 / clk_us + chain);
+                if (t < best) best = t, best_rb = RB, best_tb = TB, best_ppt = ppt;
+            }
     // The tiled kernel: 32 rows x 4 TPT tokens, TPT = 8 unless that leaves
     // fewer than three blocks per CU (latency then shows: 32 x 32 tiles at
     // one block per CU ran 4.5x slower than their FMA count); ~1150 cycles
@@ -1352,11 +1378,20 @@ hipError_t launch_router(const float *W, const float *x, int T, int n_rows, int 
         const size_t lds = (size_t)(RB + TB) * router_lds_stride(H) * 4;
         static bool raised = false;
         if (!raised) {
-            (void)hipFuncSetAttribute((const void *)router_lds_kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
+            (void)hipFuncSetAttribute((const void *)router_lds_kernel<1>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                      160 * 1024);
+            (void)hipFuncSetAttribute((const void *)router_lds_kernel<2>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                      160 * 1024);
+            (void)hipFuncSetAttribute((const void *)router_lds_kernel<4>, hipFuncAttributeMaxDynamicSharedMemorySize,
                                       160 * 1024);
             raised = true;
         }
-        hipLaunchKernelGGL(router_lds_kernel, grid, dim3(256), lds, s, W, x, T, n_rows, E, H, RB, TB, temp, logits);
+        if (best_ppt == 4)
+            hipLaunchKernelGGL(router_lds_kernel<4>, grid, dim3(256), lds, s, W, x, T, n_rows, E, H, RB, TB, temp, logits);
+        else if (best_ppt == 2)
+            hipLaunchKernelGGL(router_lds_kernel<2>, grid, dim3(256), lds, s, W, x, T, n_rows, E, H, RB, TB, temp, logits);
+        else
+            hipLaunchKernelGGL(router_lds_kernel<1>, grid, dim3(256), lds, s, W, x, T, n_rows, E, H, RB, TB, temp, logits);
     } else {
         dim3 grid((n_rows + kRT - 1) / kRT, (T + 4 * tpt - 1) / (4 * tpt));
         if ((H & 3) != 0 || H < 16) {

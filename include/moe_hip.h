@@ -24,10 +24,12 @@
  *     owns, so calls on different streams (or workspaces) share no scratch.
  *     Host threads may call concurrently; moe_layer_set_routing and
  *     moe_layer_set_mode apply to calls made after they return.
- *   - Inside a forward call on the few-tokens or MFMA path, a layer's shared
- *     expert runs on a stream the context owns, which waits for `stream`
- *     (an event) before it starts, and `stream` waits for it before the
- *     combine: the call stays ordered on `stream` as a whole.  Calls on a
+ *   - Inside a forward call on the few-tokens or MFMA path, a layer with a
+ *     shared expert encodes x and runs the shared expert on a stream the
+ *     context owns, which waits for `stream` (an event) before it starts;
+ *     `stream` waits for x's encoding before its first expert kernel and
+ *     for the shared expert before the combine: the call stays ordered on
+ *     `stream` as a whole.  Calls on a
  *     stream that is being captured into a graph, and
  *     moe_layer_forward_noalloc, keep every launch on `stream`.
  */

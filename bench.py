@@ -361,14 +361,21 @@ COUNTER_PASSES = [
     "SQ_ACTIVE_INST_VALU SQ_ACTIVE_INST_LDS SQ_ACTIVE_INST_ANY SQ_WAIT_ANY SQ_INST_CYCLES_SALU SQ_INSTS_SALU "
     "SQ_WAVES SQ_LDS_BANK_CONFLICT",
 ]
-COUNTER_BENCH = "bench.py --no-cpu --steps 3 --warmup 1 --tokens 512 --batch-tokens 0 --copies 2"
+COUNTER_BENCHES = {
+    "mixtral": ("Mixtral shape, Q4_0, T=512",
+                "bench.py --no-cpu --steps 3 --warmup 1 --tokens 512 --batch-tokens 0 --copies 2"),
+    "qwen3": ("Qwen3-30B-A3B shape, Q8_0, T=2048",
+              "bench.py --no-cpu --steps 3 --warmup 1 --shape qwen3 --tokens 2048 --batch-tokens 0 --copies 2"),
+}
+COUNTER_BENCH = COUNTER_BENCHES["mixtral"][1]
 
 
-def summarize_counters(dirs: list, out_md: str) -> int:
-    """The MFMA kernels' counters at T=512 from rocprofv3 --pmc passes (one
-    directory per COUNTER_PASSES entry, each holding bench_counter_collection.csv
-    and bench_kernel_trace.csv): clock, MFMA-busy share and instruction mix
-    per launch of the gate/up and down kernels of the largest grid."""
+def summarize_counters(dirs: list, out_md: str, shape: str = "mixtral") -> int:
+    """The MFMA kernels' counters from rocprofv3 --pmc passes over
+    COUNTER_BENCHES[shape] (one directory per COUNTER_PASSES entry, each
+    holding bench_counter_collection.csv and bench_kernel_trace.csv): clock,
+    MFMA-busy share and instruction mix per launch of the gate/up and down
+    kernels of the largest grid."""
     import csv
     import re
 
@@ -393,12 +400,15 @@ def summarize_counters(dirs: list, out_md: str) -> int:
         ds = dur.get(key) or [float("nan")]
         rows.append((key, c, sum(ds) / len(ds)))
     simds = 1024
-    lines = [f"# MFMA expert kernels (Mixtral shape, Q4_0, T=512): clock, MFMA busy, instruction mix", "",
+    title, cmd = COUNTER_BENCHES[shape]
+    tag = "mfma_pmc" if shape == "mixtral" else f"{shape}_pmc"
+    lines = [f"# MFMA expert kernels ({title}): clock, MFMA busy, instruction mix", "",
              "Counter passes (from the repo root on the GPU box; at most 8 SQ counters per pass):", ""]
     for i, p in enumerate(COUNTER_PASSES):
         lines.append(f"    cd /tmp && export TMPDIR=/tmp && rocprofv3 --kernel-trace --pmc {p} --output-format csv "
-                     f"-d $REPO/gpurun_out/mfma_pmc{i + 1} -o bench -- python3 $REPO/{COUNTER_BENCH}")
-    lines += ["", "then `python bench.py --summarize-counters gpurun_out/mfma_pmc1 gpurun_out/mfma_pmc2 OUT`.",
+                     f"-d $REPO/gpurun_out/{tag}{i + 1} -o bench -- python3 $REPO/{cmd}")
+    opt = "" if shape == "mixtral" else f" --counter-shape {shape}"
+    lines += ["", f"then `python bench.py --summarize-counters gpurun_out/{tag}1 gpurun_out/{tag}2 OUT{opt}`.",
               "Counters are summed over the device per dispatch and averaged over dispatches; GRBM_GUI_ACTIVE "
               "sums the 8 XCDs, SQ_VALU_MFMA_BUSY_CYCLES the 1024 SIMDs.  Launches under counter collection are "
               "serialised, so durations run a little long; the ratios are what the text uses.", "",
@@ -505,6 +515,8 @@ def main() -> int:
     ap.add_argument("--summarize-counters", nargs="+", metavar="DIR",
                     help="write the MFMA kernels' counter summary from the rocprofv3 passes of COUNTER_PASSES "
                          "(directories, then the output markdown path) and exit")
+    ap.add_argument("--counter-shape", choices=sorted(COUNTER_BENCHES), default="mixtral",
+                    help="workload whose counter passes --summarize-counters reads")
     ap.add_argument("--grid-barrier", action="store_true",
                     help="time grid-wide barriers in cooperative launches and exit")
     ap.add_argument("--mfma-valu", action="store_true",
@@ -534,7 +546,7 @@ def main() -> int:
     if args.summarize_pmc:
         return summarize_pmc(args.summarize_pmc[0], args.summarize_pmc[1], TRAFFIC_FILE)
     if args.summarize_counters:
-        return summarize_counters(args.summarize_counters[:-1], args.summarize_counters[-1])
+        return summarize_counters(args.summarize_counters[:-1], args.summarize_counters[-1], args.counter_shape)
     if args.summarize_trace:
         return summarize_trace(args.summarize_trace[0], args.summarize_trace[1],
                                "Mixtral-8x7B-shape routed layer (Q4_0, top-2), T=1, T=32 and T=512: kernel durations",
